@@ -1,0 +1,96 @@
+"""Build the gfx950 kernel library in-tree.
+
+    python colabfold-legacy-kernels_amd/build.py [--jobs N] [--asm]
+
+Compiles every ``csrc/*.hip`` and ``csrc/*.cpp`` with hipcc for gfx950 into ``_build/`` and
+links them into ``colabfold_legacy_kernels/kernels/gfx950/libclk_gfx950.so``, the file the
+locator's ``library_path`` names. This is the counterpart of the reference's per-arch build
+(scripts/build_kernels.sh:86-116): one target architecture, no CUTLASS, no XLA headers needed.
+
+``--asm`` also writes the gfx950 assembly of each kernel source to ``_build/<name>.s`` (device
+code only), which ``tests/test_build.py`` scans for ``v_mfma`` instructions -- the analogue of
+the reference's tensor-core SASS check (scripts/build_kernels.sh:120-150), applied to the AMD
+assembly of code built here.
+"""
+
+import argparse
+import concurrent.futures as cf
+import os
+import subprocess
+import sys
+from pathlib import Path
+
+HERE = Path(__file__).resolve().parent
+REPO = HERE.parent
+CSRC = HERE / "csrc"
+BUILD = HERE / "_build"
+OUT_DIR = HERE / "colabfold_legacy_kernels" / "kernels" / "gfx950"
+LIB = OUT_DIR / "libclk_gfx950.so"
+ARCH = "gfx950"
+
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+# Packed-FP32 VALU forms are disabled for all device code: hipcc -O3 would otherwise form
+# v_pk_{add,mul,fma}_f32 from scalar float code.
+COMMON = [
+    "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
+    "--offload-arch=" + ARCH,
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-I" + str(REPO / "include"), "-I" + str(CSRC),
+]
+
+
+def sources():
+    return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
+
+
+def _run(cmd):
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("command failed: %s\n%s%s" % (" ".join(cmd), res.stdout, res.stderr))
+    return res
+
+
+def _compile(src):
+    obj = BUILD / (src.stem + ".o")
+    lang = ["-x", "hip"] if src.suffix == ".hip" else []
+    _run([HIPCC] + COMMON + lang + ["-c", str(src), "-o", str(obj)])
+    return obj
+
+
+def _asm(src):
+    out = BUILD / (src.stem + ".s")
+    _run([HIPCC] + COMMON + ["-x", "hip", "--cuda-device-only", "-S", str(src), "-o", str(out)])
+    return out
+
+
+def build(jobs=None, asm=False, verbose=True):
+    """Compile and link; returns the library path."""
+    BUILD.mkdir(exist_ok=True)
+    OUT_DIR.mkdir(parents=True, exist_ok=True)
+    srcs = sources()
+    jobs = jobs or min(8, os.cpu_count() or 1)
+    with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
+        objs = list(pool.map(_compile, srcs))
+        if asm:
+            list(pool.map(_asm, [s for s in srcs if s.suffix == ".hip"]))
+    tmp = LIB.with_name(LIB.name + ".tmp")
+    _run([HIPCC, "-shared", "-fPIC", "--offload-arch=" + ARCH, "-o", str(tmp)]
+         + [str(o) for o in objs])
+    os.replace(tmp, LIB)
+    if verbose:
+        print("built %s (%d units)" % (LIB, len(objs)))
+    return LIB
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--jobs", type=int, default=None)
+    ap.add_argument("--asm", action="store_true")
+    args = ap.parse_args(argv)
+    build(args.jobs, args.asm)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,73 @@
+"""ctypes binding of the C ABI declared in include/clk.h.
+
+Loads the gfx950 library that ``library_path`` names and declares every entry point's argument
+and return types. There is no fallback: if the library is missing, ``lib()`` raises
+FileNotFoundError, and every op in ``colabfold_legacy_kernels.ops`` fails with it.
+"""
+
+import ctypes
+import threading
+
+from . import library_path
+
+_lock = threading.Lock()
+_lib = None
+
+c_void_p = ctypes.c_void_p
+c_i64 = ctypes.c_int64
+c_f32 = ctypes.c_float
+c_int = ctypes.c_int
+c_size = ctypes.c_size_t
+
+# name -> (restype, argtypes); the same order as the prototypes in include/clk.h.
+PROTOTYPES = {
+    "clk_last_error": (ctypes.c_char_p, []),
+    "clk_version": (ctypes.c_char_p, []),
+    "clk_attention_fwd": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                                  c_void_p, c_void_p, c_void_p, c_i64, c_i64, c_i64, c_i64,
+                                  c_i64, c_f32, c_i64, c_i64]),
+    "clk_attention_bwd_workspace_size": (c_size, [c_i64, c_i64, c_i64, c_i64, c_i64]),
+    "clk_attention_bwd": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                                  c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                  c_void_p, c_void_p, c_void_p, c_size, c_i64, c_i64, c_i64,
+                                  c_i64, c_i64, c_f32]),
+    "clk_layer_norm_fwd": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                                   c_i64, c_i64, c_f32]),
+    "clk_layer_norm_bwd_workspace_size": (c_size, [c_i64, c_i64]),
+    "clk_layer_norm_bwd": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                                   c_void_p, c_void_p, c_void_p, c_size, c_i64, c_i64, c_f32]),
+    "clk_gated_dual_proj": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                                    c_void_p, c_void_p, c_void_p, c_i64, c_i64, c_i64]),
+    "clk_ln_gated_dual_proj": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                                       c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                       c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_i64,
+                                       c_i64, c_i64, c_f32]),
+}
+
+# Status codes (clk_status) and dtype codes (clk_dtype).
+OK, INVALID_ARGUMENT, UNIMPLEMENTED, INTERNAL = 0, 3, 12, 13
+U8, F16, F32, BF16 = 6, 10, 11, 16
+
+
+def load(path=None):
+    """Load the library at ``path`` (default: the packaged gfx950 library) and declare types."""
+    lib = ctypes.CDLL(path or library_path("attention", "gfx950"))
+    for name, (res, args) in PROTOTYPES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+def lib():
+    """The process-wide handle of the packaged library."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                _lib = load()
+    return _lib
+
+
+def last_error():
+    return lib().clk_last_error().decode()

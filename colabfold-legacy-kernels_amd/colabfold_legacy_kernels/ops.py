@@ -1,0 +1,301 @@
+"""PyTorch front end of the gfx950 kernels: allocate outputs, pass pointers to the C ABI.
+
+Each function mirrors one XLA FFI target of the reference -- the same operands in the same order,
+the same attributes, the same errors -- with torch tensors on a ROCm device in place of XLA
+buffers:
+
+  attention(q, k, v, bias, kmask, scale, block_q, block_k)   VoltaMma   (cuda/volta_mma_attn.cu:338-351)
+  layer_norm(x, scale, offset, eps)                          VoltaLayerNorm (cuda/volta_ops.cu:87-95)
+  gated_dual_proj(x, wp, bp, wg, bg, mask)                   VoltaGdp   (cuda/volta_ops.cu:254-265)
+
+and the targets the reference lacks: attention_fwd (also returns the logsumexp), attention_bwd,
+layer_norm_bwd and ln_gated_dual_proj. An invalid call raises InvalidArgument (a ValueError), as
+the reference handlers return ffi::Error::InvalidArgument; a launch failure raises InternalError.
+
+Torch is used only for device memory and the current stream; all arithmetic runs in the HIP
+library, and a missing library raises FileNotFoundError (there is no fallback path).
+"""
+
+import math
+
+import torch
+
+from . import _native
+
+__all__ = [
+    "ClkError", "InvalidArgument", "InternalError",
+    "attention", "attention_fwd", "attention_bwd",
+    "layer_norm", "layer_norm_bwd",
+    "gated_dual_proj", "ln_gated_dual_proj",
+    "AttentionFunction", "LayerNormFunction",
+]
+
+
+class ClkError(RuntimeError):
+    """A non-OK status from the library; ``code`` is the clk_status value."""
+
+    def __init__(self, code, message):
+        super().__init__(message)
+        self.code = code
+
+
+class InvalidArgument(ClkError, ValueError):
+    pass
+
+
+class InternalError(ClkError):
+    pass
+
+
+_DTYPES = {torch.float16: _native.F16, torch.bfloat16: _native.BF16,
+           torch.float32: _native.F32}
+
+
+def _check(status):
+    if status == _native.OK:
+        return
+    msg = _native.last_error()
+    if status == _native.INVALID_ARGUMENT:
+        raise InvalidArgument(status, msg)
+    raise InternalError(status, msg)
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _dtype_code(t, allowed, what):
+    code = _DTYPES.get(t.dtype)
+    if code is None or code not in allowed:
+        raise InvalidArgument(_native.INVALID_ARGUMENT,
+                              "%s: dtype %s not supported" % (what, t.dtype))
+    return code
+
+
+def _require(tensors, what):
+    dev = None
+    for name, t in tensors:
+        if t is None:
+            continue
+        if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+            raise InvalidArgument(_native.INVALID_ARGUMENT,
+                                  "%s: %s must be a tensor on a ROCm device" % (what, name))
+        if not t.is_contiguous():
+            raise InvalidArgument(_native.INVALID_ARGUMENT, "%s: %s must be contiguous" % (what, name))
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise InvalidArgument(_native.INVALID_ARGUMENT,
+                                  "%s: all operands must be on one device" % what)
+    return dev
+
+
+def _stream(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _shape_check(cond, what, msg):
+    if not cond:
+        raise InvalidArgument(_native.INVALID_ARGUMENT, "%s: %s" % (what, msg))
+
+
+def _attn_dims(q, k, v, bias, kmask, what):
+    _shape_check(q.dim() == 4, what, "q must be [N,H,S,D]")
+    n, h, sq, d = q.shape
+    _shape_check(k.dim() == 4 and k.shape[0] == n and k.shape[1] == h and k.shape[3] == d,
+                 what, "k must be [N,H,Sk,D]")
+    sk = k.shape[2]
+    _shape_check(tuple(v.shape) == tuple(k.shape), what, "v must have the shape of k")
+    _shape_check(tuple(bias.shape) == (h, sq, sk), what, "bias must be [H,Sq,Sk]")
+    _shape_check(q.dtype == k.dtype == v.dtype == bias.dtype, what,
+                 "q, k, v and bias must share one dtype")
+    if kmask is not None:
+        _shape_check(tuple(kmask.shape) == (n, sk) and kmask.dtype == torch.uint8, what,
+                     "kmask must be uint8 [N,Sk]")
+    return n, h, sq, sk, d
+
+
+def _attention_call(q, k, v, bias, kmask, scale, block_q, block_k, want_lse, what):
+    dev = _require([("q", q), ("k", k), ("v", v), ("bias", bias), ("kmask", kmask)], what)
+    n, h, sq, sk, d = _attn_dims(q, k, v, bias, kmask, what)
+    code = _dtype_code(q, (_native.F16, _native.BF16), what)
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    out = torch.empty_like(q)
+    lse = torch.empty((n, h, sq), device=dev, dtype=torch.float32) if want_lse else None
+    lib = _native.lib()
+    with torch.cuda.device(dev):
+        _check(lib.clk_attention_fwd(_stream(dev), code, _ptr(q), _ptr(k), _ptr(v), _ptr(bias),
+                                     _ptr(kmask), _ptr(out), _ptr(lse), n, h, sq, sk, d,
+                                     float(scale), int(block_q), int(block_k)))
+    return out, lse
+
+
+def attention(q, k, v, bias, kmask=None, scale=None, block_q=64, block_k=64):
+    """softmax(scale*q.k^T + bias, masked keys -> -1e9) . v for q [N,H,Sq,D], k/v [N,H,Sk,D],
+    bias [H,Sq,Sk], kmask uint8 [N,Sk]. block_q/block_k are accepted as hints."""
+    out, _ = _attention_call(q, k, v, bias, kmask, scale, block_q, block_k, False, "attention")
+    return out
+
+
+def attention_fwd(q, k, v, bias, kmask=None, scale=None):
+    """(out, lse): the forward plus the float32 natural-log logsumexp [N,H,Sq] per query."""
+    return _attention_call(q, k, v, bias, kmask, scale, 64, 64, True, "attention_fwd")
+
+
+def attention_bwd(q, k, v, bias, kmask, out, dout, lse, scale=None):
+    """(dq, dk, dv, dbias) with dbias [H,Sq,Sk] float32 summed over the N rows."""
+    what = "attention_bwd"
+    dev = _require([("q", q), ("k", k), ("v", v), ("bias", bias), ("kmask", kmask),
+                    ("out", out), ("dout", dout), ("lse", lse)], what)
+    n, h, sq, sk, d = _attn_dims(q, k, v, bias, kmask, what)
+    code = _dtype_code(q, (_native.F16, _native.BF16), what)
+    _shape_check(tuple(out.shape) == tuple(q.shape) and out.dtype == q.dtype, what,
+                 "out must match q")
+    _shape_check(tuple(dout.shape) == tuple(q.shape) and dout.dtype == q.dtype, what,
+                 "dout must match q")
+    _shape_check(tuple(lse.shape) == (n, h, sq) and lse.dtype == torch.float32, what,
+                 "lse must be float32 [N,H,Sq]")
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    lib = _native.lib()
+    ws_bytes = lib.clk_attention_bwd_workspace_size(n, h, sq, sk, d)
+    ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dbias = torch.empty((h, sq, sk), device=dev, dtype=torch.float32)
+    with torch.cuda.device(dev):
+        _check(lib.clk_attention_bwd(_stream(dev), code, _ptr(q), _ptr(k), _ptr(v), _ptr(bias),
+                                     _ptr(kmask), _ptr(out), _ptr(dout), _ptr(lse), _ptr(dq),
+                                     _ptr(dk), _ptr(dv), _ptr(dbias), _ptr(ws), ws_bytes, n, h,
+                                     sq, sk, d, float(scale)))
+    return dq, dk, dv, dbias
+
+
+def _ln_dims(x, scale, what):
+    _shape_check(x.dim() >= 1, what, "x must have at least one axis")
+    c = x.shape[-1]
+    m = x.numel() // c if c else 0
+    _shape_check(tuple(scale.shape) == (c,) and scale.dtype == torch.float32, what,
+                 "scale must be float32 [C]")
+    return m, c
+
+
+def layer_norm(x, scale, offset, eps=1e-5):
+    """LayerNorm over the last axis of x (f16, bf16 or f32); scale and offset float32 [C]."""
+    what = "layer_norm"
+    dev = _require([("x", x), ("scale", scale), ("offset", offset)], what)
+    m, c = _ln_dims(x, scale, what)
+    _shape_check(tuple(offset.shape) == (c,) and offset.dtype == torch.float32, what,
+                 "offset must be float32 [C]")
+    code = _dtype_code(x, (_native.F16, _native.BF16, _native.F32), what)
+    y = torch.empty_like(x)
+    with torch.cuda.device(dev):
+        _check(_native.lib().clk_layer_norm_fwd(_stream(dev), code, _ptr(x), _ptr(scale),
+                                                _ptr(offset), _ptr(y), m, c, float(eps)))
+    return y
+
+
+def layer_norm_bwd(x, scale, dy, eps=1e-5):
+    """(dx, dscale, doffset); dscale and doffset are float32 [C]."""
+    what = "layer_norm_bwd"
+    dev = _require([("x", x), ("scale", scale), ("dy", dy)], what)
+    m, c = _ln_dims(x, scale, what)
+    _shape_check(tuple(dy.shape) == tuple(x.shape) and dy.dtype == x.dtype, what,
+                 "dy must match x")
+    code = _dtype_code(x, (_native.F16, _native.BF16, _native.F32), what)
+    lib = _native.lib()
+    ws_bytes = lib.clk_layer_norm_bwd_workspace_size(m, c)
+    ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+    dx = torch.empty_like(x)
+    dscale = torch.empty(c, device=dev, dtype=torch.float32)
+    doffset = torch.empty(c, device=dev, dtype=torch.float32)
+    with torch.cuda.device(dev):
+        _check(lib.clk_layer_norm_bwd(_stream(dev), code, _ptr(x), _ptr(scale), _ptr(dy),
+                                      _ptr(dx), _ptr(dscale), _ptr(doffset), _ptr(ws), ws_bytes,
+                                      m, c, float(eps)))
+    return dx, dscale, doffset
+
+
+def gated_dual_proj(x, wp, bp, wg, bg, mask):
+    """mask[m] * (x.wp + bp) * sigmoid(x.wg + bg) for x [M,K], wp/wg [K,N], bp/bg [N], mask [M]."""
+    what = "gated_dual_proj"
+    dev = _require([("x", x), ("wp", wp), ("bp", bp), ("wg", wg), ("bg", bg), ("mask", mask)],
+                   what)
+    _shape_check(x.dim() == 2, what, "x must be [M,K]")
+    m, kdim = x.shape
+    _shape_check(wp.dim() == 2 and wp.shape[0] == kdim, what, "wp must be [K,N]")
+    n = wp.shape[1]
+    _shape_check(tuple(wg.shape) == (kdim, n), what, "wg must be [K,N]")
+    _shape_check(tuple(bp.shape) == (n,) and tuple(bg.shape) == (n,), what, "bp, bg must be [N]")
+    _shape_check(tuple(mask.shape) == (m,), what, "mask must be [M]")
+    _shape_check(all(t.dtype == x.dtype for t in (wp, bp, wg, bg, mask)), what,
+                 "all operands must share one dtype")
+    code = _dtype_code(x, (_native.F16, _native.BF16), what)
+    out = torch.empty((m, n), device=dev, dtype=x.dtype)
+    with torch.cuda.device(dev):
+        _check(_native.lib().clk_gated_dual_proj(_stream(dev), code, _ptr(x), _ptr(wp), _ptr(bp),
+                                                 _ptr(wg), _ptr(bg), _ptr(mask), _ptr(out), m,
+                                                 kdim, n))
+    return out
+
+
+def ln_gated_dual_proj(z, ln_scale, ln_offset, branch_a, branch_b, mask, eps=1e-5):
+    """(a, b): LayerNorm(z) then both gated projections, in one pass. Each branch is
+    (wp, bp, wg, bg); z [M,C] (or [..., C]); mask [M]."""
+    what = "ln_gated_dual_proj"
+    wpa, bpa, wga, bga = branch_a
+    wpb, bpb, wgb, bgb = branch_b
+    dev = _require([("z", z), ("ln_scale", ln_scale), ("ln_offset", ln_offset), ("wpa", wpa),
+                    ("bpa", bpa), ("wga", wga), ("bga", bga), ("wpb", wpb), ("bpb", bpb),
+                    ("wgb", wgb), ("bgb", bgb), ("mask", mask)], what)
+    m, c = _ln_dims(z, ln_scale, what)
+    _shape_check(wpa.dim() == 2 and wpa.shape[0] == c, what, "weights must be [C,N]")
+    n = wpa.shape[1]
+    for name, w in (("wga", wga), ("wpb", wpb), ("wgb", wgb)):
+        _shape_check(tuple(w.shape) == (c, n), what, "%s must be [C,N]" % name)
+    for name, b in (("bpa", bpa), ("bga", bga), ("bpb", bpb), ("bgb", bgb)):
+        _shape_check(tuple(b.shape) == (n,), what, "%s must be [N]" % name)
+    _shape_check(mask.numel() == m, what, "mask must have M elements")
+    code = _dtype_code(z, (_native.F16, _native.BF16), what)
+    a = torch.empty(tuple(z.shape[:-1]) + (n,), device=dev, dtype=z.dtype)
+    b = torch.empty_like(a)
+    with torch.cuda.device(dev):
+        _check(_native.lib().clk_ln_gated_dual_proj(
+            _stream(dev), code, _ptr(z), _ptr(ln_scale), _ptr(ln_offset), _ptr(wpa), _ptr(bpa),
+            _ptr(wga), _ptr(bga), _ptr(wpb), _ptr(bpb), _ptr(wgb), _ptr(bgb), _ptr(mask),
+            _ptr(a), _ptr(b), m, c, n, float(eps)))
+    return a, b
+
+
+class AttentionFunction(torch.autograd.Function):
+    """Differentiable attention: forward saves (out, lse); backward calls attention_bwd."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, bias, kmask, scale):
+        out, lse = attention_fwd(q, k, v, bias, kmask, scale)
+        ctx.save_for_backward(q, k, v, bias, kmask, out, lse)
+        ctx.scale = scale
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, bias, kmask, out, lse = ctx.saved_tensors
+        dq, dk, dv, dbias = attention_bwd(q, k, v, bias, kmask, out, dout.contiguous(), lse,
+                                          ctx.scale)
+        return dq, dk, dv, dbias.to(bias.dtype), None, None
+
+
+class LayerNormFunction(torch.autograd.Function):
+    """Differentiable LayerNorm over the last axis (statistics recomputed in backward)."""
+
+    @staticmethod
+    def forward(ctx, x, scale, offset, eps):
+        ctx.save_for_backward(x, scale)
+        ctx.eps = eps
+        return layer_norm(x, scale, offset, eps)
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, scale = ctx.saved_tensors
+        dx, dscale, doffset = layer_norm_bwd(x, scale, dy.contiguous(), ctx.eps)
+        return dx, dscale, doffset, None

@@ -1,0 +1,200 @@
+// Pieces shared by the attention forward and backward kernels: tile geometry, global->LDS tile
+// staging, MFMA operand reads from LDS, bias/mask loads and host-side validation.
+#pragma once
+
+#include "common.hpp"
+
+namespace clk {
+
+// Geometry for head dim D: 64-key (or 64-query) tiles; KS contraction steps of 32 head dims for
+// the products that contract over D; DT 16-row tiles of head dims for the products that output
+// head dims. LDS rows are padded by 8 elements (16 bytes) to spread banks.
+template <int D>
+struct AttnGeom {
+    static_assert(D == 8 || D == 16 || D == 32 || D == 64, "head dim 8, 16, 32 or 64");
+    static constexpr int BK = 64;
+    static constexpr int KS = (D + 31) / 32;
+    static constexpr int DT = (D + 15) / 16;
+    static constexpr int DV = DT * 16;
+    static constexpr int KLD = D + 8;
+    static constexpr int VLD = DV + 8;
+};
+
+// Row of the 16-row operand tile t (0..3) of a 64-row tile that lane row r16 supplies. Inside
+// each 32-row chunk c = t/2 the rows are permuted so that the C tile of the product holds rows
+// 32c + 8*(l/16) + 0..7 in lane l: half t%2 covers +0..3, the other +4..7.
+__device__ __forceinline__ int perm_key(int t, int r16) {
+    return 32 * (t >> 1) + 8 * (r16 >> 2) + 4 * (t & 1) + (r16 & 3);
+}
+
+// 8-slot MFMA operand from a row-major LDS tile: row `row`, head dims 32*ks + 8*g + 0..7
+// (zero beyond D).
+template <typename V8, int D, typename E>
+__device__ __forceinline__ V8 lds_row_operand(const E* lds, int row, int ld, int ks, int g) {
+    const int d0 = ks * 32 + g * 8;
+    u32x4 raw = {0u, 0u, 0u, 0u};
+    if (d0 < D) raw = *reinterpret_cast<const u32x4*>(lds + row * ld + d0);
+    return bits_as<V8>(raw);
+}
+
+// 8-slot MFMA operand of the transposed tile: lane (r16, g) gets column 16*dt + r16 of rows
+// 32c + 8g + 0..7 of a row-major LDS tile (two ds_read_b64_tr_b16).
+template <typename V8, typename E>
+__device__ __forceinline__ V8 lds_tr_operand(const E* lds, int ld, int c, int dt, int r16,
+                                             int g) {
+    const E* lo = lds + (32 * c + 8 * g + (r16 >> 2)) * ld + 16 * dt + 4 * (r16 & 3);
+    return lds_tr8<V8>(lo, lo + 4 * ld);
+}
+
+// Stages a 64-row x D tile of one or two [S, D] operands: 16-byte global loads into registers
+// (rows past S read as zero), then 16-byte LDS stores.
+template <typename E, int D, int NOPS>
+struct RowTileStager {
+    static constexpr int CPR = D / 8;
+    static constexpr int CHUNKS = 64 * CPR;
+    static constexpr int CPT = (CHUNKS + 255) / 256;
+    u32x4 r[NOPS][CPT];
+
+    __device__ __forceinline__ void load(const E* const* src, int row0, int S) {
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int ch = threadIdx.x + 256 * i;
+            const int row = ch / CPR, c8 = (ch % CPR) * 8;
+            const bool in = ch < CHUNKS && row0 + row < S;
+#pragma unroll
+            for (int o = 0; o < NOPS; ++o) {
+                r[o][i] = u32x4{0u, 0u, 0u, 0u};
+                if (in) r[o][i] = ld16(src[o] + (size_t)(row0 + row) * D + c8);
+            }
+        }
+    }
+    __device__ __forceinline__ void store(E* const* dst, const int* ld) {
+#pragma unroll
+        for (int i = 0; i < CPT; ++i) {
+            const int ch = threadIdx.x + 256 * i;
+            if (ch < CHUNKS) {
+                const int row = ch / CPR, c8 = (ch % CPR) * 8;
+#pragma unroll
+                for (int o = 0; o < NOPS; ++o)
+                    *reinterpret_cast<u32x4*>(dst[o] + row * ld[o] + c8) = r[o][i];
+            }
+        }
+    }
+};
+
+// K and V key tiles for the forward pass.
+template <typename E, int D>
+struct TileStager {
+    RowTileStager<E, D, 2> st;
+    __device__ __forceinline__ void load(const E* kp, const E* vp, int k0, int Sk) {
+        const E* src[2] = {kp, vp};
+        st.load(src, k0, Sk);
+    }
+    __device__ __forceinline__ void store(E* k_lds, E* v_lds) {
+        E* dst[2] = {k_lds, v_lds};
+        const int ld[2] = {AttnGeom<D>::KLD, AttnGeom<D>::VLD};
+        st.store(dst, ld);
+    }
+};
+
+// Zero the LDS columns D..DV-1 of a V-like tile (only D = 8 has any); they feed output rows that
+// are never stored, but must not hold NaN bit patterns from earlier kernels.
+template <typename E, int D>
+__device__ __forceinline__ void zero_v_padding(E* lds) {
+    constexpr int DV = AttnGeom<D>::DV, VLD = AttnGeom<D>::VLD;
+    if constexpr (DV > D) {
+        for (int i = threadIdx.x; i < 64 * (DV - D); i += blockDim.x)
+            lds[(i / (DV - D)) * VLD + D + i % (DV - D)] = E(0.f);
+    }
+}
+
+// Eight elements of a 16-byte vector as float.
+template <typename TR>
+__device__ __forceinline__ void unpack8(u32x4 raw, float* out) {
+    typename TR::elem e[8];
+    __builtin_memcpy(e, &raw, 16);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) out[j] = TR::to_f(e[j]);
+}
+
+// Eight bias values bias_row[kk .. kk+7] as float (zero past Sk).
+template <typename TR>
+__device__ __forceinline__ void load_bias8(const typename TR::elem* row, int kk, int Sk,
+                                           int vec_ok, float* out) {
+    using E = typename TR::elem;
+    if (vec_ok && kk + 8 <= Sk) {
+        E e[8];
+        u32x4 raw = ld16(row + kk);
+        __builtin_memcpy(e, &raw, 16);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) out[j] = TR::to_f(e[j]);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) out[j] = (kk + j < Sk) ? TR::to_f(row[kk + j]) : 0.f;
+    }
+}
+
+// Bit j set when key kk + j exists (< Sk) and is present in the mask row (or there is no mask).
+__device__ __forceinline__ unsigned key_valid8(const uint8_t* mrow, int kk, int Sk, int vec_ok) {
+    unsigned bits = 0;
+    if (mrow && vec_ok && kk + 8 <= Sk && ((reinterpret_cast<uintptr_t>(mrow + kk) & 7u) == 0)) {
+        const u32x2 w = *reinterpret_cast<const u32x2*>(mrow + kk);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            bits |= (((w[0] >> (8 * j)) & 0xffu) != 0u ? 1u : 0u) << j;
+            bits |= (((w[1] >> (8 * j)) & 0xffu) != 0u ? 1u : 0u) << (4 + j);
+        }
+        return bits;
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const bool in = kk + j < Sk;
+        const bool present = in && (mrow == nullptr || mrow[kk + j] != 0);
+        bits |= (present ? 1u : 0u) << j;
+    }
+    return bits;
+}
+
+// Logit given to masked keys of one mask row: -1e9, or 0 when the row has no present key (the
+// softmax is uniform either way; 0 keeps the running max and the logsumexp exact in float32).
+// Must be reached by every thread of the block.
+__device__ __forceinline__ float masked_logit_for_row(const uint8_t* mrow, int Sk) {
+    int any = 0;
+    if (mrow) {
+        for (int i = threadIdx.x; i < Sk; i += blockDim.x) any |= mrow[i] != 0;
+    }
+    any = __syncthreads_or(any);
+    return (mrow && !any) ? 0.f : kMaskedLogit;
+}
+
+template <typename TR>
+__device__ __forceinline__ void store4(typename TR::elem* p, f32x4 v) {
+    using E = typename TR::elem;
+    E e[4] = {TR::from_f(v[0]), TR::from_f(v[1]), TR::from_f(v[2]), TR::from_f(v[3])};
+    u32x2 raw;
+    __builtin_memcpy(&raw, e, 8);
+    st8(p, raw);
+}
+
+// Host-side shape/dtype validation shared by the forward and backward entry points. The
+// reference checks only the rank of q (cuda/volta_mma_attn.cu:310-314); every size is checked
+// here before any launch.
+inline clk_status validate_attention(const char* who, clk_dtype dtype, int64_t N, int64_t H,
+                                     int64_t Sq, int64_t Sk, int64_t D) {
+    if (dtype != CLK_F16 && dtype != CLK_BF16)
+        return fail(CLK_INVALID_ARGUMENT, "%s: dtype %s not supported (f16, bf16)", who,
+                    dtype_name(dtype));
+    if (N < 0 || H < 0 || Sq < 0 || Sk < 0)
+        return fail(CLK_INVALID_ARGUMENT, "%s: negative dimension", who);
+    if (D != 8 && D != 16 && D != 32 && D != 64)
+        return fail(CLK_INVALID_ARGUMENT, "%s: unsupported head dim D=%lld (8, 16, 32, 64)", who,
+                    (long long)D);
+    if (N > 65535 || H > 65535 || Sq > (1 << 20) || Sk > (1 << 20))
+        return fail(CLK_INVALID_ARGUMENT, "%s: dims [N=%lld,H=%lld,Sq=%lld,Sk=%lld] too large",
+                    who, (long long)N, (long long)H, (long long)Sq, (long long)Sk);
+    if (N * H * (Sq > Sk ? Sq : Sk) * D > ((int64_t)1 << 40) || H * Sq * Sk > ((int64_t)1 << 40))
+        return fail(CLK_INVALID_ARGUMENT, "%s: tensor too large", who);
+    return CLK_OK;
+}
+
+}  // namespace clk

@@ -1,0 +1,132 @@
+// Shared helpers for the gfx950 Evoformer kernels: vector types, MFMA wrappers, element
+// conversions, the LDS transpose read and the host-side status plumbing.
+//
+// MFMA register layouts used throughout (measured on gfx950 with an in-bounds probe):
+//   v_mfma_f32_16x16x32_{bf16,f16}: A[16 x 32] lane l holds row l%16, 8 k-slots of group l/16;
+//   B[32 x 16] lane l holds column l%16, the same 8 k-slots; C[16 x 16] lane l holds column
+//   l%16, rows 4*(l/16)+i for i = 0..3. A and B share the k-slot map, so any permutation of the
+//   contraction index that is applied to both operands is exact.
+//   ds_read_b64_tr_b16: within each 16-lane group, lane r supplies an 8-byte address; lane i
+//   receives element i%4 of the read of lane 4*j + i/4 as its element j. With lane 4*j+t
+//   pointing at row j, columns c0+4t..c0+4t+3 of a row-major tile, lane i gets column c0+i of
+//   rows 0..3: a transposed 4x16 block.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_bf16.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <cstdarg>
+#include <string>
+
+#include "clk.h"
+
+namespace clk {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kMaskedLogit = -1.0e9f;
+
+// ---------------------------------------------------------------------------------------------
+// Element traits: storage type <-> float, and the 8-wide MFMA operand type.
+// ---------------------------------------------------------------------------------------------
+struct BF16 {
+    using elem = __bf16;
+    using vec8 = bf16x8;
+    using vec4 = bf16x4;
+    static __device__ __forceinline__ float to_f(elem x) { return (float)x; }
+    static __device__ __forceinline__ elem from_f(float x) { return (elem)x; }
+    static __device__ __forceinline__ f32x4 mfma(vec8 a, vec8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+};
+
+struct F16 {
+    using elem = _Float16;
+    using vec8 = f16x8;
+    using vec4 = f16x4;
+    static __device__ __forceinline__ float to_f(elem x) { return (float)x; }
+    static __device__ __forceinline__ elem from_f(float x) { return (elem)x; }
+    static __device__ __forceinline__ f32x4 mfma(vec8 a, vec8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+};
+
+struct F32 {
+    using elem = float;
+    static __device__ __forceinline__ float to_f(elem x) { return x; }
+    static __device__ __forceinline__ elem from_f(float x) { return x; }
+};
+
+// 16-byte global load/store of 8 half-width elements, as raw bits.
+__device__ __forceinline__ u32x4 ld16(const void* p) {
+    return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+__device__ __forceinline__ u32x2 ld8(const void* p) {
+    return *reinterpret_cast<const u32x2*>(p);
+}
+__device__ __forceinline__ void st8(void* p, u32x2 v) { *reinterpret_cast<u32x2*>(p) = v; }
+
+template <typename V>
+__device__ __forceinline__ V bits_as(u32x4 v) {
+    return __builtin_bit_cast(V, v);
+}
+
+// Two 4-element LDS transpose reads -> one 8-slot MFMA operand.
+__device__ __forceinline__ i16x4 lds_tr4(const void* lds_ptr) {
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) i16x4*)(lds_ptr));
+}
+template <typename V>
+__device__ __forceinline__ V lds_tr8(const void* p_lo, const void* p_hi) {
+    i16x4 a = lds_tr4(p_lo);
+    i16x4 b = lds_tr4(p_hi);
+    typedef short i16x8 __attribute__((ext_vector_type(8)));
+    i16x8 r = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    return __builtin_bit_cast(V, r);
+}
+
+// Cross-lane reductions among the four lanes l, l^16, l^32, l^48 (same column of a C tile).
+__device__ __forceinline__ float xgroup_max(float v) {
+    v = fmaxf(v, __shfl_xor(v, 16));
+    v = fmaxf(v, __shfl_xor(v, 32));
+    return v;
+}
+__device__ __forceinline__ float xgroup_sum(float v) {
+    v += __shfl_xor(v, 16);
+    v += __shfl_xor(v, 32);
+    return v;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
+
+// ---------------------------------------------------------------------------------------------
+// Host side: thread-local last-error message and status helpers.
+// ---------------------------------------------------------------------------------------------
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+clk_status fail(clk_status code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+clk_status ok();
+clk_status check_launch(const char* what);
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+inline size_t elem_size(clk_dtype t) {
+    return t == CLK_F32 ? 4 : (t == CLK_U8 ? 1 : 2);
+}
+const char* dtype_name(clk_dtype t);
+
+inline int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+
+}  // namespace clk

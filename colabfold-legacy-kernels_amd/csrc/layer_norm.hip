@@ -1,0 +1,501 @@
+// LayerNorm over the last axis for gfx950: forward (replaces VoltaLayerNorm,
+// cuda/volta_ops.cu:28-95) and backward (new).
+//
+// Layout: x, y, dy, dx [M, C] of bf16, f16 or f32; scale, offset [C] float32.
+// Each row is owned by LPR consecutive lanes; lane s of a row holds NV 16-byte vectors at
+// columns ((v*LPR + s)*VEC ... +VEC), so a wave's loads are contiguous 16-byte chunks. The row
+// stays in registers: the statistics are a per-lane two-pass mean/M2 merged across the LPR lanes
+// with Chan's pairwise (Welford) update, then y is formed from the same registers -- one read and
+// one write of HBM per element (the reference reads x twice, volta_ops.cu:40-45 and :55-58).
+// HBM-bound: forward moves M*C*(b_in + b_out) bytes, backward M*C*(2*b_in + b_out).
+#include "common.hpp"
+
+namespace clk {
+namespace {
+
+constexpr int kThreads = 256;
+
+template <typename TR>
+struct Vec {
+    static constexpr int N = 16 / sizeof(typename TR::elem);
+};
+
+template <typename TR>
+__device__ __forceinline__ void unpack(u32x4 raw, float* out) {
+    using E = typename TR::elem;
+    constexpr int N = Vec<TR>::N;
+    E e[N];
+    __builtin_memcpy(e, &raw, 16);
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = TR::to_f(e[i]);
+}
+
+template <typename TR>
+__device__ __forceinline__ u32x4 pack(const float* in) {
+    using E = typename TR::elem;
+    constexpr int N = Vec<TR>::N;
+    E e[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) e[i] = TR::from_f(in[i]);
+    u32x4 raw;
+    __builtin_memcpy(&raw, e, 16);
+    return raw;
+}
+
+// Chan's merge of (mean, M2) between lanes that own equal element counts; every lane of the row
+// ends with bit-identical values (each step is symmetric in its two operands).
+template <int LPR>
+__device__ __forceinline__ void merge_stats(float& mean, float& m2, float count) {
+#pragma unroll
+    for (int off = 1; off < LPR; off <<= 1) {
+        const float om = __shfl_xor(mean, off);
+        const float o2 = __shfl_xor(m2, off);
+        const float d = om - mean;
+        mean = (mean + om) * 0.5f;
+        m2 = (m2 + o2) + d * d * (count * 0.5f);
+        count *= 2.f;
+    }
+}
+
+template <int LPR>
+__device__ __forceinline__ float row_sum(float v) {
+#pragma unroll
+    for (int off = 1; off < LPR; off <<= 1) v += __shfl_xor(v, off);
+    return v;
+}
+
+template <typename TR, int LPR, int NV>
+__global__ __launch_bounds__(kThreads) void ln_fwd_kernel(const void* __restrict__ xv,
+                                                          const float* __restrict__ scale,
+                                                          const float* __restrict__ offset,
+                                                          void* __restrict__ yv, int M, float eps) {
+    using E = typename TR::elem;
+    constexpr int VEC = Vec<TR>::N;
+    constexpr int C = LPR * NV * VEC;
+    constexpr int ROWS = kThreads / LPR;
+    const E* x = static_cast<const E*>(xv);
+    E* y = static_cast<E*>(yv);
+    const int s = threadIdx.x % LPR;
+    const int slot = threadIdx.x / LPR;
+
+    float g[NV][VEC], b[NV][VEC];
+#pragma unroll
+    for (int v = 0; v < NV; ++v)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+            const int c = (v * LPR + s) * VEC + i;
+            g[v][i] = scale[c];
+            b[v][i] = offset[c];
+        }
+
+    for (int row = blockIdx.x * ROWS + slot; row < M; row += gridDim.x * ROWS) {
+        const E* xr = x + (size_t)row * C;
+        float xs[NV][VEC];
+#pragma unroll
+        for (int v = 0; v < NV; ++v) unpack<TR>(ld16(xr + (v * LPR + s) * VEC), xs[v]);
+        float sum = 0.f;
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) sum += xs[v][i];
+        float mean = sum * (1.f / (NV * VEC));
+        float m2 = 0.f;
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) {
+                const float d = xs[v][i] - mean;
+                m2 += d * d;
+            }
+        merge_stats<LPR>(mean, m2, (float)(NV * VEC));
+        const float rstd = rsqrtf(m2 * (1.f / C) + eps);
+        E* yr = y + (size_t)row * C;
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            float o[VEC];
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) o[i] = (xs[v][i] - mean) * rstd * g[v][i] + b[v][i];
+            st16(yr + (v * LPR + s) * VEC, pack<TR>(o));
+        }
+    }
+}
+
+// One wave per row, any C: two passes over the row from global memory.
+template <typename TR>
+__global__ __launch_bounds__(kThreads) void ln_fwd_generic(const void* __restrict__ xv,
+                                                           const float* __restrict__ scale,
+                                                           const float* __restrict__ offset,
+                                                           void* __restrict__ yv, int M, int C,
+                                                           float eps) {
+    using E = typename TR::elem;
+    const E* x = static_cast<const E*>(xv);
+    E* y = static_cast<E*>(yv);
+    const int lane = threadIdx.x % 64;
+    const int waves = kThreads / 64;
+    for (int row = blockIdx.x * waves + threadIdx.x / 64; row < M; row += gridDim.x * waves) {
+        const E* xr = x + (size_t)row * C;
+        float sum = 0.f;
+        for (int c = lane; c < C; c += 64) sum += TR::to_f(xr[c]);
+        sum = row_sum<64>(sum);
+        const float mean = sum / C;
+        float m2 = 0.f;
+        for (int c = lane; c < C; c += 64) {
+            const float d = TR::to_f(xr[c]) - mean;
+            m2 += d * d;
+        }
+        m2 = row_sum<64>(m2);
+        const float rstd = rsqrtf(m2 / C + eps);
+        E* yr = y + (size_t)row * C;
+        for (int c = lane; c < C; c += 64)
+            yr[c] = TR::from_f((TR::to_f(xr[c]) - mean) * rstd * scale[c] + offset[c]);
+    }
+}
+
+// Backward. Per row: dx = r*(g - mean(g) - xhat*mean(g*xhat)), g = scale*dy. Column sums of
+// dy*xhat and dy accumulate per lane over the rows the lane visits, then over the block's row
+// slots in a fixed order, into part[block][2][C]; ln_colsum adds the blocks in a fixed order.
+template <typename TR, int LPR, int NV>
+__global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const void* __restrict__ xv,
+                                                          const float* __restrict__ scale,
+                                                          const void* __restrict__ dyv,
+                                                          void* __restrict__ dxv,
+                                                          float* __restrict__ part, int M,
+                                                          float eps) {
+    using E = typename TR::elem;
+    constexpr int VEC = Vec<TR>::N;
+    constexpr int C = LPR * NV * VEC;
+    constexpr int ROWS = kThreads / LPR;
+    const E* x = static_cast<const E*>(xv);
+    const E* dy = static_cast<const E*>(dyv);
+    E* dx = static_cast<E*>(dxv);
+    const int s = threadIdx.x % LPR;
+    const int slot = threadIdx.x / LPR;
+
+    float g[NV][VEC], acc_g[NV][VEC], acc_b[NV][VEC];
+#pragma unroll
+    for (int v = 0; v < NV; ++v)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+            g[v][i] = scale[(v * LPR + s) * VEC + i];
+            acc_g[v][i] = 0.f;
+            acc_b[v][i] = 0.f;
+        }
+
+    for (int row = blockIdx.x * ROWS + slot; row < M; row += gridDim.x * ROWS) {
+        const size_t base = (size_t)row * C;
+        float xs[NV][VEC], ds[NV][VEC];
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            unpack<TR>(ld16(x + base + (v * LPR + s) * VEC), xs[v]);
+            unpack<TR>(ld16(dy + base + (v * LPR + s) * VEC), ds[v]);
+        }
+        float sum = 0.f;
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) sum += xs[v][i];
+        float mean = sum * (1.f / (NV * VEC));
+        float m2 = 0.f;
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) {
+                const float d = xs[v][i] - mean;
+                m2 += d * d;
+            }
+        merge_stats<LPR>(mean, m2, (float)(NV * VEC));
+        const float rstd = rsqrtf(m2 * (1.f / C) + eps);
+        float sg = 0.f, sgx = 0.f;
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) {
+                const float xh = (xs[v][i] - mean) * rstd;
+                const float gg = g[v][i] * ds[v][i];
+                xs[v][i] = xh;
+                sg += gg;
+                sgx += gg * xh;
+                acc_g[v][i] += ds[v][i] * xh;
+                acc_b[v][i] += ds[v][i];
+            }
+        sg = row_sum<LPR>(sg) * (1.f / C);
+        sgx = row_sum<LPR>(sgx) * (1.f / C);
+#pragma unroll
+        for (int v = 0; v < NV; ++v) {
+            float o[VEC];
+#pragma unroll
+            for (int i = 0; i < VEC; ++i)
+                o[i] = rstd * (g[v][i] * ds[v][i] - sg - xs[v][i] * sgx);
+            st16(dx + base + (v * LPR + s) * VEC, pack<TR>(o));
+        }
+    }
+
+    // Fixed-order reduction over the ROWS row slots of this block.
+    __shared__ float red[ROWS][2][C];
+#pragma unroll
+    for (int v = 0; v < NV; ++v)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+            const int c = (v * LPR + s) * VEC + i;
+            red[slot][0][c] = acc_g[v][i];
+            red[slot][1][c] = acc_b[v][i];
+        }
+    __syncthreads();
+    for (int t = threadIdx.x; t < 2 * C; t += kThreads) {
+        const int which = t / C, c = t % C;
+        float a = 0.f;
+        for (int r = 0; r < ROWS; ++r) a += red[r][which][c];
+        part[((size_t)blockIdx.x * 2 + which) * C + c] = a;
+    }
+}
+
+template <typename TR>
+__global__ __launch_bounds__(kThreads) void ln_bwd_generic(const void* __restrict__ xv,
+                                                           const float* __restrict__ scale,
+                                                           const void* __restrict__ dyv,
+                                                           void* __restrict__ dxv,
+                                                           float* __restrict__ part, int M, int C,
+                                                           float eps) {
+    using E = typename TR::elem;
+    const E* x = static_cast<const E*>(xv);
+    const E* dy = static_cast<const E*>(dyv);
+    E* dx = static_cast<E*>(dxv);
+    const int lane = threadIdx.x % 64;
+    const int wave = threadIdx.x / 64;
+    constexpr int waves = kThreads / 64;
+    // Per-wave column partials live in part as scratch rows [block][wave][2][C] -> reduced below.
+    float* wpart = part + ((size_t)blockIdx.x * (waves + 1) + 1 + wave) * 2 * C;
+    for (int c = lane; c < C; c += 64) {
+        wpart[c] = 0.f;
+        wpart[C + c] = 0.f;
+    }
+    for (int row = blockIdx.x * waves + wave; row < M; row += gridDim.x * waves) {
+        const size_t base = (size_t)row * C;
+        float sum = 0.f;
+        for (int c = lane; c < C; c += 64) sum += TR::to_f(x[base + c]);
+        const float mean = row_sum<64>(sum) / C;
+        float m2 = 0.f;
+        for (int c = lane; c < C; c += 64) {
+            const float d = TR::to_f(x[base + c]) - mean;
+            m2 += d * d;
+        }
+        const float rstd = rsqrtf(row_sum<64>(m2) / C + eps);
+        float sg = 0.f, sgx = 0.f;
+        for (int c = lane; c < C; c += 64) {
+            const float xh = (TR::to_f(x[base + c]) - mean) * rstd;
+            const float d = TR::to_f(dy[base + c]);
+            sg += scale[c] * d;
+            sgx += scale[c] * d * xh;
+            wpart[c] += d * xh;
+            wpart[C + c] += d;
+        }
+        sg = row_sum<64>(sg) / C;
+        sgx = row_sum<64>(sgx) / C;
+        for (int c = lane; c < C; c += 64) {
+            const float xh = (TR::to_f(x[base + c]) - mean) * rstd;
+            const float d = TR::to_f(dy[base + c]);
+            dx[base + c] = TR::from_f(rstd * (scale[c] * d - sg - xh * sgx));
+        }
+    }
+    __syncthreads();
+    float* bpart = part + (size_t)blockIdx.x * (waves + 1) * 2 * C;
+    for (int t = threadIdx.x; t < 2 * C; t += kThreads) {
+        float a = 0.f;
+        for (int w = 0; w < waves; ++w)
+            a += part[((size_t)blockIdx.x * (waves + 1) + 1 + w) * 2 * C + t];
+        bpart[t] = a;
+    }
+}
+
+// out[which][c] = sum over blocks b (in order) of part[b*stride + which*C + c].
+__global__ __launch_bounds__(kThreads) void ln_colsum(const float* __restrict__ part,
+                                                      size_t stride, int nblocks, int C,
+                                                      float* __restrict__ dscale,
+                                                      float* __restrict__ doffset) {
+    constexpr int kCols = 64, kSplit = kThreads / kCols;
+    __shared__ float red[kSplit][kCols];
+    const int cl = threadIdx.x % kCols, sp = threadIdx.x / kCols;
+    const int t = blockIdx.x * kCols + cl;  // over 2*C outputs
+    float a = 0.f;
+    if (t < 2 * C) {
+        for (int b = sp; b < nblocks; b += kSplit) a += part[(size_t)b * stride + t];
+    }
+    red[sp][cl] = a;
+    __syncthreads();
+    if (sp == 0 && t < 2 * C) {
+        float r = 0.f;
+        for (int i = 0; i < kSplit; ++i) r += red[i][cl];
+        if (t < C) dscale[t] = r;
+        else doffset[t - C] = r;
+    }
+}
+
+// (LPR, NV) for a row of C elements of VEC per 16-byte vector; {0,0} when no fast kernel fits.
+struct RowShape {
+    int lpr, nv;
+};
+RowShape row_shape(int64_t C, int vec) {
+    if (C <= 0 || C % vec != 0) return {0, 0};
+    const int64_t nvec = C / vec;
+    int lpr = 1;
+    while (lpr < 64 && nvec % (lpr * 2) == 0) lpr *= 2;
+    const int64_t nv = nvec / lpr;
+    if (lpr < 4 || nv > 4) return {0, 0};
+    return {lpr, (int)nv};
+}
+
+constexpr int kMaxBwdBlocks = 1024;
+
+int fwd_blocks(int64_t M, int rows_per_block) {
+    const int64_t b = (M + rows_per_block - 1) / rows_per_block;
+    return (int)(b < 4096 ? b : 4096);
+}
+int bwd_blocks(int64_t M, int rows_per_block) {
+    const int64_t b = (M + rows_per_block - 1) / rows_per_block;
+    return (int)(b < kMaxBwdBlocks ? b : kMaxBwdBlocks);
+}
+
+template <typename TR, int LPR, int NV>
+void launch_fwd(hipStream_t st, const void* x, const float* sc, const float* of, void* y, int M,
+                float eps) {
+    const int grid = fwd_blocks(M, kThreads / LPR);
+    ln_fwd_kernel<TR, LPR, NV><<<grid, kThreads, 0, st>>>(x, sc, of, y, M, eps);
+}
+
+template <typename TR>
+bool dispatch_fwd(hipStream_t st, const void* x, const float* sc, const float* of, void* y,
+                  int M, int C, float eps) {
+    const RowShape rs = row_shape(C, Vec<TR>::N);
+#define CLK_LN_CASE(L, V)                                        \
+    if (rs.lpr == (L) && rs.nv == (V)) {                         \
+        launch_fwd<TR, L, V>(st, x, sc, of, y, M, eps);          \
+        return true;                                             \
+    }
+#define CLK_LN_ROW(L) CLK_LN_CASE(L, 1) CLK_LN_CASE(L, 2) CLK_LN_CASE(L, 3) CLK_LN_CASE(L, 4)
+    CLK_LN_ROW(4) CLK_LN_ROW(8) CLK_LN_ROW(16) CLK_LN_ROW(32) CLK_LN_ROW(64)
+#undef CLK_LN_ROW
+#undef CLK_LN_CASE
+    const int grid = fwd_blocks(M, kThreads / 64);
+    ln_fwd_generic<TR><<<grid, kThreads, 0, st>>>(x, sc, of, y, M, C, eps);
+    return false;
+}
+
+template <typename TR, int LPR, int NV>
+void launch_bwd(hipStream_t st, const void* x, const float* sc, const void* dy, void* dx,
+                float* part, int M, float eps) {
+    const int grid = bwd_blocks(M, kThreads / LPR);
+    ln_bwd_kernel<TR, LPR, NV><<<grid, kThreads, 0, st>>>(x, sc, dy, dx, part, M, eps);
+}
+
+// Returns the number of partial rows written and their stride (floats).
+template <typename TR>
+void dispatch_bwd(hipStream_t st, const void* x, const float* sc, const void* dy, void* dx,
+                  float* part, int M, int C, float eps, int* nblocks, size_t* stride) {
+    const RowShape rs = row_shape(C, Vec<TR>::N);
+#define CLK_LN_CASE(L, V)                                          \
+    if (rs.lpr == (L) && rs.nv == (V)) {                           \
+        launch_bwd<TR, L, V>(st, x, sc, dy, dx, part, M, eps);     \
+        *nblocks = bwd_blocks(M, kThreads / (L));                  \
+        *stride = 2 * (size_t)C;                                   \
+        return;                                                    \
+    }
+#define CLK_LN_ROW(L) CLK_LN_CASE(L, 1) CLK_LN_CASE(L, 2) CLK_LN_CASE(L, 3) CLK_LN_CASE(L, 4)
+    CLK_LN_ROW(4) CLK_LN_ROW(8) CLK_LN_ROW(16) CLK_LN_ROW(32) CLK_LN_ROW(64)
+#undef CLK_LN_ROW
+#undef CLK_LN_CASE
+    const int grid = bwd_blocks(M, kThreads / 64);
+    ln_bwd_generic<TR><<<grid, kThreads, 0, st>>>(x, sc, dy, dx, part, M, C, eps);
+    *nblocks = grid;
+    *stride = (size_t)(kThreads / 64 + 1) * 2 * C;
+}
+
+size_t bwd_workspace(int64_t M, int64_t C) {
+    // Generic path needs (waves + 1) * 2 * C floats per block; the fast path 2 * C.
+    const int64_t blocks = bwd_blocks(M, kThreads / 64);
+    return (size_t)blocks * (kThreads / 64 + 1) * 2 * C * sizeof(float);
+}
+
+clk_status validate(const char* who, clk_dtype dtype, const void* x, const float* scale,
+                    const void* y, int64_t M, int64_t C) {
+    if (dtype != CLK_F16 && dtype != CLK_BF16 && dtype != CLK_F32)
+        return fail(CLK_INVALID_ARGUMENT, "%s: dtype %s not supported (f16, bf16, f32)", who,
+                    dtype_name(dtype));
+    if (M < 0 || C <= 0) return fail(CLK_INVALID_ARGUMENT, "%s: x must be [M,C] with C > 0", who);
+    if (M > INT32_MAX || C > (1 << 20) || M * C > ((int64_t)1 << 40))
+        return fail(CLK_INVALID_ARGUMENT, "%s: [M,C] = [%lld,%lld] too large", who,
+                    (long long)M, (long long)C);
+    if (M > 0 && (!x || !scale || !y))
+        return fail(CLK_INVALID_ARGUMENT, "%s: null pointer", who);
+    if (M > 0 && (!aligned16(x) || !aligned16(y)))
+        return fail(CLK_INVALID_ARGUMENT, "%s: x and y must be 16-byte aligned", who);
+    return CLK_OK;
+}
+
+}  // namespace
+}  // namespace clk
+
+using namespace clk;
+
+extern "C" clk_status clk_layer_norm_fwd(hipStream_t stream, clk_dtype dtype, const void* x,
+                                         const float* scale, const float* offset, void* y,
+                                         int64_t M, int64_t C, float eps) {
+    clk_status s = validate("layer_norm", dtype, x, scale, y, M, C);
+    if (s != CLK_OK) return s;
+    if (M > 0 && !offset) return fail(CLK_INVALID_ARGUMENT, "layer_norm: null offset");
+    if (M == 0) return ok();
+    switch (dtype) {
+        case CLK_BF16: dispatch_fwd<BF16>(stream, x, scale, offset, y, (int)M, (int)C, eps); break;
+        case CLK_F16: dispatch_fwd<F16>(stream, x, scale, offset, y, (int)M, (int)C, eps); break;
+        default: dispatch_fwd<F32>(stream, x, scale, offset, y, (int)M, (int)C, eps); break;
+    }
+    return check_launch("layer_norm");
+}
+
+extern "C" size_t clk_layer_norm_bwd_workspace_size(int64_t M, int64_t C) {
+    if (M <= 0 || C <= 0) return 0;
+    return bwd_workspace(M, C);
+}
+
+extern "C" clk_status clk_layer_norm_bwd(hipStream_t stream, clk_dtype dtype, const void* x,
+                                         const float* scale, const void* dy, void* dx,
+                                         float* dscale, float* doffset, void* workspace,
+                                         size_t workspace_bytes, int64_t M, int64_t C,
+                                         float eps) {
+    clk_status s = validate("layer_norm_bwd", dtype, x, scale, dx, M, C);
+    if (s != CLK_OK) return s;
+    if (M > 0 && (!dy || !dscale || !doffset || !workspace))
+        return fail(CLK_INVALID_ARGUMENT, "layer_norm_bwd: null pointer");
+    if (M > 0 && !aligned16(dy))
+        return fail(CLK_INVALID_ARGUMENT, "layer_norm_bwd: dy must be 16-byte aligned");
+    const size_t need = clk_layer_norm_bwd_workspace_size(M, C);
+    if (workspace_bytes < need)
+        return fail(CLK_INVALID_ARGUMENT, "layer_norm_bwd: workspace %zu bytes, needs %zu",
+                    workspace_bytes, need);
+    if (M == 0) {
+        if (!dscale || !doffset) return fail(CLK_INVALID_ARGUMENT, "layer_norm_bwd: null pointer");
+        // No rows: the column sums are zero (a fill kernel, so the call stays graph-capturable).
+        ln_colsum<<<ceil_div(2 * C, 64), kThreads, 0, stream>>>(nullptr, 0, 0, (int)C, dscale,
+                                                               doffset);
+        return check_launch("layer_norm_bwd");
+    }
+    float* part = static_cast<float*>(workspace);
+    int nblocks = 0;
+    size_t stride = 0;
+    switch (dtype) {
+        case CLK_BF16:
+            dispatch_bwd<BF16>(stream, x, scale, dy, dx, part, (int)M, (int)C, eps, &nblocks,
+                               &stride);
+            break;
+        case CLK_F16:
+            dispatch_bwd<F16>(stream, x, scale, dy, dx, part, (int)M, (int)C, eps, &nblocks,
+                              &stride);
+            break;
+        default:
+            dispatch_bwd<F32>(stream, x, scale, dy, dx, part, (int)M, (int)C, eps, &nblocks,
+                              &stride);
+            break;
+    }
+    ln_colsum<<<ceil_div(2 * C, 64), kThreads, 0, stream>>>(part, stride, nblocks, (int)C, dscale,
+                                                           doffset);
+    return check_launch("layer_norm_bwd");
+}

@@ -1,0 +1,133 @@
+/*
+ * clk.h -- C ABI of the gfx950 Evoformer kernels (attention with pair bias, LayerNorm,
+ * gated dual projection).
+ *
+ * Every entry point takes raw device pointers, sizes and a HIP stream, launches its kernels on
+ * that stream in order and returns without synchronising. Nothing is allocated, retained or
+ * freed: the caller owns every buffer, including the workspace of the backward passes. A
+ * non-OK status leaves a message in clk_last_error() (thread-local). Validation of every shape,
+ * dtype and pointer runs on the host before any HIP call, so an invalid call never launches.
+ *
+ * Status and dtype codes use the XLA FFI numbering (XLA_FFI_Error_Code, XLA_FFI_DataType), so
+ * the XLA FFI handlers pass them through unchanged.
+ *
+ * Layouts (all row-major, contiguous):
+ *   attention  q, out [N,H,Sq,D]; k, v [N,H,Sk,D]; bias [H,Sq,Sk] shared by the N rows;
+ *              kmask [N,Sk] uint8 (0 = key absent); lse [N,H,Sq] float32 (natural log)
+ *   layer norm x, y [M,C]; scale, offset [C] float32
+ *   gdp        x [M,K]; wp, wg [K,N]; bp, bg [N]; mask [M]; out [M,N]
+ */
+#ifndef CLK_H_
+#define CLK_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* hipStream_t;
+
+typedef enum clk_status {
+    CLK_OK = 0,
+    CLK_INVALID_ARGUMENT = 3,
+    CLK_UNIMPLEMENTED = 12,
+    CLK_INTERNAL = 13,
+} clk_status;
+
+typedef enum clk_dtype {
+    CLK_U8 = 6,
+    CLK_F16 = 10,
+    CLK_F32 = 11,
+    CLK_BF16 = 16,
+} clk_dtype;
+
+/* Message of the last non-OK status returned on this thread ("" if none). */
+const char* clk_last_error(void);
+
+/* Library version string. */
+const char* clk_version(void);
+
+/*
+ * Attention forward: out = softmax(scale * q.k^T + bias, masked keys at logit -1e9) . v.
+ * Replaces VoltaMma (cuda/volta_mma_attn.cu:304-351) and VoltaWmma (cuda/volta_wmma_attn.cu:
+ * 264-311): same operands, same attributes (scale, block_q, block_k). dtype is CLK_F16 or
+ * CLK_BF16 for q, k, v, bias and out. D is 8, 16, 32 or 64. block_q and block_k are hints: any
+ * value the reference dispatch accepts is accepted, and other positive values too.
+ * kmask may be NULL (every key present). lse may be NULL (inference); when given, the natural-log
+ * logsumexp of every query row is written for clk_attention_bwd.
+ */
+clk_status clk_attention_fwd(hipStream_t stream, clk_dtype dtype, const void* q, const void* k,
+                             const void* v, const void* bias, const uint8_t* kmask, void* out,
+                             float* lse, int64_t N, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
+                             float scale, int64_t block_q, int64_t block_k);
+
+/* Bytes of device workspace clk_attention_bwd needs for these sizes. */
+size_t clk_attention_bwd_workspace_size(int64_t N, int64_t H, int64_t Sq, int64_t Sk, int64_t D);
+
+/*
+ * Attention backward. No reference counterpart (the reference is forward-only); it is the
+ * gradient of clk_attention_fwd's math with the additive-mask convention: dS = P*(dP - D) at
+ * every key, masked ones included. Inputs q, k, v, bias, kmask as in the forward, plus out and
+ * lse from it and dout. Outputs dq, dk, dv (dtype) and dbias [H,Sq,Sk] float32 = sum over the N
+ * rows of dS. Deterministic: fixed-order reductions, no floating-point atomics, so repeated
+ * calls give identical bits. workspace must hold clk_attention_bwd_workspace_size() bytes,
+ * 256-byte aligned.
+ */
+clk_status clk_attention_bwd(hipStream_t stream, clk_dtype dtype, const void* q, const void* k,
+                             const void* v, const void* bias, const uint8_t* kmask,
+                             const void* out, const void* dout, const float* lse, void* dq,
+                             void* dk, void* dv, float* dbias, void* workspace,
+                             size_t workspace_bytes, int64_t N, int64_t H, int64_t Sq, int64_t Sk,
+                             int64_t D, float scale);
+
+/*
+ * LayerNorm forward over the last axis. Replaces VoltaLayerNorm (cuda/volta_ops.cu:62-95):
+ * x and y of dtype CLK_F16, CLK_BF16 or CLK_F32; scale and offset float32; attribute eps.
+ */
+clk_status clk_layer_norm_fwd(hipStream_t stream, clk_dtype dtype, const void* x,
+                              const float* scale, const float* offset, void* y, int64_t M,
+                              int64_t C, float eps);
+
+/* Bytes of device workspace clk_layer_norm_bwd needs for these sizes. */
+size_t clk_layer_norm_bwd_workspace_size(int64_t M, int64_t C);
+
+/*
+ * LayerNorm backward. No reference counterpart. Statistics are recomputed from x. Outputs
+ * dx (dtype) and dscale, doffset [C] float32 (deterministic two-stage column sums).
+ */
+clk_status clk_layer_norm_bwd(hipStream_t stream, clk_dtype dtype, const void* x,
+                              const float* scale, const void* dy, void* dx, float* dscale,
+                              float* doffset, void* workspace, size_t workspace_bytes, int64_t M,
+                              int64_t C, float eps);
+
+/*
+ * Gated dual projection: out = mask[m] * (x.wp + bp) * sigmoid(x.wg + bg).
+ * Replaces VoltaGdp (cuda/volta_ops.cu:210-265) and VoltaGdpWmma (cuda/volta_gdp_wmma.cu:
+ * 99-140): the same six operands and result, all of dtype CLK_F16 or CLK_BF16. N must be a
+ * multiple of 8 (volta_ops.cu:234-236); K a multiple of 8, at most 512.
+ */
+clk_status clk_gated_dual_proj(hipStream_t stream, clk_dtype dtype, const void* x,
+                               const void* wp, const void* bp, const void* wg, const void* bg,
+                               const void* mask, void* out, int64_t M, int64_t K, int64_t N);
+
+/*
+ * LayerNorm fused with both gated-projection branches of the triangle multiplication:
+ *   y = LN(z); a = mask*(y.wpa+bpa)*sigmoid(y.wga+bga); b = likewise with the b weights.
+ * One pass over z instead of VoltaLayerNorm followed by two VoltaGdp calls. z, weights, biases,
+ * mask, a and b of dtype CLK_F16 or CLK_BF16; ln_scale, ln_offset float32. C and N must be
+ * multiples of 32, at most 128 each.
+ */
+clk_status clk_ln_gated_dual_proj(hipStream_t stream, clk_dtype dtype, const void* z,
+                                  const float* ln_scale, const float* ln_offset, const void* wpa,
+                                  const void* bpa, const void* wga, const void* bga,
+                                  const void* wpb, const void* bpb, const void* wgb,
+                                  const void* bgb, const void* mask, void* a, void* b, int64_t M,
+                                  int64_t C, int64_t N, float eps);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* CLK_H_ */

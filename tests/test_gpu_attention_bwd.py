@@ -1,0 +1,125 @@
+"""Attention backward on the GPU against the float64 oracle (through the C ABI)."""
+import numpy as np
+import pytest
+import torch
+
+from _util import TOL, assert_close, dname, np64
+from colabfold_legacy_kernels import ops
+from colabfold_legacy_kernels.workloads import attention_inputs, attention_workload
+from oracle import attention as ref
+
+pytestmark = pytest.mark.gpu
+
+# (N, H, Sq, Sk, D, masked_tail, masked_rows)
+CASES = [
+    (2, 2, 64, 64, 32, 0.0, 0),
+    (3, 2, 100, 77, 32, 0.1, 1),
+    (2, 1, 130, 200, 64, 0.2, 0),
+    (2, 4, 64, 64, 16, 0.0, 1),
+    (2, 2, 48, 40, 8, 0.1, 0),
+    (1, 1, 1, 1, 32, 0.0, 0),
+    (5, 3, 257, 129, 32, 0.05, 2),
+    (2, 2, 33, 300, 64, 0.0, 0),
+    (4, 2, 96, 600, 32, 0.1, 1),   # Sk > 512: two key ranges, dQ partials
+]
+
+
+def _run(inp, dev):
+    g = {k: (v.to(dev) if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    out, lse = ops.attention_fwd(g["q"], g["k"], g["v"], g["bias"], g["kmask"], g["scale"])
+    grads = ops.attention_bwd(g["q"], g["k"], g["v"], g["bias"], g["kmask"], out, g["dout"], lse,
+                              g["scale"])
+    return g, out, lse, grads
+
+
+def _oracle(inp, rows=None):
+    sel = slice(None) if rows is None else rows
+    return ref.attention_bwd(np64(inp["q"][sel]), np64(inp["k"][sel]), np64(inp["v"][sel]),
+                             np64(inp["bias"]), inp["kmask"][sel].cpu().numpy(), inp["scale"],
+                             np64(inp["dout"][sel]))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=dname)
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(map(str, c[:5])))
+def test_attention_bwd_parity(cuda, case, dtype):
+    n, h, sq, sk, d, tail, rows = case
+    inp = attention_inputs(n, h, sq, sk, d, dtype, seed=sq * 13 + sk, masked_tail=tail,
+                           masked_rows=rows)
+    _, _, _, (dq, dk, dv, dbias) = _run(inp, cuda)
+    rq, rk, rv, rb = _oracle(inp)
+    tol = TOL[dname(dtype)]["grad"]
+    assert_close("dQ", dq, rq, tol)
+    assert_close("dK", dk, rk, tol)
+    assert_close("dV", dv, rv, tol)
+    assert_close("dBias", dbias, rb, tol)
+
+
+def test_attention_bwd_deterministic(cuda):
+    inp = attention_inputs(6, 4, 200, 200, 32, torch.bfloat16, seed=21, masked_tail=0.1,
+                           masked_rows=1)
+    g, out, lse, first = _run(inp, cuda)
+    for _ in range(2):
+        again = ops.attention_bwd(g["q"], g["k"], g["v"], g["bias"], g["kmask"], out, g["dout"],
+                                  lse, g["scale"])
+        for a, b in zip(first, again):
+            assert torch.equal(a, b)
+
+
+def test_attention_bwd_empty_axes(cuda):
+    dt = torch.bfloat16
+    for n, h, sq, sk in [(0, 2, 16, 16), (2, 2, 16, 0), (2, 2, 0, 16)]:
+        q = torch.randn((n, h, sq, 32), device=cuda).to(dt)
+        k = torch.randn((n, h, sk, 32), device=cuda).to(dt)
+        bias = torch.randn((h, sq, sk), device=cuda).to(dt)
+        km = torch.ones((n, sk), device=cuda, dtype=torch.uint8)
+        lse = torch.zeros((n, h, sq), device=cuda)
+        dq, dk, dv, db = ops.attention_bwd(q, k, k, bias, km, q, q, lse)
+        for t in (dq, dk, dv, db):
+            assert torch.count_nonzero(t).item() == 0
+
+
+def test_attention_bwd_full_triangle_256(cuda):
+    """The 256-residue triangle attention: every gradient against the full float64 oracle."""
+    inp = attention_workload("triangle_attn_256", torch.bfloat16, device=cuda)
+    _, _, _, (dq, dk, dv, dbias) = _run(inp, cuda)
+    cpu = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    rq, rk, rv, rb = _oracle(cpu)
+    tol = TOL["bf16"]["grad"]
+    assert_close("dQ", dq, rq, tol)
+    assert_close("dK", dk, rk, tol)
+    assert_close("dV", dv, rv, tol)
+    assert_close("dBias", dbias, rb, tol)
+
+
+@pytest.mark.parametrize("name", ["triangle_attn_384", "msa_row_attn"])
+def test_attention_bwd_full_size_properties(cuda, name):
+    """Full workloads: sampled rows of dQ/dK/dV against the oracle (they depend on their own row
+    only); sum_k dBias[h,q,k] = 0 (rows of dS sum to zero); bit-identical repeat."""
+    inp = attention_workload(name, torch.bfloat16, device=cuda)
+    g, out, lse, (dq, dk, dv, dbias) = _run(inp, cuda)
+    n = inp["q"].shape[0]
+    rows = sorted({0, n // 3, n - 1})
+    cpu = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    rq, rk, rv, _ = _oracle(cpu, rows)
+    tol = TOL["bf16"]["grad"]
+    assert_close("dQ[rows]", dq[rows], rq, tol)
+    assert_close("dK[rows]", dk[rows], rk, tol)
+    assert_close("dV[rows]", dv[rows], rv, tol)
+    row_sum = dbias.double().sum(dim=-1).abs().max().item()
+    assert row_sum <= 2e-2 * dbias.double().abs().sum(dim=-1).max().item()
+    again = ops.attention_bwd(g["q"], g["k"], g["v"], g["bias"], g["kmask"], out, g["dout"], lse,
+                              g["scale"])
+    assert torch.equal(dbias, again[3]) and torch.equal(dq, again[0])
+
+
+def test_attention_autograd_function(cuda):
+    inp = attention_inputs(2, 2, 64, 64, 32, torch.bfloat16, seed=4, masked_tail=0.1)
+    g = {k: (v.to(cuda) if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    q, k, v, b = (g[x].clone().requires_grad_(True) for x in ("q", "k", "v", "bias"))
+    out = ops.AttentionFunction.apply(q, k, v, b, g["kmask"], g["scale"])
+    out.backward(g["dout"])
+    rq, rk, rv, rb = _oracle(inp)
+    tol = TOL["bf16"]["grad"]
+    assert_close("q.grad", q.grad, rq, tol)
+    assert_close("bias.grad", b.grad.float(), rb, tol)
+    _ = np

@@ -1,0 +1,107 @@
+"""Attention forward on the GPU against the float64 oracle (through the C ABI)."""
+import numpy as np
+import pytest
+import torch
+
+from _util import TOL, assert_close, dname, np64
+from colabfold_legacy_kernels import ops
+from colabfold_legacy_kernels.workloads import attention_inputs, attention_workload
+from oracle import attention as ref
+
+pytestmark = pytest.mark.gpu
+
+# (N, H, Sq, Sk, D, masked_tail, masked_rows): aligned, ragged, every head dim, masks.
+CASES = [
+    (2, 2, 64, 64, 32, 0.0, 0),
+    (3, 2, 100, 77, 32, 0.1, 1),
+    (2, 1, 130, 200, 64, 0.2, 0),
+    (2, 4, 64, 64, 16, 0.0, 1),
+    (2, 2, 48, 40, 8, 0.1, 0),
+    (1, 1, 1, 1, 32, 0.0, 0),
+    (2, 3, 257, 129, 32, 0.05, 1),
+    (2, 2, 33, 300, 64, 0.0, 0),
+]
+
+
+def _oracle(inp, rows=None):
+    sel = slice(None) if rows is None else rows
+    return ref.attention_fwd(np64(inp["q"][sel]), np64(inp["k"][sel]), np64(inp["v"][sel]),
+                             np64(inp["bias"]), inp["kmask"][sel].cpu().numpy(), inp["scale"])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=dname)
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(map(str, c[:5])))
+def test_attention_fwd_parity(cuda, case, dtype):
+    n, h, sq, sk, d, tail, rows = case
+    inp = attention_inputs(n, h, sq, sk, d, dtype, seed=sq * 7 + sk, bias_var=1.0,
+                           masked_tail=tail, masked_rows=rows, with_dout=False)
+    g = {k: (v.to(cuda) if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    out, lse = ops.attention_fwd(g["q"], g["k"], g["v"], g["bias"], g["kmask"], g["scale"])
+    o_ref, lse_ref = _oracle(inp)
+    tol = TOL[dname(dtype)]["o"]
+    assert_close("O", out, o_ref, tol)
+    # lse is float32 from float32 logits: absolute error on the logit scale. A row with no
+    # present key reports ln(Sk) (relative to its masked logit); the oracle's value is
+    # -1e9 + ln(Sk), which float32 cannot hold.
+    empty = (inp["kmask"].numpy() == 0).all(axis=1)[:, None, None]
+    lse_ref = np.where(empty, np.log(sk), lse_ref)
+    assert np.abs(np64(lse) - lse_ref).max() < 5e-2
+    # The inference entry (VoltaMma contract) gives the same bits as the training entry.
+    out2 = ops.attention(g["q"], g["k"], g["v"], g["bias"], g["kmask"], g["scale"], 64, 64)
+    assert torch.equal(out, out2)
+
+
+def test_attention_fwd_no_mask_is_all_present(cuda):
+    inp = attention_inputs(2, 2, 64, 96, 32, torch.bfloat16, seed=5, with_dout=False)
+    g = {k: (v.to(cuda) if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    a = ops.attention(g["q"], g["k"], g["v"], g["bias"], None, g["scale"])
+    b = ops.attention(g["q"], g["k"], g["v"], g["bias"], torch.ones_like(g["kmask"]), g["scale"])
+    assert torch.equal(a, b)
+
+
+def test_attention_fwd_fully_masked_row_is_mean_v(cuda):
+    """jnp's float32 additive mask: a row with every key masked attends uniformly over its Sk
+    keys (not over tile padding), so O = mean(V)."""
+    inp = attention_inputs(2, 2, 40, 70, 32, torch.bfloat16, seed=9, with_dout=False)
+    inp["kmask"][1] = 0
+    g = {k: (v.to(cuda) if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    out = ops.attention(g["q"], g["k"], g["v"], g["bias"], g["kmask"], g["scale"])
+    mean_v = np64(inp["v"][1]).mean(axis=1, keepdims=True).repeat(40, axis=1)
+    assert_close("O[masked]", out[1], mean_v, TOL["bf16"]["o"])
+
+
+@pytest.mark.parametrize("block", [(64, 64), (64, 32), (32, 32), (128, 64), (32, 64), (16, 64),
+                                   (128, 32), (7, 5)])
+def test_attention_fwd_accepts_reference_block_hints(cuda, block):
+    inp = attention_inputs(1, 2, 64, 64, 32, torch.float16, seed=3, with_dout=False)
+    g = {k: (v.to(cuda) if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    base = ops.attention(g["q"], g["k"], g["v"], g["bias"], g["kmask"], g["scale"])
+    out = ops.attention(g["q"], g["k"], g["v"], g["bias"], g["kmask"], g["scale"], *block)
+    assert torch.equal(base, out)
+
+
+@pytest.mark.parametrize("name", ["triangle_attn_256", "triangle_attn_384", "msa_row_attn",
+                                  "triangle_attn_1024"])
+def test_attention_fwd_full_size_rows(cuda, name):
+    """Full workload on the GPU; sampled rows n against the oracle (rows are independent)."""
+    inp = attention_workload(name, torch.bfloat16, device=cuda, with_dout=False)
+    out, lse = ops.attention_fwd(inp["q"], inp["k"], inp["v"], inp["bias"], inp["kmask"],
+                                 inp["scale"])
+    n = inp["q"].shape[0]
+    rows = sorted({0, 1, n // 2, n - 1})
+    cpu = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    o_ref, _ = _oracle(cpu, rows)
+    assert_close("O[rows]", out[rows], o_ref, TOL["bf16"]["o"])
+    assert torch.isfinite(lse).all()
+
+
+def test_attention_rejects_bad_operands(cuda):
+    inp = attention_inputs(1, 2, 16, 16, 32, torch.bfloat16, seed=1, with_dout=False)
+    g = {k: (v.to(cuda) if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    with pytest.raises(ops.InvalidArgument):
+        ops.attention(g["q"], g["k"], g["v"], g["bias"][:, :8], g["kmask"])
+    q24 = torch.zeros((1, 2, 16, 24), device=cuda, dtype=torch.bfloat16)
+    with pytest.raises(ops.InvalidArgument):
+        ops.attention(q24, q24, q24, g["bias"], g["kmask"])
+    with pytest.raises(ops.InvalidArgument):
+        ops.attention(g["q"], g["k"], g["v"], g["bias"], g["kmask"], None, 0, 64)
