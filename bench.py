@@ -1,0 +1,281 @@
+"""Benchmark of the Evoformer hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+Headline (one JSON line on stdout): triangle attention forward + backward at N_res = 384
+(q, k, v [384 rows, 4 heads, 384 residues, 32], bf16 in, float32 accumulate), in TFLOP/s of
+algorithmic work 12*N*H*Sq*Sk*D per step. A step is one forward and one backward over the whole
+batch, through the C ABI with preallocated buffers; inputs rotate over 3 sets (~0.9 GB) so the
+256 MB Infinity Cache cannot hold them. Secondary figures: LayerNorm forward/backward and
+LayerNorm + gated dual projection on the 512x512x128 pair representation, in HBM GB/s.
+
+The roofline block names the kernel with the most time per step, its algorithmic work per launch
+divided by its average duration from per-launch HIP events on the launch stream (the library's
+clk_profile_* hooks), against MI355X's dense bf16 MFMA peak (2516.6 TFLOP/s) or HBM (8 TB/s).
+cpu_baseline times the same math in torch float32 on the host cores (oracle/cpu_baseline.py) on
+a bounded sample of rows, scaled to the same unit.
+"""
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT / "colabfold-legacy-kernels_amd", ROOT):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "attn fwd+bwd TFLOP/s (% bf16 MFMA peak) at N_res=384; LN/GDP HBM GB/s"
+MFMA_PEAK_BF16 = 2516.6  # TFLOP/s, dense
+HBM_PEAK = 8000.0        # GB/s
+
+N_ROWS, HEADS, NRES, HEAD_DIM = 384, 4, 384, 32
+ROTATE = 3
+
+
+def _cores():
+    try:
+        return len(os.sched_getaffinity(0))
+    except AttributeError:
+        return os.cpu_count() or 1
+
+
+def attention_flops(n, h, sq, sk, d):
+    fwd = 4.0 * n * h * sq * sk * d
+    return {"fwd": fwd, "bwd": 2.0 * fwd, "step": 3.0 * fwd,
+            # per kernel: the products whose results the kernel owns (recomputes excluded)
+            "attn_fwd": fwd, "attn_bwd_dkv": 1.5 * fwd, "attn_bwd_dq": 0.5 * fwd}
+
+
+class AttentionSet:
+    """One rotating set of inputs and preallocated outputs for the C ABI."""
+
+    def __init__(self, torch, workloads, native, dev, seed):
+        inp = workloads.attention_inputs(N_ROWS, HEADS, NRES, NRES, HEAD_DIM, torch.bfloat16,
+                                         seed=seed, device=dev, masked_tail=0.10)
+        self.__dict__.update(inp)
+        self.out = torch.empty_like(self.q)
+        self.lse = torch.empty((N_ROWS, HEADS, NRES), device=dev, dtype=torch.float32)
+        self.dq = torch.empty_like(self.q)
+        self.dk = torch.empty_like(self.k)
+        self.dv = torch.empty_like(self.v)
+        self.dbias = torch.empty((HEADS, NRES, NRES), device=dev, dtype=torch.float32)
+        lib = native.lib()
+        self.ws_bytes = lib.clk_attention_bwd_workspace_size(N_ROWS, HEADS, NRES, NRES, HEAD_DIM)
+        self.ws = torch.empty(max(self.ws_bytes, 1), device=dev, dtype=torch.uint8)
+
+
+def attention_step(lib, native, stream, s):
+    dims = (N_ROWS, HEADS, NRES, NRES, HEAD_DIM)
+    st = lib.clk_attention_fwd(stream, native.BF16, s.q.data_ptr(), s.k.data_ptr(),
+                               s.v.data_ptr(), s.bias.data_ptr(), s.kmask.data_ptr(),
+                               s.out.data_ptr(), s.lse.data_ptr(), *dims, s.scale, 64, 64)
+    if st != 0:
+        raise RuntimeError(native.last_error())
+    st = lib.clk_attention_bwd(stream, native.BF16, s.q.data_ptr(), s.k.data_ptr(),
+                               s.v.data_ptr(), s.bias.data_ptr(), s.kmask.data_ptr(),
+                               s.out.data_ptr(), s.dout.data_ptr(), s.lse.data_ptr(),
+                               s.dq.data_ptr(), s.dk.data_ptr(), s.dv.data_ptr(),
+                               s.dbias.data_ptr(), s.ws.data_ptr(), s.ws_bytes, *dims, s.scale)
+    if st != 0:
+        raise RuntimeError(native.last_error())
+
+
+def timed(torch, fn, steps, warmup, stream_obj):
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    a = torch.cuda.Event(enable_timing=True)
+    b = torch.cuda.Event(enable_timing=True)
+    a.record(stream_obj)
+    for i in range(steps):
+        fn(i)
+    b.record(stream_obj)
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / steps
+
+
+def per_kernel(torch, native, fn, steps):
+    """Average ms per launch of each kernel, from the library's per-launch HIP events."""
+    torch.cuda.synchronize()
+    with native.profile() as prof:
+        for i in range(steps):
+            fn(i)
+    torch.cuda.synchronize()
+    agg = {}
+    for name, ms in prof.records:
+        tot, cnt = agg.get(name, (0.0, 0))
+        agg[name] = (tot + ms, cnt + 1)
+    return {k: {"avg_ms": t / c, "launches_per_step": c / steps} for k, (t, c) in agg.items()}
+
+
+def bench_layer_norm(torch, workloads, native, dev, stream, steps, warmup):
+    """LayerNorm fwd and bwd on [512*512, 128] bf16; rotates 4 sets (> 512 MB)."""
+    m, c = 512 * 512, 128
+    lib = native.lib()
+    sets = []
+    for r in range(4):
+        li = workloads.layer_norm_inputs(m, c, torch.bfloat16, seed=3 + r, device=dev)
+        li["y"] = torch.empty_like(li["x"])
+        li["dx"] = torch.empty_like(li["x"])
+        li["ds"] = torch.empty(c, device=dev)
+        li["do"] = torch.empty(c, device=dev)
+        wsb = lib.clk_layer_norm_bwd_workspace_size(m, c)
+        li["ws"] = torch.empty(wsb, device=dev, dtype=torch.uint8)
+        li["wsb"] = wsb
+        sets.append(li)
+
+    def fwd(i):
+        s = sets[i % len(sets)]
+        lib.clk_layer_norm_fwd(stream, native.BF16, s["x"].data_ptr(), s["scale"].data_ptr(),
+                               s["offset"].data_ptr(), s["y"].data_ptr(), m, c, 1e-5)
+
+    def bwd(i):
+        s = sets[i % len(sets)]
+        lib.clk_layer_norm_bwd(stream, native.BF16, s["x"].data_ptr(), s["scale"].data_ptr(),
+                               s["dy"].data_ptr(), s["dx"].data_ptr(), s["ds"].data_ptr(),
+                               s["do"].data_ptr(), s["ws"].data_ptr(), s["wsb"], m, c, 1e-5)
+
+    so = torch.cuda.current_stream(dev)
+    t_f = timed(torch, fwd, steps, warmup, so)
+    t_b = timed(torch, bwd, steps, warmup, so)
+    bytes_f = m * c * 4.0
+    bytes_b = m * c * 6.0
+    kf = per_kernel(torch, native, fwd, steps)
+    kb = per_kernel(torch, native, bwd, steps)
+    return {
+        "ln_fwd_GBps": bytes_f / (t_f * 1e-3) / 1e9, "ln_fwd_ms": t_f,
+        "ln_bwd_GBps": bytes_b / (t_b * 1e-3) / 1e9, "ln_bwd_ms": t_b,
+        "ln_fwd_kernel_ms": kf.get("ln_fwd", {}).get("avg_ms"),
+        "ln_bwd_kernel_ms": kb.get("ln_bwd", {}).get("avg_ms"),
+        "ln_bwd_colsum_ms": kb.get("ln_bwd_colsum", {}).get("avg_ms"),
+        "ln_bytes_fwd": bytes_f, "ln_bytes_bwd": bytes_b,
+    }
+
+
+def bench_ln_gdp(torch, workloads, native, dev, stream, steps, warmup):
+    """LayerNorm + both gated branches on z [512*512, 128] bf16 (a, b [512*512, 128])."""
+    m, c, n = 512 * 512, 128, 128
+    lib = native.lib()
+    sets = []
+    for r in range(3):
+        li = workloads.layer_norm_inputs(m, c, torch.bfloat16, seed=3 + r, device=dev)
+        wa = workloads.gdp_weights(c, n, torch.bfloat16, seed=21 + r, device=dev)
+        wb = workloads.gdp_weights(c, n, torch.bfloat16, seed=41 + r, device=dev)
+        sets.append((li, wa, wb, torch.empty((m, n), device=dev, dtype=torch.bfloat16),
+                     torch.empty((m, n), device=dev, dtype=torch.bfloat16)))
+
+    def run(i):
+        li, wa, wb, a, b = sets[i % len(sets)]
+        st = lib.clk_ln_gated_dual_proj(
+            stream, native.BF16, li["x"].data_ptr(), li["scale"].data_ptr(),
+            li["offset"].data_ptr(), wa[0].data_ptr(), wa[1].data_ptr(), wa[2].data_ptr(),
+            wa[3].data_ptr(), wb[0].data_ptr(), wb[1].data_ptr(), wb[2].data_ptr(),
+            wb[3].data_ptr(), li["mask"].data_ptr(), a.data_ptr(), b.data_ptr(), m, c, n, 1e-5)
+        if st != 0:
+            raise RuntimeError(native.last_error())
+
+    so = torch.cuda.current_stream(dev)
+    t = timed(torch, run, steps, warmup, so)
+    nbytes = m * c * 2.0 + m * 2.0 + 2.0 * m * n * 2.0 + 4.0 * c * n * 2.0
+    k = per_kernel(torch, native, run, steps)
+    return {"ln_gdp_GBps": nbytes / (t * 1e-3) / 1e9, "ln_gdp_ms": t,
+            "ln_gdp_kernel_ms": k.get("ln_gdp", {}).get("avg_ms"), "ln_gdp_bytes": nbytes,
+            "ln_gdp_TFLOPs": 4 * 2.0 * m * c * n / (t * 1e-3) / 1e12}
+
+
+def cpu_baseline(torch, workloads, rows, min_seconds):
+    from oracle import cpu_baseline as cb
+    cores = _cores()
+    inp = workloads.attention_inputs(rows, HEADS, NRES, NRES, HEAD_DIM, torch.bfloat16, seed=1,
+                                     device="cpu", masked_tail=0.10)
+    sec = cb.time_attention_fwd_bwd(inp, rows, cores, min_seconds=min_seconds)
+    flops = attention_flops(rows, HEADS, NRES, NRES, HEAD_DIM)["step"]
+    return {"value": flops / sec / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": "torch float32 jnp restatement (materialised logits + autograd), fwd+bwd of "
+                      "%d of the %d rows at N_res=%d, median of >=3 runs (%.2f s each), scaled "
+                      "by algorithmic flops" % (rows, N_ROWS, NRES, sec)}
+
+
+def main(argv=None):
+    ap = argparse.ArgumentParser(description="Evoformer hot-path benchmark (one MI355X)")
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=64)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-secondary", action="store_true")
+    args = ap.parse_args(argv)
+    if args.gpus != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (the attention rows "
+              "would shard across GPUs with one dBias all-reduce; not built). Use --gpus 1.",
+              file=sys.stderr)
+        return 2
+
+    import torch
+    from colabfold_legacy_kernels import _native as native
+    from colabfold_legacy_kernels import workloads
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib = native.lib()
+    so = torch.cuda.current_stream(dev)
+    stream = so.cuda_stream
+    print("bench: building %d attention input sets" % ROTATE, file=sys.stderr, flush=True)
+    sets = [AttentionSet(torch, workloads, native, dev, seed=1 + r) for r in range(ROTATE)]
+
+    def step(i):
+        attention_step(lib, native, stream, sets[i % ROTATE])
+
+    print("bench: timing attention fwd+bwd", file=sys.stderr, flush=True)
+    ms = timed(torch, step, args.steps, args.warmup, so)
+    fl = attention_flops(N_ROWS, HEADS, NRES, NRES, HEAD_DIM)
+    tflops = fl["step"] / (ms * 1e-3) / 1e12
+    kernels = per_kernel(torch, native, step, args.steps)
+    per_step = {k: v["avg_ms"] * v["launches_per_step"] for k, v in kernels.items()}
+    dom = max(per_step, key=per_step.get)
+    dom_flops = fl.get(dom, 0.0)
+    achieved = dom_flops / (kernels[dom]["avg_ms"] * 1e-3) / 1e12 if dom_flops else None
+    roofline = {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": MFMA_PEAK_BF16,
+                "unit": "TFLOP/s", "frac": (achieved / MFMA_PEAK_BF16) if achieved else None,
+                "traffic": None, "avg_ms": kernels[dom]["avg_ms"],
+                "algorithmic_flops_per_launch": dom_flops}
+
+    result = {
+        "metric": METRIC, "value": tflops, "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "triangle attention fwd+bwd, N_res=384", "rows": N_ROWS,
+                   "heads": HEADS, "seq_q": NRES, "seq_k": NRES, "head_dim": HEAD_DIM,
+                   "masked_keys": "last 10%", "rotating_sets": ROTATE,
+                   "parallelism": "single GPU"},
+        "frac_of_mfma_peak": tflops / MFMA_PEAK_BF16,
+        "roofline": roofline,
+        "kernels_ms_per_step": per_step,
+    }
+    if not args.no_secondary:
+        print("bench: timing LayerNorm", file=sys.stderr, flush=True)
+        sec = bench_layer_norm(torch, workloads, native, dev, stream, args.steps, args.warmup)
+        sec["ln_fwd_frac_hbm"] = sec["ln_fwd_GBps"] / HBM_PEAK
+        sec["ln_bwd_frac_hbm"] = sec["ln_bwd_GBps"] / HBM_PEAK
+        print("bench: timing LayerNorm + gated dual projection", file=sys.stderr, flush=True)
+        sec.update(bench_ln_gdp(torch, workloads, native, dev, stream, args.steps, args.warmup))
+        sec["ln_gdp_frac_hbm"] = sec["ln_gdp_GBps"] / HBM_PEAK
+        result["secondary"] = sec
+    if not args.no_cpu_baseline:
+        print("bench: timing CPU baseline", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(torch, workloads, args.cpu_rows, args.cpu_seconds)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -23,6 +23,9 @@ c_size = ctypes.c_size_t
 PROTOTYPES = {
     "clk_last_error": (ctypes.c_char_p, []),
     "clk_version": (ctypes.c_char_p, []),
+    "clk_profile_enable": (None, [c_int]),
+    "clk_profile_collect": (c_int, [ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(c_f32),
+                                    c_int]),
     "clk_attention_fwd": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                                   c_void_p, c_void_p, c_void_p, c_i64, c_i64, c_i64, c_i64,
                                   c_i64, c_f32, c_i64, c_i64]),
@@ -71,3 +74,28 @@ def lib():
 
 def last_error():
     return lib().clk_last_error().decode()
+
+
+class profile:
+    """Context manager: record per-launch HIP event times of every kernel the library launches
+    from this thread; ``records`` holds (kernel name, milliseconds) after exit."""
+
+    def __init__(self):
+        self.records = []
+
+    def __enter__(self):
+        lib().clk_profile_enable(1)
+        return self
+
+    def __exit__(self, *exc):
+        lib().clk_profile_enable(0)
+        self.records = collect()
+        return False
+
+
+def collect(max_records=65536):
+    """Wait for and return the (name, ms) records taken so far on this thread, clearing them."""
+    names = (ctypes.c_char_p * max_records)()
+    ms = (c_f32 * max_records)()
+    n = lib().clk_profile_collect(names, ms, max_records)
+    return [(names[i].decode(), float(ms[i])) for i in range(min(n, max_records))]

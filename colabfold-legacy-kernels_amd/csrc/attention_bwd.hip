@@ -463,6 +463,7 @@ void launch_dq(hipStream_t st, dim3 grid, const void* q, const void* k, const vo
                const float* di, void* dq, float* dq_part, float* dbias_dst, int N, int H, int Sq,
                int Sk, int NB, int nranges, float scale, int vec_ok) {
     using E = typename TR::elem;
+    KernelTimer timer("attn_bwd_dq", st);
     attn_bwd_dq<TR, D, KT><<<grid, 256, 0, st>>>(
         (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (const E*)dout, lse, di,
         (E*)dq, dq_part, dbias_dst, N, H, Sq, Sk, NB, nranges, scale, vec_ok);
@@ -483,6 +484,7 @@ void run_bwd(hipStream_t st, const BwdPlan& p, const void* q, const void* k, con
 
     {
         const int64_t threads = rows * (D / 8);
+        KernelTimer timer("attn_bwd_dot", st);
         attn_bwd_dot<TR, D><<<(int)((threads + 255) / 256), 256, 0, st>>>(
             (const E*)out, (const E*)dout, di, rows);
     }
@@ -501,16 +503,21 @@ void run_bwd(hipStream_t st, const BwdPlan& p, const void* q, const void* k, con
     }
     {
         dim3 grid(ceil_div(Sk, 64), H, N);
+        KernelTimer timer("attn_bwd_dkv", st);
         attn_bwd_dkv<TR, D><<<grid, 256, 0, st>>>((const E*)q, (const E*)k, (const E*)v,
                                                   (const E*)bias, kmask, (const E*)dout, lse, di,
                                                   (E*)dk, (E*)dv, H, Sq, Sk, scale, vec_ok);
     }
-    if (p.nchunks > 1)
+    if (p.nchunks > 1) {
+        KernelTimer timer("attn_bwd_dbias_sum", st);
         sum_partials_f32<<<grid_for(dbias_count), 256, 0, st>>>(dbias_part, dbias_count,
                                                                 p.nchunks, dbias);
-    if (p.nranges > 1)
+    }
+    if (p.nranges > 1) {
+        KernelTimer timer("attn_bwd_dq_sum", st);
         sum_partials_cast<TR><<<grid_for((size_t)rows * D), 256, 0, st>>>(
             dq_part, (size_t)rows * D, p.nranges, (E*)dq);
+    }
 }
 
 // Sizes with an empty axis: write the zeros that the gradient formulas give (fill kernels, so

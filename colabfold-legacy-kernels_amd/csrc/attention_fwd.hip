@@ -203,6 +203,7 @@ void launch_fwd(hipStream_t st, const void* q, const void* k, const void* v, con
                 float scale) {
     using E = typename TR::elem;
     const int vec_ok = (Sk % 8 == 0) ? 1 : 0;
+    KernelTimer timer("attn_fwd", st);
     if (Sq <= 64) {
         dim3 grid(ceil_div(Sq, 64), H, N);
         attn_fwd_kernel<TR, D, 1><<<grid, 256, 0, st>>>(

@@ -121,6 +121,20 @@ clk_status fail(clk_status code, const char* fmt, ...) __attribute__((format(pri
 clk_status ok();
 clk_status check_launch(const char* what);
 
+// Brackets one kernel launch with HIP events when per-launch timing is enabled on this thread.
+class KernelTimer {
+   public:
+    KernelTimer(const char* name, hipStream_t stream);
+    ~KernelTimer();
+    KernelTimer(const KernelTimer&) = delete;
+    KernelTimer& operator=(const KernelTimer&) = delete;
+
+   private:
+    const char* name_;
+    hipStream_t stream_;
+    hipEvent_t start_ = nullptr;
+};
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 inline size_t elem_size(clk_dtype t) {
     return t == CLK_F32 ? 4 : (t == CLK_U8 ? 1 : 2);

@@ -1,0 +1,445 @@
+// Gated dual projection for gfx950:
+//   out[m, n] = mask[m] * (x[m,:].wp[:,n] + bp[n]) * sigmoid(x[m,:].wg[:,n] + bg[n])
+// gdp_kernel replaces VoltaGdp / VoltaGdpWmma (cuda/volta_ops.cu:109-265,
+// cuda/volta_gdp_wmma.cu:16-140); ln_gdp_kernel fuses the LayerNorm in front of both gated
+// branches of the triangle multiplication (one read of z for LN + two GDPs).
+//
+// Both compute out^T = W^T . x^T on MFMA 16x16x32: the weights are the A operand, read from LDS
+// with ds_read_b64_tr_b16 (W stays row-major [K][N] in LDS, as in global memory), and x^T is the
+// B operand, loaded straight from global memory as 16-byte row chunks. The output columns of
+// each 32-column chunk are permuted across the two 16-row A tiles so that a lane's accumulators
+// hold 8 consecutive output columns of one row: the epilogue (bias, sigmoid gate, row mask) ends
+// in one 16-byte store per lane and chunk. At K = N = 128 the op is HBM-bound (about 170 flop/B
+// against MI355X's ridge of about 315).
+#include "common.hpp"
+
+#include <mutex>
+
+namespace clk {
+namespace {
+
+// A operand W^T for output-column chunk c (32 columns), half h, contraction rows kbase + 8g + 0..7.
+// A-tile row r16 stands for output column 32c + 8*(r16/4) + 4h + r16%4, so the C tile's rows
+// 4g'+i land in lane group g' as columns 32c + 8g' + 4h + i. For the transposed read, lane
+// (r16, g) supplies row kbase + 8g + (r16>>2) (+4 for the upper four slots), columns
+// 32c + 8*(r16&3) + 4h .. +3 (four consecutive output columns of one A-row group).
+template <typename V8, typename E>
+__device__ __forceinline__ V8 w_operand(const E* lds, int ld, int kbase, int c, int h, int r16,
+                                        int g) {
+    const E* lo = lds + (kbase + 8 * g + (r16 >> 2)) * ld + 32 * c + 8 * (r16 & 3) + 4 * h;
+    return lds_tr8<V8>(lo, lo + 4 * ld);
+}
+
+__device__ __forceinline__ float sigmoid(float x) {
+    return fast_rcp(1.f + fast_exp2(-x * kLog2e));
+}
+
+template <typename TR>
+__device__ __forceinline__ u32x4 pack8(const float* v) {
+    using E = typename TR::elem;
+    E e[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) e[j] = TR::from_f(v[j]);
+    u32x4 raw;
+    __builtin_memcpy(&raw, e, 16);
+    return raw;
+}
+
+// Stages rows [0, KP) x columns [n0, n0 + BN) of a row-major [K, N] weight into LDS (row stride
+// ld); rows past K and columns past N read as zero.
+template <typename E>
+__device__ void stage_weight(E* lds, int ld, const E* w, int K, int N, int KP, int n0, int BN,
+                             int tid, int nthreads) {
+    const int cpr = BN / 8;
+    for (int i = tid; i < KP * cpr; i += nthreads) {
+        const int k = i / cpr, c8 = (i % cpr) * 8;
+        u32x4 v = {0u, 0u, 0u, 0u};
+        if (k < K && n0 + c8 < N) v = ld16(w + (size_t)k * N + n0 + c8);
+        *reinterpret_cast<u32x4*>(lds + k * ld + c8) = v;
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// GDP: a block owns BN output columns and walks row tiles of 4 waves x 16*RT rows.
+// ---------------------------------------------------------------------------------------------
+template <typename TR, int BN>
+__global__ __launch_bounds__(256) void gdp_kernel(const typename TR::elem* __restrict__ x,
+                                                  const typename TR::elem* __restrict__ wp,
+                                                  const typename TR::elem* __restrict__ bp,
+                                                  const typename TR::elem* __restrict__ wg,
+                                                  const typename TR::elem* __restrict__ bg,
+                                                  const typename TR::elem* __restrict__ mask,
+                                                  typename TR::elem* __restrict__ out, int M,
+                                                  int K, int N, int KP) {
+    using E = typename TR::elem;
+    using V8 = typename TR::vec8;
+    constexpr int NT = BN / 16;   // 16-column A tiles
+    constexpr int RT = 256 / BN;  // 16-row B tiles per wave
+    constexpr int LD = BN + 8;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    E* wp_lds = reinterpret_cast<E*>(smem);
+    E* wg_lds = wp_lds + KP * LD;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.y * BN;
+
+    stage_weight(wp_lds, LD, wp, K, N, KP, n0, BN, threadIdx.x, 256);
+    stage_weight(wg_lds, LD, wg, K, N, KP, n0, BN, threadIdx.x, 256);
+
+    // Biases of the lane's output columns n0 + 32c + 8g + j.
+    float bpv[NT / 2][8], bgv[NT / 2][8];
+#pragma unroll
+    for (int c = 0; c < NT / 2; ++c)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int n = n0 + 32 * c + 8 * g + j;
+            bpv[c][j] = n < N ? TR::to_f(bp[n]) : 0.f;
+            bgv[c][j] = n < N ? TR::to_f(bg[n]) : 0.f;
+        }
+    __syncthreads();
+
+    const int rows_per_iter = 4 * 16 * RT;
+    for (int r0 = blockIdx.x * rows_per_iter; r0 < M; r0 += gridDim.x * rows_per_iter) {
+        const int rbase = r0 + wave * 16 * RT;
+        f32x4 ap[RT][NT], ag[RT][NT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                ap[rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+                ag[rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+        for (int kb = 0; kb < KP; kb += 32) {
+            V8 xf[RT];
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const int row = rbase + 16 * rt + r16;
+                const int k = kb + 8 * g;
+                u32x4 raw = {0u, 0u, 0u, 0u};
+                if (row < M && k < K) raw = ld16(x + (size_t)row * K + k);
+                xf[rt] = bits_as<V8>(raw);
+            }
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const V8 pa = w_operand<V8>(wp_lds, LD, kb, t >> 1, t & 1, r16, g);
+                const V8 ga = w_operand<V8>(wg_lds, LD, kb, t >> 1, t & 1, r16, g);
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    ap[rt][t] = TR::mfma(pa, xf[rt], ap[rt][t]);
+                    ag[rt][t] = TR::mfma(ga, xf[rt], ag[rt][t]);
+                }
+            }
+        }
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            const int row = rbase + 16 * rt + r16;
+            if (row >= M) continue;
+            const float mv = TR::to_f(mask[row]);
+#pragma unroll
+            for (int c = 0; c < NT / 2; ++c) {
+                const int n = n0 + 32 * c + 8 * g;
+                if (n >= N) continue;
+                float o[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int t = 2 * c + (j >> 2), i = j & 3;
+                    const float p = ap[rt][t][i] + bpv[c][j];
+                    const float gt = ag[rt][t][i] + bgv[c][j];
+                    o[j] = mv * p * sigmoid(gt);
+                }
+                st16(out + (size_t)row * N + n, pack8<TR>(o));
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
+// LayerNorm + both gated branches. The LN affine is folded into the weights while they are
+// staged: (xhat*gamma + beta).W + b = xhat.(diag(gamma) W) + (beta.W + b). A block keeps all four
+// folded weights [C][N] in LDS and walks row tiles of 8 waves x 32 rows; each wave normalises
+// its rows in registers (the row of C values is spread over the four lanes l, l^16, l^32, l^48)
+// and feeds them as the B operand.
+// ---------------------------------------------------------------------------------------------
+constexpr int kLnGdpThreads = 512;
+
+// Weights and biases of the two branches, passed by value: w = {wpa, wga, wpb, wgb}, same for b.
+template <typename E>
+struct LnGdpWeights {
+    const E* w[4];
+    const E* b[4];
+};
+
+template <typename TR, int C, int N>
+__global__ __launch_bounds__(kLnGdpThreads) void ln_gdp_kernel(
+    const typename TR::elem* __restrict__ z, const float* __restrict__ gamma,
+    const float* __restrict__ beta, LnGdpWeights<typename TR::elem> wb,
+    const typename TR::elem* __restrict__ mask, typename TR::elem* __restrict__ outa,
+    typename TR::elem* __restrict__ outb, int M, float eps) {
+    using E = typename TR::elem;
+    using V8 = typename TR::vec8;
+    constexpr int LD = N + 8;
+    constexpr int KS = C / 32;
+    constexpr int NC = N / 32;  // 32-column chunks
+    constexpr int RT = 2;
+    extern __shared__ __attribute__((aligned(16))) char smem[];
+    E* w_lds = reinterpret_cast<E*>(smem);                  // [4][C][LD]: pa, ga, pb, gb
+    float* b_lds = reinterpret_cast<float*>(w_lds + 4 * C * LD);  // [4][N]
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int r16 = lane & 15, g = lane >> 4;
+    constexpr int NW = kLnGdpThreads / 64;
+
+    // Fold and stage: W'[k][n] = gamma[k] * W[k][n]; b'[n] = b[n] + sum_k beta[k] * W[k][n].
+    for (int i = tid; i < 4 * C * N; i += kLnGdpThreads) {
+        const int w = i / (C * N), r = i % (C * N), k = r / N, n = r % N;
+        const float v = TR::to_f(wb.w[w][(size_t)k * N + n]);
+        w_lds[(w * C + k) * LD + n] = TR::from_f(gamma[k] * v);
+    }
+    for (int i = tid; i < 4 * N; i += kLnGdpThreads) {
+        const int w = i / N, n = i % N;
+        float s = TR::to_f(wb.b[w][n]);
+        for (int k = 0; k < C; ++k) s += beta[k] * TR::to_f(wb.w[w][(size_t)k * N + n]);
+        b_lds[w * N + n] = s;
+    }
+    __syncthreads();
+
+    const int rows_per_iter = NW * 16 * RT;
+    for (int r0 = blockIdx.x * rows_per_iter; r0 < M; r0 += gridDim.x * rows_per_iter) {
+        const int rbase = r0 + wave * 16 * RT;
+        V8 xf[RT][KS];
+        float mv[RT];
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            const int row = rbase + 16 * rt + r16;
+            const bool in = row < M;
+            float v[KS][8];
+            float sum = 0.f;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                u32x4 raw = {0u, 0u, 0u, 0u};
+                if (in) raw = ld16(z + (size_t)row * C + ks * 32 + 8 * g);
+                E e[8];
+                __builtin_memcpy(e, &raw, 16);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    v[ks][j] = TR::to_f(e[j]);
+                    sum += v[ks][j];
+                }
+            }
+            const float mean = xgroup_sum(sum) * (1.f / C);
+            float m2 = 0.f;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float d = v[ks][j] - mean;
+                    m2 += d * d;
+                }
+            const float rstd = rsqrtf(xgroup_sum(m2) * (1.f / C) + eps);
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                E e[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) e[j] = TR::from_f((v[ks][j] - mean) * rstd);
+                u32x4 raw;
+                __builtin_memcpy(&raw, e, 16);
+                xf[rt][ks] = bits_as<V8>(raw);
+            }
+            mv[rt] = in ? TR::to_f(mask[row]) : 0.f;
+        }
+
+#pragma unroll
+        for (int br = 0; br < 2; ++br) {
+            const E* wpl = w_lds + (2 * br) * C * LD;
+            const E* wgl = w_lds + (2 * br + 1) * C * LD;
+            const float* bpl = b_lds + (2 * br) * N;
+            const float* bgl = b_lds + (2 * br + 1) * N;
+            E* out = br == 0 ? outa : outb;
+#pragma unroll
+            for (int c = 0; c < NC; ++c) {
+                f32x4 ap[RT][2], ag[RT][2];
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    // Bias of columns 32c + 8g + 4h + 0..3 as the accumulator's starting value.
+                    const f32x4 pb = *reinterpret_cast<const f32x4*>(bpl + 32 * c + 8 * g + 4 * h);
+                    const f32x4 gb = *reinterpret_cast<const f32x4*>(bgl + 32 * c + 8 * g + 4 * h);
+#pragma unroll
+                    for (int rt = 0; rt < RT; ++rt) {
+                        ap[rt][h] = pb;
+                        ag[rt][h] = gb;
+                    }
+                }
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const V8 pa = w_operand<V8>(wpl, LD, ks * 32, c, h, r16, g);
+                        const V8 ga = w_operand<V8>(wgl, LD, ks * 32, c, h, r16, g);
+#pragma unroll
+                        for (int rt = 0; rt < RT; ++rt) {
+                            ap[rt][h] = TR::mfma(pa, xf[rt][ks], ap[rt][h]);
+                            ag[rt][h] = TR::mfma(ga, xf[rt][ks], ag[rt][h]);
+                        }
+                    }
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    const int row = rbase + 16 * rt + r16;
+                    if (row >= M) continue;
+                    float o[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int h = j >> 2, i = j & 3;
+                        o[j] = mv[rt] * ap[rt][h][i] * sigmoid(ag[rt][h][i]);
+                    }
+                    st16(out + (size_t)row * N + 32 * c + 8 * g, pack8<TR>(o));
+                }
+            }
+        }
+    }
+}
+
+template <typename F>
+void allow_lds(F* kern, size_t bytes) {
+    // One attribute call per kernel instantiation (thread-safe, process lifetime).
+    static std::once_flag once;
+    std::call_once(once, [&] {
+        hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    });
+}
+
+constexpr size_t kMaxLds = 160 * 1024;
+
+int row_blocks(int64_t M, int rows_per_block, int cap) {
+    const int64_t b = (M + rows_per_block - 1) / rows_per_block;
+    return (int)(b < cap ? (b > 0 ? b : 1) : cap);
+}
+
+template <typename TR, int BN>
+clk_status launch_gdp(hipStream_t st, const void* x, const void* wp, const void* bp,
+                      const void* wg, const void* bg, const void* mask, void* out, int M, int K,
+                      int N) {
+    using E = typename TR::elem;
+    const int KP = (K + 31) / 32 * 32;
+    const size_t lds = (size_t)2 * KP * (BN + 8) * sizeof(E);
+    if (lds > kMaxLds) return fail(CLK_INVALID_ARGUMENT, "gated_dual_proj: K=%d too large", K);
+    allow_lds(gdp_kernel<TR, BN>, kMaxLds);
+    dim3 grid(row_blocks(M, 256, 2048), (N + BN - 1) / BN);
+    KernelTimer timer("gdp", st);
+    gdp_kernel<TR, BN><<<grid, 256, lds, st>>>((const E*)x, (const E*)wp, (const E*)bp,
+                                                (const E*)wg, (const E*)bg, (const E*)mask,
+                                                (E*)out, M, K, N, KP);
+    return check_launch("gated_dual_proj");
+}
+
+template <typename TR>
+clk_status dispatch_gdp(hipStream_t st, const void* x, const void* wp, const void* bp,
+                        const void* wg, const void* bg, const void* mask, void* out, int M, int K,
+                        int N) {
+    const int KP = (K + 31) / 32 * 32;
+    if (N >= 128 && KP <= 256)
+        return launch_gdp<TR, 128>(st, x, wp, bp, wg, bg, mask, out, M, K, N);
+    return launch_gdp<TR, 64>(st, x, wp, bp, wg, bg, mask, out, M, K, N);
+}
+
+template <typename TR, int C, int N>
+clk_status launch_ln_gdp(hipStream_t st, const void* z, const float* gamma, const float* beta,
+                         const LnGdpWeights<typename TR::elem>& wb, const void* mask, void* a,
+                         void* b, int M, float eps) {
+    using E = typename TR::elem;
+    const size_t lds = (size_t)4 * C * (N + 8) * sizeof(E) + 4 * N * sizeof(float);
+    static_assert((size_t)4 * C * (N + 8) * 2 + 4 * N * 4 <= kMaxLds, "weights exceed LDS");
+    allow_lds(ln_gdp_kernel<TR, C, N>, kMaxLds);
+    const int grid = row_blocks(M, kLnGdpThreads / 64 * 32, 256);
+    KernelTimer timer("ln_gdp", st);
+    ln_gdp_kernel<TR, C, N><<<grid, kLnGdpThreads, lds, st>>>((const E*)z, gamma, beta, wb,
+                                                              (const E*)mask, (E*)a, (E*)b, M,
+                                                              eps);
+    return check_launch("ln_gated_dual_proj");
+}
+
+template <typename TR>
+clk_status dispatch_ln_gdp(hipStream_t st, const void* z, const float* gamma, const float* beta,
+                           const void* const* w, const void* const* bias, const void* mask,
+                           void* a, void* b, int M, int C, int N, float eps) {
+    using E = typename TR::elem;
+    LnGdpWeights<E> wb;
+    for (int i = 0; i < 4; ++i) {
+        wb.w[i] = static_cast<const E*>(w[i]);
+        wb.b[i] = static_cast<const E*>(bias[i]);
+    }
+#define CLK_LNGDP(CC, NN)                                                                   \
+    if (C == (CC) && N == (NN))                                                             \
+        return launch_ln_gdp<TR, CC, NN>(st, z, gamma, beta, wb, mask, a, b, M, eps);
+    CLK_LNGDP(128, 128) CLK_LNGDP(128, 64) CLK_LNGDP(64, 128) CLK_LNGDP(64, 64)
+    CLK_LNGDP(128, 32) CLK_LNGDP(32, 128) CLK_LNGDP(96, 96) CLK_LNGDP(64, 32) CLK_LNGDP(32, 64)
+    CLK_LNGDP(32, 32) CLK_LNGDP(96, 128) CLK_LNGDP(128, 96) CLK_LNGDP(96, 64) CLK_LNGDP(64, 96)
+    CLK_LNGDP(96, 32) CLK_LNGDP(32, 96)
+#undef CLK_LNGDP
+    return fail(CLK_INVALID_ARGUMENT, "ln_gated_dual_proj: C=%d, N=%d not supported", C, N);
+}
+
+}  // namespace
+}  // namespace clk
+
+using namespace clk;
+
+extern "C" clk_status clk_gated_dual_proj(hipStream_t stream, clk_dtype dtype, const void* x,
+                                          const void* wp, const void* bp, const void* wg,
+                                          const void* bg, const void* mask, void* out, int64_t M,
+                                          int64_t K, int64_t N) {
+    const char* who = "gated_dual_proj";
+    if (dtype != CLK_F16 && dtype != CLK_BF16)
+        return fail(CLK_INVALID_ARGUMENT, "%s: dtype %s not supported (f16, bf16)", who,
+                    dtype_name(dtype));
+    if (M < 0 || K <= 0 || N <= 0) return fail(CLK_INVALID_ARGUMENT, "%s: bad dims", who);
+    // Same divisibility rule as the reference for N (cuda/volta_ops.cu:234-236); K for 16-byte
+    // row chunks; the weights of one 64/128-column slab must fit in LDS.
+    if (N % 8) return fail(CLK_INVALID_ARGUMENT, "%s: N must be a multiple of 8", who);
+    if (K % 8) return fail(CLK_INVALID_ARGUMENT, "%s: K must be a multiple of 8", who);
+    if (K > 512) return fail(CLK_INVALID_ARGUMENT, "%s: K=%lld above 512", who, (long long)K);
+    if (M > INT32_MAX || N > (1 << 20))
+        return fail(CLK_INVALID_ARGUMENT, "%s: dims too large", who);
+    if (M == 0) return ok();
+    if (!x || !wp || !bp || !wg || !bg || !mask || !out)
+        return fail(CLK_INVALID_ARGUMENT, "%s: null operand pointer", who);
+    if (!aligned16(x) || !aligned16(wp) || !aligned16(wg) || !aligned16(out))
+        return fail(CLK_INVALID_ARGUMENT, "%s: x, wp, wg, out must be 16-byte aligned", who);
+    if (dtype == CLK_BF16)
+        return dispatch_gdp<BF16>(stream, x, wp, bp, wg, bg, mask, out, (int)M, (int)K, (int)N);
+    return dispatch_gdp<F16>(stream, x, wp, bp, wg, bg, mask, out, (int)M, (int)K, (int)N);
+}
+
+extern "C" clk_status clk_ln_gated_dual_proj(hipStream_t stream, clk_dtype dtype, const void* z,
+                                             const float* ln_scale, const float* ln_offset,
+                                             const void* wpa, const void* bpa, const void* wga,
+                                             const void* bga, const void* wpb, const void* bpb,
+                                             const void* wgb, const void* bgb, const void* mask,
+                                             void* a, void* b, int64_t M, int64_t C, int64_t N,
+                                             float eps) {
+    const char* who = "ln_gated_dual_proj";
+    if (dtype != CLK_F16 && dtype != CLK_BF16)
+        return fail(CLK_INVALID_ARGUMENT, "%s: dtype %s not supported (f16, bf16)", who,
+                    dtype_name(dtype));
+    if (M < 0 || C % 32 || N % 32 || C < 32 || N < 32 || C > 128 || N > 128)
+        return fail(CLK_INVALID_ARGUMENT,
+                    "%s: C and N must be multiples of 32 in [32, 128] (C=%lld, N=%lld)", who,
+                    (long long)C, (long long)N);
+    if (M > INT32_MAX) return fail(CLK_INVALID_ARGUMENT, "%s: M too large", who);
+    if (M == 0) return ok();
+    const void* w[4] = {wpa, wga, wpb, wgb};
+    const void* bias[4] = {bpa, bga, bpb, bgb};
+    for (int i = 0; i < 4; ++i)
+        if (!w[i] || !bias[i]) return fail(CLK_INVALID_ARGUMENT, "%s: null weight", who);
+    if (!z || !ln_scale || !ln_offset || !mask || !a || !b)
+        return fail(CLK_INVALID_ARGUMENT, "%s: null operand pointer", who);
+    if (!aligned16(z) || !aligned16(a) || !aligned16(b))
+        return fail(CLK_INVALID_ARGUMENT, "%s: z, a, b must be 16-byte aligned", who);
+    if (dtype == CLK_BF16)
+        return dispatch_ln_gdp<BF16>(stream, z, ln_scale, ln_offset, w, bias, mask, a, b, (int)M,
+                                     (int)C, (int)N, eps);
+    return dispatch_ln_gdp<F16>(stream, z, ln_scale, ln_offset, w, bias, mask, a, b, (int)M,
+                                (int)C, (int)N, eps);
+}

@@ -307,19 +307,33 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_generic(const void* __restric
     }
 }
 
-// out[which][c] = sum over blocks b (in order) of part[b*stride + which*C + c].
-__global__ __launch_bounds__(kThreads) void ln_colsum(const float* __restrict__ part,
-                                                      size_t stride, int nblocks, int C,
-                                                      float* __restrict__ dscale,
-                                                      float* __restrict__ doffset) {
-    constexpr int kCols = 64, kSplit = kThreads / kCols;
+// out[which][c] = sum over the partial rows b of part[b*stride + which*C + c], in a fixed order:
+// 16 row groups (b = sp, sp+16, ...) each summed with eight interleaved accumulators so eight
+// loads are in flight, then the groups are added in order. Columns are spread over many blocks
+// (32 columns per block).
+__global__ __launch_bounds__(512) void ln_colsum(const float* __restrict__ part, size_t stride,
+                                                 int nblocks, int C, float* __restrict__ dscale,
+                                                 float* __restrict__ doffset) {
+    constexpr int kCols = 32, kSplit = 16, kAcc = 8;
     __shared__ float red[kSplit][kCols];
     const int cl = threadIdx.x % kCols, sp = threadIdx.x / kCols;
     const int t = blockIdx.x * kCols + cl;  // over 2*C outputs
-    float a = 0.f;
+    float acc[kAcc];
+#pragma unroll
+    for (int i = 0; i < kAcc; ++i) acc[i] = 0.f;
     if (t < 2 * C) {
-        for (int b = sp; b < nblocks; b += kSplit) a += part[(size_t)b * stride + t];
+        int b = sp;
+        for (; b + (kAcc - 1) * kSplit < nblocks; b += kAcc * kSplit) {
+#pragma unroll
+            for (int i = 0; i < kAcc; ++i) acc[i] += part[(size_t)(b + i * kSplit) * stride + t];
+        }
+#pragma unroll
+        for (int i = 0; i < kAcc - 1; ++i)
+            if (b + i * kSplit < nblocks) acc[i] += part[(size_t)(b + i * kSplit) * stride + t];
     }
+    float a = 0.f;
+#pragma unroll
+    for (int i = 0; i < kAcc; ++i) a += acc[i];
     red[sp][cl] = a;
     __syncthreads();
     if (sp == 0 && t < 2 * C) {
@@ -359,6 +373,7 @@ template <typename TR, int LPR, int NV>
 void launch_fwd(hipStream_t st, const void* x, const float* sc, const float* of, void* y, int M,
                 float eps) {
     const int grid = fwd_blocks(M, kThreads / LPR);
+    KernelTimer timer("ln_fwd", st);
     ln_fwd_kernel<TR, LPR, NV><<<grid, kThreads, 0, st>>>(x, sc, of, y, M, eps);
 }
 
@@ -376,6 +391,7 @@ bool dispatch_fwd(hipStream_t st, const void* x, const float* sc, const float* o
 #undef CLK_LN_ROW
 #undef CLK_LN_CASE
     const int grid = fwd_blocks(M, kThreads / 64);
+    KernelTimer timer("ln_fwd", st);
     ln_fwd_generic<TR><<<grid, kThreads, 0, st>>>(x, sc, of, y, M, C, eps);
     return false;
 }
@@ -384,6 +400,7 @@ template <typename TR, int LPR, int NV>
 void launch_bwd(hipStream_t st, const void* x, const float* sc, const void* dy, void* dx,
                 float* part, int M, float eps) {
     const int grid = bwd_blocks(M, kThreads / LPR);
+    KernelTimer timer("ln_bwd", st);
     ln_bwd_kernel<TR, LPR, NV><<<grid, kThreads, 0, st>>>(x, sc, dy, dx, part, M, eps);
 }
 
@@ -404,6 +421,7 @@ void dispatch_bwd(hipStream_t st, const void* x, const float* sc, const void* dy
 #undef CLK_LN_ROW
 #undef CLK_LN_CASE
     const int grid = bwd_blocks(M, kThreads / 64);
+    KernelTimer timer("ln_bwd", st);
     ln_bwd_generic<TR><<<grid, kThreads, 0, st>>>(x, sc, dy, dx, part, M, C, eps);
     *nblocks = grid;
     *stride = (size_t)(kThreads / 64 + 1) * 2 * C;
@@ -474,7 +492,7 @@ extern "C" clk_status clk_layer_norm_bwd(hipStream_t stream, clk_dtype dtype, co
     if (M == 0) {
         if (!dscale || !doffset) return fail(CLK_INVALID_ARGUMENT, "layer_norm_bwd: null pointer");
         // No rows: the column sums are zero (a fill kernel, so the call stays graph-capturable).
-        ln_colsum<<<ceil_div(2 * C, 64), kThreads, 0, stream>>>(nullptr, 0, 0, (int)C, dscale,
+        ln_colsum<<<ceil_div(2 * C, 32), 512, 0, stream>>>(nullptr, 0, 0, (int)C, dscale,
                                                                doffset);
         return check_launch("layer_norm_bwd");
     }
@@ -495,7 +513,8 @@ extern "C" clk_status clk_layer_norm_bwd(hipStream_t stream, clk_dtype dtype, co
                               &stride);
             break;
     }
-    ln_colsum<<<ceil_div(2 * C, 64), kThreads, 0, stream>>>(part, stride, nblocks, (int)C, dscale,
+    KernelTimer timer("ln_bwd_colsum", stream);
+    ln_colsum<<<ceil_div(2 * C, 32), 512, 0, stream>>>(part, stride, nblocks, (int)C, dscale,
                                                            doffset);
     return check_launch("layer_norm_bwd");
 }

@@ -4,8 +4,9 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <vector>
 
-#include "clk.h"
+#include "common.hpp"
 
 namespace clk {
 
@@ -41,6 +42,35 @@ clk_status check_launch(const char* what) {
     return ok();
 }
 
+namespace {
+struct LaunchRecord {
+    const char* name;
+    hipEvent_t start, stop;
+};
+thread_local bool g_profile = false;
+thread_local std::vector<LaunchRecord> g_records;
+}  // namespace
+
+KernelTimer::KernelTimer(const char* name, hipStream_t stream) : name_(name), stream_(stream) {
+    if (!g_profile) return;
+    if (hipEventCreate(&start_) != hipSuccess) {
+        start_ = nullptr;
+        return;
+    }
+    hipEventRecord(start_, stream_);
+}
+
+KernelTimer::~KernelTimer() {
+    if (!start_) return;
+    hipEvent_t stop = nullptr;
+    if (hipEventCreate(&stop) != hipSuccess) {
+        hipEventDestroy(start_);
+        return;
+    }
+    hipEventRecord(stop, stream_);
+    g_records.push_back({name_, start_, stop});
+}
+
 const char* dtype_name(clk_dtype t) {
     switch (t) {
         case CLK_U8: return "u8";
@@ -54,5 +84,24 @@ const char* dtype_name(clk_dtype t) {
 }  // namespace clk
 
 extern "C" const char* clk_last_error(void) { return clk::g_last_error; }
+
+extern "C" void clk_profile_enable(int on) { clk::g_profile = on != 0; }
+
+extern "C" int clk_profile_collect(const char** names, float* ms, int max) {
+    const int n = (int)clk::g_records.size();
+    for (int i = 0; i < n; ++i) {
+        auto& r = clk::g_records[i];
+        float t = -1.f;
+        if (hipEventSynchronize(r.stop) == hipSuccess) hipEventElapsedTime(&t, r.start, r.stop);
+        if (i < max) {
+            if (names) names[i] = r.name;
+            if (ms) ms[i] = t;
+        }
+        hipEventDestroy(r.start);
+        hipEventDestroy(r.stop);
+    }
+    clk::g_records.clear();
+    return n;
+}
 
 extern "C" const char* clk_version(void) { return "colabfold-legacy-kernels gfx950 0.2.0"; }

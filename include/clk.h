@@ -50,6 +50,17 @@ const char* clk_last_error(void);
 const char* clk_version(void);
 
 /*
+ * Per-launch timing (no reference counterpart; the reference has no run-time tracing). While
+ * enabled on a thread, every kernel an entry point launches from that thread is bracketed by a
+ * pair of HIP events on its stream. clk_profile_collect waits for the recorded events, writes up
+ * to `max` (kernel name, milliseconds) pairs in launch order, releases the events and returns
+ * the number of records (which may exceed `max`). Names are static strings. Off by default;
+ * creating events allocates host-side resources, so keep it out of graph capture.
+ */
+void clk_profile_enable(int on);
+int clk_profile_collect(const char** names, float* ms, int max);
+
+/*
  * Attention forward: out = softmax(scale * q.k^T + bias, masked keys at logit -1e9) . v.
  * Replaces VoltaMma (cuda/volta_mma_attn.cu:304-351) and VoltaWmma (cuda/volta_wmma_attn.cu:
  * 264-311): same operands, same attributes (scale, block_q, block_k). dtype is CLK_F16 or

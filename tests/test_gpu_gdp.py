@@ -1,0 +1,95 @@
+"""Gated dual projection and LayerNorm-fused GDP on the GPU against the float64 oracle."""
+import numpy as np
+import pytest
+import torch
+
+from _util import TOL, assert_close, dname, np64
+from colabfold_legacy_kernels import ops
+from colabfold_legacy_kernels.workloads import gdp_weights, layer_norm_inputs
+from oracle import gdp as ref
+
+pytestmark = pytest.mark.gpu
+
+# (M, K, N): reference shapes (128x128), the MSA width, ragged rows, K/N not multiples of 32/64.
+GDP_SHAPES = [(1000, 128, 128), (77, 256, 256), (300, 128, 64), (33, 64, 200), (5, 40, 8),
+              (129, 512, 72), (1, 8, 8)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=dname)
+@pytest.mark.parametrize("m,k,n", GDP_SHAPES)
+def test_gdp_parity(cuda, m, k, n, dtype):
+    li = layer_norm_inputs(m, k, dtype, seed=m + k + n)
+    w = gdp_weights(k, n, dtype, seed=n, bias_std=0.3)
+    x, mask = li["x"], li["mask"]
+    out = ops.gated_dual_proj(x.to(cuda), *(t.to(cuda) for t in w), mask.to(cuda))
+    r = ref.gated_dual_proj(np64(x), *(np64(t) for t in w), np64(mask))
+    assert_close("gdp", out, r, TOL[dname(dtype)]["gdp"])
+
+
+def test_gdp_special_cases(cuda):
+    """mask = 0 gives 0; wg = bg = 0 gives 0.5*(x.wp + bp); a large bg gives x.wp + bp."""
+    dt = torch.bfloat16
+    li = layer_norm_inputs(256, 128, dt, seed=1)
+    wp, bp, wg, bg = (t.to(cuda) for t in gdp_weights(128, 128, dt, seed=2, bias_std=0.2))
+    x = li["x"].to(cuda)
+    zero_mask = torch.zeros(256, device=cuda, dtype=dt)
+    assert torch.count_nonzero(ops.gated_dual_proj(x, wp, bp, wg, bg, zero_mask)).item() == 0
+    ones = torch.ones(256, device=cuda, dtype=dt)
+    half = ops.gated_dual_proj(x, wp, bp, torch.zeros_like(wg), torch.zeros_like(bg), ones)
+    lin = np64(x) @ np64(wp) + np64(bp)
+    assert_close("0.5*lin", half, 0.5 * lin, 1e-2)
+    open_gate = ops.gated_dual_proj(x, wp, bp, torch.zeros_like(wg),
+                                    torch.full_like(bg, 60.0), ones)
+    assert_close("lin", open_gate, lin, 1e-2)
+
+
+def test_gdp_rejects_bad_operands(cuda):
+    dt = torch.bfloat16
+    x = torch.zeros((4, 128), device=cuda, dtype=dt)
+    w = torch.zeros((128, 12), device=cuda, dtype=dt)
+    b = torch.zeros(12, device=cuda, dtype=dt)
+    with pytest.raises(ops.InvalidArgument):   # N % 8 != 0, as the reference requires
+        ops.gated_dual_proj(x, w, b, w, b, torch.ones(4, device=cuda, dtype=dt))
+
+
+LN_GDP_SHAPES = [(1000, 128, 128), (77, 64, 64), (130, 128, 32), (33, 32, 128), (9, 96, 96)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=dname)
+@pytest.mark.parametrize("m,c,n", LN_GDP_SHAPES)
+def test_ln_gdp_parity(cuda, m, c, n, dtype):
+    li = layer_norm_inputs(m, c, dtype, seed=m * 3 + c)
+    wa = gdp_weights(c, n, dtype, seed=11, bias_std=0.2)
+    wb = gdp_weights(c, n, dtype, seed=12, bias_std=0.2)
+    dev = lambda ts: tuple(t.to(cuda) for t in ts)  # noqa: E731
+    a, b = ops.ln_gated_dual_proj(li["x"].to(cuda), li["scale"].to(cuda), li["offset"].to(cuda),
+                                  dev(wa), dev(wb), li["mask"].to(cuda), 1e-5)
+    ra, rb = ref.ln_gated_dual_proj(np64(li["x"]), np64(li["scale"]), np64(li["offset"]), 1e-5,
+                                    tuple(np64(t) for t in wa), tuple(np64(t) for t in wb),
+                                    np64(li["mask"]))
+    tol = TOL[dname(dtype)]["gdp"]
+    assert_close("a", a, ra, tol)
+    assert_close("b", b, rb, tol)
+
+
+def test_ln_gdp_full_pair_rep(cuda):
+    """The 512x512x128 pair representation with a 5% padding mask: sampled rows against the
+    oracle, masked rows exactly zero, and agreement with LayerNorm followed by two GDP calls."""
+    m, c = 512 * 512, 128
+    li = layer_norm_inputs(m, c, torch.bfloat16, seed=3, device=cuda)
+    wa = gdp_weights(c, c, torch.bfloat16, seed=21, device=cuda)
+    wb = gdp_weights(c, c, torch.bfloat16, seed=22, device=cuda)
+    a, b = ops.ln_gated_dual_proj(li["x"], li["scale"], li["offset"], wa, wb, li["mask"])
+    rows = torch.tensor([0, 7, 65536, 200000, m - 1], device=cuda)
+    ra, rb = ref.ln_gated_dual_proj(np64(li["x"][rows]), np64(li["scale"]), np64(li["offset"]),
+                                    1e-5, tuple(np64(t) for t in wa), tuple(np64(t) for t in wb),
+                                    np64(li["mask"][rows]))
+    assert_close("a[rows]", a[rows], ra, TOL["bf16"]["gdp"])
+    assert_close("b[rows]", b[rows], rb, TOL["bf16"]["gdp"])
+    masked = li["mask"] == 0
+    assert torch.count_nonzero(a[masked]).item() == 0
+    y = ops.layer_norm(li["x"], li["scale"], li["offset"])
+    a2 = ops.gated_dual_proj(y, *wa, li["mask"])
+    err = (a.float() - a2.float()).abs().max().item()
+    assert err <= 2e-2 * a2.float().abs().max().item()
+    _ = np
