@@ -1,0 +1,354 @@
+// XLA FFI custom-call targets for the gfx950 kernels, exported as C symbols so JAX can register
+// them with jax.ffi.register_ffi_target(name, jax.ffi.pycapsule(getattr(lib, name)),
+// platform="ROCM"). Each handler decodes the call frame (operands, results, attributes, the
+// platform stream), checks every rank, dtype and shape on the host, and forwards to the C ABI in
+// clk.h; the status code becomes the XLA error code. No handler allocates, retains or
+// synchronises anything, so all of them declare the command-buffer-compatible trait.
+//
+// Target names and operand order follow the reference handlers:
+//   VoltaMma, VoltaWmma   (cuda/volta_mma_attn.cu:338-351, cuda/volta_wmma_attn.cu:298-311)
+//       q, k, v, bias, kmask -> out; attributes scale (f32), block_q, block_k (i64)
+//   VoltaLayerNorm        (cuda/volta_ops.cu:87-95)      x, scale, offset -> y; attribute eps
+//   VoltaGdp, VoltaGdpWmma (cuda/volta_ops.cu:254-265, cuda/volta_gdp_wmma.cu:130-140)
+//       x, wp, bp, wg, bg, mask -> out
+// and accept bf16 as well as f16. Targets without a reference counterpart:
+//   ClkAttentionFwd   q, k, v, bias, kmask -> out, lse (f32 [N,H,Sq]); attribute scale
+//   ClkAttentionBwd   q, k, v, bias, kmask, out, dout, lse -> dq, dk, dv, dbias (f32 [H,Sq,Sk]),
+//                     workspace (u8, clk_attention_bwd_workspace_size bytes); attribute scale
+//   ClkLayerNormBwd   x, scale, dy -> dx, dscale, doffset, workspace (u8); attribute eps
+//   ClkLnGdp          z, ln_scale, ln_offset, wpa, bpa, wga, bga, wpb, bpb, wgb, bgb, mask
+//                     -> a, b; attribute eps
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+
+#include "clk.h"
+#include "xla_ffi_abi.h"
+
+namespace clk {
+clk_status fail(clk_status code, const char* fmt, ...);
+}
+
+namespace {
+
+using namespace clk::xffi;
+
+class Frame {
+   public:
+    explicit Frame(CallFrame* f) : f_(f) {}
+
+    Error* error(clk_status code, const char* msg) const {
+        ErrorCreateArgs a;
+        a.struct_size = sizeof(ErrorCreateArgs);
+        a.extension_start = nullptr;
+        a.message = msg;
+        a.errc = static_cast<ErrorCode>(code);
+        return f_->api->error_create(&a);
+    }
+
+    int64_t nargs() const { return f_->args.size; }
+    int64_t nrets() const { return f_->rets.size; }
+
+    const Buffer* arg(int64_t i) const {
+        if (i >= f_->args.size || f_->args.types[i] != kArgBuffer) return nullptr;
+        return static_cast<const Buffer*>(f_->args.args[i]);
+    }
+    const Buffer* ret(int64_t i) const {
+        if (i >= f_->rets.size || f_->rets.types[i] != kRetBuffer) return nullptr;
+        return static_cast<const Buffer*>(f_->rets.rets[i]);
+    }
+
+    const Scalar* scalar(const char* name) const {
+        const size_t len = std::strlen(name);
+        for (int64_t i = 0; i < f_->attrs.size; ++i) {
+            const ByteSpan* n = f_->attrs.names[i];
+            if (n->len == len && std::memcmp(n->ptr, name, len) == 0 &&
+                f_->attrs.types[i] == kAttrScalar)
+                return static_cast<const Scalar*>(f_->attrs.attrs[i]);
+        }
+        return nullptr;
+    }
+    bool attr_f32(const char* name, float* out) const {
+        const Scalar* s = scalar(name);
+        if (!s) return false;
+        if (s->dtype == kF32) *out = *static_cast<const float*>(s->value);
+        else if (s->dtype == kF64) *out = (float)*static_cast<const double*>(s->value);
+        else return false;
+        return true;
+    }
+    bool attr_i64(const char* name, int64_t* out) const {
+        const Scalar* s = scalar(name);
+        if (!s) return false;
+        if (s->dtype == kS64) *out = *static_cast<const int64_t*>(s->value);
+        else if (s->dtype == kS32) *out = *static_cast<const int32_t*>(s->value);
+        else return false;
+        return true;
+    }
+
+    hipStream_t stream() const {
+        StreamGetArgs a;
+        a.struct_size = sizeof(StreamGetArgs);
+        a.extension_start = nullptr;
+        a.ctx = f_->ctx;
+        a.stream = nullptr;
+        if (f_->api->stream_get(&a) != nullptr) return nullptr;
+        return static_cast<hipStream_t>(a.stream);
+    }
+
+   private:
+    CallFrame* f_;
+};
+
+// The metadata query XLA makes when it registers a handler: report the API version and traits.
+bool answer_metadata(CallFrame* frame) {
+    ExtensionBase* ext = frame->extension_start;
+    while (ext && ext->type != kExtensionMetadata) ext = ext->next;
+    if (!ext) return false;
+    Metadata* md = reinterpret_cast<MetadataExtension*>(ext)->metadata;
+    md->api_version.struct_size = sizeof(ApiVersion);
+    md->api_version.extension_start = nullptr;
+    md->api_version.major_version = kApiMajor;
+    md->api_version.minor_version = kApiMinor;
+    md->traits = kCommandBufferCompatible;
+    return true;
+}
+
+template <typename Body>
+Error* run(CallFrame* frame, Body body) {
+    if (!frame) return nullptr;
+    if (answer_metadata(frame)) return nullptr;
+    if (frame->stage != kExecute) return nullptr;
+    Frame f(frame);
+    const clk_status s = body(f);
+    if (s == CLK_OK) return nullptr;
+    return f.error(s, clk_last_error());
+}
+
+// ---- shape helpers ---------------------------------------------------------------------------
+
+int64_t numel(const Buffer* b) {
+    int64_t n = 1;
+    for (int64_t i = 0; i < b->rank; ++i) n *= b->dims[i];
+    return n;
+}
+
+bool dims_are(const Buffer* b, std::initializer_list<int64_t> d) {
+    if (!b || b->rank != (int64_t)d.size()) return false;
+    int64_t i = 0;
+    for (int64_t v : d)
+        if (b->dims[i++] != v) return false;
+    return true;
+}
+
+bool half_type(DataType t) { return t == kF16 || t == kBF16; }
+
+clk_status bad(const char* who, const char* what) {
+    return clk::fail(CLK_INVALID_ARGUMENT, "%s: %s", who, what);
+}
+
+struct AttnDims {
+    int64_t N, H, Sq, Sk, D;
+};
+
+// q [N,H,Sq,D], k, v [N,H,Sk,D], bias [H,Sq,Sk], kmask u8 [N,Sk], all half types alike.
+clk_status decode_attention(const char* who, const Frame& f, AttnDims* d) {
+    const Buffer *q = f.arg(0), *k = f.arg(1), *v = f.arg(2), *bias = f.arg(3), *km = f.arg(4);
+    if (!q || !k || !v || !bias || !km) return bad(who, "expects buffers q, k, v, bias, kmask");
+    if (q->rank != 4) return bad(who, "q must be [N,H,S,D]");
+    d->N = q->dims[0];
+    d->H = q->dims[1];
+    d->Sq = q->dims[2];
+    d->D = q->dims[3];
+    if (k->rank != 4) return bad(who, "k must be [N,H,S,D]");
+    d->Sk = k->dims[2];
+    if (!dims_are(k, {d->N, d->H, d->Sk, d->D}) || !dims_are(v, {d->N, d->H, d->Sk, d->D}))
+        return bad(who, "k and v must be [N,H,Sk,D] matching q");
+    if (!dims_are(bias, {d->H, d->Sq, d->Sk})) return bad(who, "bias must be [H,Sq,Sk]");
+    if (!dims_are(km, {d->N, d->Sk}) || km->dtype != kU8) return bad(who, "kmask must be u8 [N,Sk]");
+    if (!half_type(q->dtype) || k->dtype != q->dtype || v->dtype != q->dtype ||
+        bias->dtype != q->dtype)
+        return bad(who, "q, k, v and bias must all be f16 or all bf16");
+    return CLK_OK;
+}
+
+clk_status attention_fwd(const char* who, const Frame& f, bool with_lse) {
+    AttnDims d;
+    clk_status s = decode_attention(who, f, &d);
+    if (s != CLK_OK) return s;
+    const Buffer* out = f.ret(0);
+    if (!dims_are(out, {d.N, d.H, d.Sq, d.D}) || out->dtype != f.arg(0)->dtype)
+        return bad(who, "result must be [N,H,Sq,D] of the input dtype");
+    float* lse = nullptr;
+    float scale = 0.f;
+    int64_t bq = 64, bk = 64;
+    if (!f.attr_f32("scale", &scale)) return bad(who, "missing f32 attribute 'scale'");
+    if (with_lse) {
+        const Buffer* l = f.ret(1);
+        if (!dims_are(l, {d.N, d.H, d.Sq}) || l->dtype != kF32)
+            return bad(who, "second result must be f32 [N,H,Sq]");
+        lse = static_cast<float*>(l->data);
+    } else {
+        if (!f.attr_i64("block_q", &bq) || !f.attr_i64("block_k", &bk))
+            return bad(who, "missing i64 attributes 'block_q', 'block_k'");
+    }
+    return clk_attention_fwd(f.stream(), static_cast<clk_dtype>(f.arg(0)->dtype), f.arg(0)->data,
+                             f.arg(1)->data, f.arg(2)->data, f.arg(3)->data,
+                             static_cast<const uint8_t*>(f.arg(4)->data), out->data, lse, d.N,
+                             d.H, d.Sq, d.Sk, d.D, scale, bq, bk);
+}
+
+clk_status attention_bwd(const Frame& f) {
+    const char* who = "ClkAttentionBwd";
+    AttnDims d;
+    clk_status s = decode_attention(who, f, &d);
+    if (s != CLK_OK) return s;
+    const DataType t = f.arg(0)->dtype;
+    const Buffer *out = f.arg(5), *dout = f.arg(6), *lse = f.arg(7);
+    if (!dims_are(out, {d.N, d.H, d.Sq, d.D}) || out->dtype != t ||
+        !dims_are(dout, {d.N, d.H, d.Sq, d.D}) || dout->dtype != t)
+        return bad(who, "out and dout must be [N,H,Sq,D] of the input dtype");
+    if (!dims_are(lse, {d.N, d.H, d.Sq}) || lse->dtype != kF32)
+        return bad(who, "lse must be f32 [N,H,Sq]");
+    const Buffer *dq = f.ret(0), *dk = f.ret(1), *dv = f.ret(2), *db = f.ret(3), *ws = f.ret(4);
+    if (!dims_are(dq, {d.N, d.H, d.Sq, d.D}) || dq->dtype != t ||
+        !dims_are(dk, {d.N, d.H, d.Sk, d.D}) || dk->dtype != t ||
+        !dims_are(dv, {d.N, d.H, d.Sk, d.D}) || dv->dtype != t)
+        return bad(who, "dq, dk, dv must match q, k, v");
+    if (!dims_are(db, {d.H, d.Sq, d.Sk}) || db->dtype != kF32)
+        return bad(who, "dbias must be f32 [H,Sq,Sk]");
+    if (!ws || ws->dtype != kU8) return bad(who, "fifth result must be the u8 workspace");
+    float scale;
+    if (!f.attr_f32("scale", &scale)) return bad(who, "missing f32 attribute 'scale'");
+    return clk_attention_bwd(f.stream(), static_cast<clk_dtype>(t), f.arg(0)->data,
+                             f.arg(1)->data, f.arg(2)->data, f.arg(3)->data,
+                             static_cast<const uint8_t*>(f.arg(4)->data), out->data, dout->data,
+                             static_cast<const float*>(lse->data), dq->data, dk->data, dv->data,
+                             static_cast<float*>(db->data), ws->data, (size_t)numel(ws), d.N, d.H,
+                             d.Sq, d.Sk, d.D, scale);
+}
+
+clk_status layer_norm_fwd(const Frame& f) {
+    const char* who = "VoltaLayerNorm";
+    const Buffer *x = f.arg(0), *sc = f.arg(1), *of = f.arg(2), *y = f.ret(0);
+    if (!x || !sc || !of || !y) return bad(who, "expects x, scale, offset -> y");
+    if (x->rank < 1) return bad(who, "x must be [M,C]");
+    const int64_t C = x->dims[x->rank - 1], M = C ? numel(x) / C : 0;
+    if (!dims_are(sc, {C}) || !dims_are(of, {C}) || sc->dtype != kF32 || of->dtype != kF32)
+        return bad(who, "scale and offset must be f32 [C]");
+    if (numel(y) != numel(x) || y->dtype != x->dtype) return bad(who, "y must match x");
+    float eps;
+    if (!f.attr_f32("eps", &eps)) return bad(who, "missing f32 attribute 'eps'");
+    return clk_layer_norm_fwd(f.stream(), static_cast<clk_dtype>(x->dtype), x->data,
+                              static_cast<const float*>(sc->data),
+                              static_cast<const float*>(of->data), y->data, M, C, eps);
+}
+
+clk_status layer_norm_bwd(const Frame& f) {
+    const char* who = "ClkLayerNormBwd";
+    const Buffer *x = f.arg(0), *sc = f.arg(1), *dy = f.arg(2);
+    const Buffer *dx = f.ret(0), *ds = f.ret(1), *dof = f.ret(2), *ws = f.ret(3);
+    if (!x || !sc || !dy || !dx || !ds || !dof || !ws)
+        return bad(who, "expects x, scale, dy -> dx, dscale, doffset, workspace");
+    if (x->rank < 1) return bad(who, "x must be [M,C]");
+    const int64_t C = x->dims[x->rank - 1], M = C ? numel(x) / C : 0;
+    if (!dims_are(sc, {C}) || sc->dtype != kF32) return bad(who, "scale must be f32 [C]");
+    if (numel(dy) != numel(x) || dy->dtype != x->dtype || numel(dx) != numel(x) ||
+        dx->dtype != x->dtype)
+        return bad(who, "dy and dx must match x");
+    if (!dims_are(ds, {C}) || !dims_are(dof, {C}) || ds->dtype != kF32 || dof->dtype != kF32)
+        return bad(who, "dscale and doffset must be f32 [C]");
+    if (ws->dtype != kU8) return bad(who, "fourth result must be the u8 workspace");
+    float eps;
+    if (!f.attr_f32("eps", &eps)) return bad(who, "missing f32 attribute 'eps'");
+    return clk_layer_norm_bwd(f.stream(), static_cast<clk_dtype>(x->dtype), x->data,
+                              static_cast<const float*>(sc->data), dy->data, dx->data,
+                              static_cast<float*>(ds->data), static_cast<float*>(dof->data),
+                              ws->data, (size_t)numel(ws), M, C, eps);
+}
+
+clk_status gdp(const char* who, const Frame& f) {
+    const Buffer *x = f.arg(0), *wp = f.arg(1), *bp = f.arg(2), *wg = f.arg(3), *bg = f.arg(4),
+                 *mask = f.arg(5), *out = f.ret(0);
+    if (!x || !wp || !bp || !wg || !bg || !mask || !out)
+        return bad(who, "expects x, wp, bp, wg, bg, mask -> out");
+    if (x->rank != 2) return bad(who, "x must be [M,K]");
+    const int64_t M = x->dims[0], K = x->dims[1];
+    if (wp->rank != 2 || wp->dims[0] != K) return bad(who, "wp must be [K,N]");
+    const int64_t N = wp->dims[1];
+    if (!dims_are(wg, {K, N}) || !dims_are(bp, {N}) || !dims_are(bg, {N}) ||
+        !dims_are(mask, {M}) || !dims_are(out, {M, N}))
+        return bad(who, "wg [K,N], bp, bg [N], mask [M], out [M,N] expected");
+    const DataType t = x->dtype;
+    if (!half_type(t) || wp->dtype != t || bp->dtype != t || wg->dtype != t || bg->dtype != t ||
+        mask->dtype != t || out->dtype != t)
+        return bad(who, "all operands must be f16 or all bf16");
+    return clk_gated_dual_proj(f.stream(), static_cast<clk_dtype>(t), x->data, wp->data,
+                               bp->data, wg->data, bg->data, mask->data, out->data, M, K, N);
+}
+
+clk_status ln_gdp(const Frame& f) {
+    const char* who = "ClkLnGdp";
+    if (f.nargs() != 12 || f.nrets() != 2)
+        return bad(who, "expects 12 operands (z, ln_scale, ln_offset, 8 weights/biases, mask) "
+                        "and 2 results");
+    const Buffer* z = f.arg(0);
+    const Buffer *sc = f.arg(1), *of = f.arg(2), *mask = f.arg(11), *a = f.ret(0), *b = f.ret(1);
+    if (!z || !sc || !of || !mask || !a || !b) return bad(who, "operands must be buffers");
+    if (z->rank < 1) return bad(who, "z must be [M,C]");
+    const int64_t C = z->dims[z->rank - 1], M = C ? numel(z) / C : 0;
+    if (!dims_are(sc, {C}) || !dims_are(of, {C}) || sc->dtype != kF32 || of->dtype != kF32)
+        return bad(who, "ln_scale and ln_offset must be f32 [C]");
+    const Buffer* w[4] = {f.arg(3), f.arg(5), f.arg(7), f.arg(9)};
+    const Buffer* bias[4] = {f.arg(4), f.arg(6), f.arg(8), f.arg(10)};
+    if (!w[0] || w[0]->rank != 2 || w[0]->dims[0] != C) return bad(who, "weights must be [C,N]");
+    const int64_t N = w[0]->dims[1];
+    const DataType t = z->dtype;
+    if (!half_type(t)) return bad(who, "z must be f16 or bf16");
+    for (int i = 0; i < 4; ++i) {
+        if (!dims_are(w[i], {C, N}) || w[i]->dtype != t) return bad(who, "weights must be [C,N]");
+        if (!dims_are(bias[i], {N}) || bias[i]->dtype != t) return bad(who, "biases must be [N]");
+    }
+    if (numel(mask) != M || mask->dtype != t) return bad(who, "mask must have M elements");
+    if (numel(a) != M * N || numel(b) != M * N || a->dtype != t || b->dtype != t)
+        return bad(who, "a and b must be [M,N]");
+    float eps;
+    if (!f.attr_f32("eps", &eps)) return bad(who, "missing f32 attribute 'eps'");
+    return clk_ln_gated_dual_proj(f.stream(), static_cast<clk_dtype>(t), z->data,
+                                  static_cast<const float*>(sc->data),
+                                  static_cast<const float*>(of->data), w[0]->data, bias[0]->data,
+                                  w[1]->data, bias[1]->data, w[2]->data, bias[2]->data,
+                                  w[3]->data, bias[3]->data, mask->data, a->data, b->data, M, C,
+                                  N, eps);
+}
+
+}  // namespace
+
+#define CLK_FFI_EXPORT extern "C" __attribute__((visibility("default")))
+
+CLK_FFI_EXPORT Error* VoltaMma(CallFrame* frame) {
+    return run(frame, [](const Frame& f) { return attention_fwd("VoltaMma", f, false); });
+}
+CLK_FFI_EXPORT Error* VoltaWmma(CallFrame* frame) {
+    return run(frame, [](const Frame& f) { return attention_fwd("VoltaWmma", f, false); });
+}
+CLK_FFI_EXPORT Error* ClkAttentionFwd(CallFrame* frame) {
+    return run(frame, [](const Frame& f) { return attention_fwd("ClkAttentionFwd", f, true); });
+}
+CLK_FFI_EXPORT Error* ClkAttentionBwd(CallFrame* frame) {
+    return run(frame, [](const Frame& f) { return attention_bwd(f); });
+}
+CLK_FFI_EXPORT Error* VoltaLayerNorm(CallFrame* frame) {
+    return run(frame, [](const Frame& f) { return layer_norm_fwd(f); });
+}
+CLK_FFI_EXPORT Error* ClkLayerNormBwd(CallFrame* frame) {
+    return run(frame, [](const Frame& f) { return layer_norm_bwd(f); });
+}
+CLK_FFI_EXPORT Error* VoltaGdp(CallFrame* frame) {
+    return run(frame, [](const Frame& f) { return gdp("VoltaGdp", f); });
+}
+CLK_FFI_EXPORT Error* VoltaGdpWmma(CallFrame* frame) {
+    return run(frame, [](const Frame& f) { return gdp("VoltaGdpWmma", f); });
+}
+CLK_FFI_EXPORT Error* ClkLnGdp(CallFrame* frame) {
+    return run(frame, [](const Frame& f) { return ln_gdp(f); });
+}

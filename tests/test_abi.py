@@ -1,0 +1,129 @@
+"""The C ABI library on the CPU: it loads, exports every symbol include/clk.h declares and every
+XLA FFI target the locator names, and rejects invalid calls before any GPU work. No kernel runs
+here (this machine may have no GPU): every call below fails host-side validation."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+import colabfold_legacy_kernels as clk
+from colabfold_legacy_kernels import _native
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "clk.h"
+
+pytestmark = pytest.mark.skipif(not clk.available("gfx950"),
+                                reason="library not built (run __graft_entry__.build())")
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(clk_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported():
+    lib = ctypes.CDLL(clk.library_path("attention", "gfx950"))
+    names = declared_functions()
+    assert len(names) >= 12, names
+    for name in names:
+        getattr(lib, name)
+    assert set(names) == set(_native.PROTOTYPES), "ctypes prototypes out of sync with clk.h"
+
+
+def test_every_ffi_target_is_exported():
+    for kernel in clk.KERNELS:
+        lib = ctypes.CDLL(clk.library_path(kernel, "gfx950"))
+        getattr(lib, clk.symbol(kernel, "gfx950"))
+    lib = ctypes.CDLL(clk.library_path("attention", "gfx950"))
+    for alias in ("VoltaWmma", "VoltaGdpWmma"):  # the reference's sm_70 target names
+        getattr(lib, alias)
+
+
+def test_version_and_last_error():
+    lib = _native.lib()
+    assert b"gfx950" in lib.clk_version()
+    assert isinstance(lib.clk_last_error(), bytes)
+
+
+def test_profile_hooks_without_launches():
+    lib = _native.lib()
+    lib.clk_profile_enable(1)
+    lib.clk_profile_enable(0)
+    assert _native.collect() == []
+
+
+INVALID = _native.INVALID_ARGUMENT
+BF16, F16, F32, U8 = _native.BF16, _native.F16, _native.F32, _native.U8
+FAKE = 0x100000  # a non-null, 16-byte aligned address that is never dereferenced
+
+
+def attn_fwd(**kw):
+    a = dict(stream=None, dtype=BF16, q=FAKE, k=FAKE, v=FAKE, bias=FAKE, kmask=FAKE, out=FAKE,
+             lse=None, N=2, H=2, Sq=16, Sk=16, D=32, scale=0.17, bq=64, bk=64)
+    a.update(kw)
+    return _native.lib().clk_attention_fwd(*a.values())
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(D=24), "head dim"), (dict(D=128), "head dim"), (dict(dtype=F32), "dtype"),
+    (dict(dtype=U8), "dtype"), (dict(N=-1), "negative"), (dict(q=None), "null"),
+    (dict(out=FAKE + 8), "aligned"), (dict(bq=0), "positive"), (dict(N=70000), "too large"),
+])
+def test_attention_fwd_validation(kw, msg):
+    assert attn_fwd(**kw) == INVALID
+    assert msg in _native.last_error()
+
+
+def test_attention_fwd_empty_is_ok():
+    assert attn_fwd(N=0) == _native.OK
+    assert attn_fwd(Sq=0) == _native.OK
+
+
+def test_attention_bwd_validation():
+    lib = _native.lib()
+    ws = lib.clk_attention_bwd_workspace_size(384, 4, 384, 384, 32)
+    assert ws > 384 * 4 * 384 * 4  # at least the D_i row sums
+    args = [None, BF16] + [FAKE] * 5 + [FAKE, FAKE, FAKE] + [FAKE] * 4 + [FAKE, ws - 1,
+                                                                         384, 4, 384, 384, 32, 0.17]
+    assert lib.clk_attention_bwd(*args) == INVALID
+    assert "workspace" in _native.last_error()
+    args[-7] = ws
+    args[-2] = 12
+    assert lib.clk_attention_bwd(*args) == INVALID
+    assert "head dim" in _native.last_error()
+
+
+def test_workspace_sizes_are_deterministic():
+    lib = _native.lib()
+    a = lib.clk_attention_bwd_workspace_size(384, 4, 384, 384, 32)
+    assert a == lib.clk_attention_bwd_workspace_size(384, 4, 384, 384, 32)
+    assert lib.clk_attention_bwd_workspace_size(-1, 4, 8, 8, 32) == 0
+    assert lib.clk_layer_norm_bwd_workspace_size(512 * 512, 128) > 0
+    assert lib.clk_layer_norm_bwd_workspace_size(0, 128) == 0
+
+
+def test_layer_norm_validation():
+    lib = _native.lib()
+    assert lib.clk_layer_norm_fwd(None, U8, FAKE, FAKE, FAKE, FAKE, 4, 128, 1e-5) == INVALID
+    assert lib.clk_layer_norm_fwd(None, BF16, FAKE, FAKE, FAKE, FAKE, 4, 0, 1e-5) == INVALID
+    assert lib.clk_layer_norm_fwd(None, BF16, None, FAKE, FAKE, FAKE, 4, 128, 1e-5) == INVALID
+    assert lib.clk_layer_norm_fwd(None, BF16, FAKE, FAKE, FAKE, FAKE, 0, 128, 1e-5) == _native.OK
+    assert lib.clk_layer_norm_bwd(None, BF16, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 0, 4, 128,
+                                  1e-5) == INVALID
+
+
+@pytest.mark.parametrize("m,k,n,msg", [(4, 128, 12, "multiple of 8"), (4, 12, 64, "multiple of 8"),
+                                       (4, 1024, 64, "above 512"), (-1, 8, 8, "bad dims")])
+def test_gdp_validation(m, k, n, msg):
+    lib = _native.lib()
+    assert lib.clk_gated_dual_proj(None, BF16, *([FAKE] * 7), m, k, n) == INVALID
+    assert msg in _native.last_error()
+
+
+@pytest.mark.parametrize("c,n", [(100, 128), (128, 160), (256, 128), (16, 32)])
+def test_ln_gdp_validation(c, n):
+    lib = _native.lib()
+    assert lib.clk_ln_gated_dual_proj(None, BF16, *([FAKE] * 14), 4, c, n, 1e-5) == INVALID
+    assert "multiples of 32" in _native.last_error()

@@ -1,0 +1,119 @@
+"""XLA FFI handlers driven by a fake XLA runtime (tests/_xla_ffi.py) on the CPU: the metadata
+query, non-execute stages, and every decode/validation error path (no kernel is launched).
+tests/test_gpu_ffi.py runs the same handlers on device buffers."""
+import ctypes
+
+import pytest
+
+import colabfold_legacy_kernels as clk
+from _xla_ffi import BF16, F16, F32, F64, S32, S64, U8, FakeXla, Metadata, MetadataExtension, \
+    ExtensionBase, ApiVersion
+
+pytestmark = pytest.mark.skipif(not clk.available("gfx950"), reason="library not built")
+
+TARGETS = ["VoltaMma", "VoltaWmma", "ClkAttentionFwd", "ClkAttentionBwd", "VoltaLayerNorm",
+           "ClkLayerNormBwd", "VoltaGdp", "VoltaGdpWmma", "ClkLnGdp"]
+FAKE = 0x100000
+
+
+@pytest.fixture
+def lib():
+    return ctypes.CDLL(clk.library_path("attention", "gfx950"))
+
+
+@pytest.mark.parametrize("name", TARGETS)
+def test_metadata_query(lib, name):
+    x = FakeXla()
+    md = Metadata(ctypes.sizeof(Metadata), ApiVersion(), 0)
+    ext = MetadataExtension(ExtensionBase(ctypes.sizeof(MetadataExtension), 1, None),
+                            ctypes.pointer(md))
+    fr = x.frame([], [], extension=ext)
+    assert x.call(lib, name, fr) is None
+    assert (md.api_version.major_version, md.api_version.minor_version) == (0, 1)
+    assert md.traits == 1  # command-buffer compatible
+    assert x.errors == []
+
+
+@pytest.mark.parametrize("name", TARGETS)
+def test_non_execute_stages_do_nothing(lib, name):
+    x = FakeXla()
+    for stage in (0, 1, 2):
+        assert x.call(lib, name, x.frame([], [], stage=stage)) is None
+    assert x.errors == []
+
+
+def attention_frame(x, n=2, h=2, sq=16, sk=16, d=32, dt=BF16, mask_dt=U8, bias_shape=None,
+                    out_dt=None, attrs=None):
+    args = [x.buffer(dt, (n, h, sq, d), FAKE), x.buffer(dt, (n, h, sk, d), FAKE),
+            x.buffer(dt, (n, h, sk, d), FAKE), x.buffer(dt, bias_shape or (h, sq, sk), FAKE),
+            x.buffer(mask_dt, (n, sk), FAKE)]
+    rets = [x.buffer(out_dt or dt, (n, h, sq, d), FAKE)]
+    if attrs is None:
+        attrs = [("block_k", S64, 64), ("block_q", S64, 64), ("scale", F32, 0.17)]
+    return x.frame(args, rets, attrs)
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(d=24), "head dim"), (dict(dt=F32), "f16 or all bf16"),
+    (dict(mask_dt=BF16), "kmask"), (dict(bias_shape=(2, 16, 8)), "bias"),
+    (dict(out_dt=F16), "result"), (dict(attrs=[("scale", F32, 0.1)]), "block_q"),
+    (dict(attrs=[("block_q", S32, 64), ("block_k", S32, 64)]), "scale"),
+])
+def test_volta_mma_rejects(lib, kw, msg):
+    x = FakeXla()
+    err = x.call(lib, "VoltaMma", attention_frame(x, **kw))
+    assert err is not None
+    code, text = x.errors[-1]
+    assert code == 3 and msg in text, text
+
+
+def test_attention_attribute_types(lib):
+    """f64 scale and i32 block sizes are accepted (decode), then the fake addresses fail the
+    alignment-free empty-batch path: N = 0 returns OK without a launch."""
+    x = FakeXla()
+    fr = attention_frame(x, n=0, attrs=[("scale", F64, 0.17), ("block_q", S32, 32),
+                                        ("block_k", S32, 32)])
+    assert x.call(lib, "VoltaMma", fr) is None, x.errors
+
+
+def test_layer_norm_rejects(lib):
+    x = FakeXla()
+    fr = x.frame([x.buffer(BF16, (4, 128), FAKE), x.buffer(BF16, (128,), FAKE),
+                  x.buffer(F32, (128,), FAKE)], [x.buffer(BF16, (4, 128), FAKE)],
+                 [("eps", F32, 1e-5)])
+    assert x.call(lib, "VoltaLayerNorm", fr) is not None
+    assert "scale and offset must be f32" in x.errors[-1][1]
+    fr = x.frame([x.buffer(BF16, (4, 128), FAKE), x.buffer(F32, (128,), FAKE),
+                  x.buffer(F32, (128,), FAKE)], [x.buffer(BF16, (4, 128), FAKE)], [])
+    assert x.call(lib, "VoltaLayerNorm", fr) is not None
+    assert "eps" in x.errors[-1][1]
+
+
+def test_gdp_rejects_n_not_multiple_of_8(lib):
+    x = FakeXla()
+    m, k, n = 4, 128, 12
+    fr = x.frame([x.buffer(BF16, (m, k), FAKE), x.buffer(BF16, (k, n), FAKE),
+                  x.buffer(BF16, (n,), FAKE), x.buffer(BF16, (k, n), FAKE),
+                  x.buffer(BF16, (n,), FAKE), x.buffer(BF16, (m,), FAKE)],
+                 [x.buffer(BF16, (m, n), FAKE)])
+    assert x.call(lib, "VoltaGdp", fr) is not None
+    assert x.errors[-1][0] == 3 and "multiple of 8" in x.errors[-1][1]
+
+
+def test_attention_bwd_rejects_small_workspace(lib):
+    x = FakeXla()
+    n, h, s, d = 2, 2, 16, 32
+    q = lambda: x.buffer(BF16, (n, h, s, d), FAKE)  # noqa: E731
+    args = [q(), q(), q(), x.buffer(BF16, (h, s, s), FAKE), x.buffer(U8, (n, s), FAKE), q(), q(),
+            x.buffer(F32, (n, h, s), FAKE)]
+    rets = [q(), q(), q(), x.buffer(F32, (h, s, s), FAKE), x.buffer(U8, (1,), FAKE)]
+    assert x.call(lib, "ClkAttentionBwd", x.frame(args, rets, [("scale", F32, 0.17)])) is not None
+    assert "workspace" in x.errors[-1][1]
+
+
+def test_ln_gdp_operand_count(lib):
+    x = FakeXla()
+    fr = x.frame([x.buffer(BF16, (4, 128), FAKE)], [x.buffer(BF16, (4, 128), FAKE)],
+                 [("eps", F32, 1e-5)])
+    assert x.call(lib, "ClkLnGdp", fr) is not None
+    assert "12 operands" in x.errors[-1][1]

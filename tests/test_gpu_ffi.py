@@ -1,0 +1,96 @@
+"""The XLA FFI targets run on device buffers through a fake XLA runtime and agree bit-for-bit with
+the C ABI calls they forward to (and hence with the oracle-checked results of the other tests)."""
+import ctypes
+
+import pytest
+import torch
+
+import colabfold_legacy_kernels as clk
+from colabfold_legacy_kernels import ops
+from colabfold_legacy_kernels.workloads import attention_inputs, gdp_weights, layer_norm_inputs
+from _xla_ffi import BF16, F32, S64, U8, FakeXla
+
+pytestmark = pytest.mark.gpu
+
+DT = {torch.bfloat16: BF16, torch.float32: F32, torch.uint8: U8}
+
+
+def buf(x, t):
+    return x.buffer(DT[t.dtype], tuple(t.shape), t.data_ptr())
+
+
+def lib_and_runtime(dev):
+    lib = ctypes.CDLL(clk.library_path("attention", "gfx950"))
+    return lib, FakeXla(stream=torch.cuda.current_stream(dev).cuda_stream)
+
+
+def test_volta_mma_and_attention_bwd_targets(cuda):
+    lib, x = lib_and_runtime(cuda)
+    inp = attention_inputs(3, 2, 100, 90, 32, torch.bfloat16, seed=8, device=cuda,
+                           masked_tail=0.1, masked_rows=1)
+    q, k, v, bias, km, dout = (inp[n] for n in ("q", "k", "v", "bias", "kmask", "dout"))
+    out = torch.empty_like(q)
+    fr = x.frame([buf(x, q), buf(x, k), buf(x, v), buf(x, bias), buf(x, km)], [buf(x, out)],
+                 [("scale", F32, inp["scale"]), ("block_q", S64, 64), ("block_k", S64, 64)])
+    assert x.call(lib, "VoltaMma", fr) is None, x.errors
+    ref_out, ref_lse = ops.attention_fwd(q, k, v, bias, km, inp["scale"])
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref_out)
+
+    out2 = torch.empty_like(q)
+    lse = torch.empty_like(ref_lse)
+    fr = x.frame([buf(x, q), buf(x, k), buf(x, v), buf(x, bias), buf(x, km)],
+                 [buf(x, out2), buf(x, lse)], [("scale", F32, inp["scale"])])
+    assert x.call(lib, "ClkAttentionFwd", fr) is None, x.errors
+    torch.cuda.synchronize()
+    assert torch.equal(out2, ref_out) and torch.equal(lse, ref_lse)
+
+    n, h, sq, d = q.shape
+    sk = k.shape[2]
+    ws = torch.empty(lib.clk_attention_bwd_workspace_size(n, h, sq, sk, d), device=cuda,
+                     dtype=torch.uint8)
+    grads = [torch.empty_like(q), torch.empty_like(k), torch.empty_like(v),
+             torch.empty((h, sq, sk), device=cuda, dtype=torch.float32)]
+    fr = x.frame([buf(x, t) for t in (q, k, v, bias, km, ref_out, dout, ref_lse)],
+                 [buf(x, t) for t in grads] + [buf(x, ws)], [("scale", F32, inp["scale"])])
+    assert x.call(lib, "ClkAttentionBwd", fr) is None, x.errors
+    ref = ops.attention_bwd(q, k, v, bias, km, ref_out, dout, ref_lse, inp["scale"])
+    torch.cuda.synchronize()
+    for a, b in zip(grads, ref):
+        assert torch.equal(a, b)
+
+
+def test_layer_norm_and_gdp_targets(cuda):
+    lib, x = lib_and_runtime(cuda)
+    li = layer_norm_inputs(500, 128, torch.bfloat16, seed=2, device=cuda)
+    y = torch.empty_like(li["x"])
+    fr = x.frame([buf(x, li["x"]), buf(x, li["scale"]), buf(x, li["offset"])], [buf(x, y)],
+                 [("eps", F32, 1e-5)])
+    assert x.call(lib, "VoltaLayerNorm", fr) is None, x.errors
+    assert torch.equal(y, ops.layer_norm(li["x"], li["scale"], li["offset"], 1e-5))
+
+    dx, ds, do = (torch.empty_like(li["x"]), torch.empty(128, device=cuda),
+                  torch.empty(128, device=cuda))
+    ws = torch.empty(lib.clk_layer_norm_bwd_workspace_size(500, 128), device=cuda,
+                     dtype=torch.uint8)
+    fr = x.frame([buf(x, li["x"]), buf(x, li["scale"]), buf(x, li["dy"])],
+                 [buf(x, dx), buf(x, ds), buf(x, do), buf(x, ws)], [("eps", F32, 1e-5)])
+    assert x.call(lib, "ClkLayerNormBwd", fr) is None, x.errors
+    for a, b in zip((dx, ds, do), ops.layer_norm_bwd(li["x"], li["scale"], li["dy"], 1e-5)):
+        assert torch.equal(a, b)
+
+    wp, bp, wg, bg = gdp_weights(128, 128, torch.bfloat16, seed=4, device=cuda, bias_std=0.1)
+    out = torch.empty_like(y)
+    fr = x.frame([buf(x, t) for t in (y, wp, bp, wg, bg, li["mask"])], [buf(x, out)])
+    assert x.call(lib, "VoltaGdp", fr) is None, x.errors
+    assert torch.equal(out, ops.gated_dual_proj(y, wp, bp, wg, bg, li["mask"]))
+
+    wb = gdp_weights(128, 128, torch.bfloat16, seed=5, device=cuda, bias_std=0.1)
+    a, b = torch.empty_like(y), torch.empty_like(y)
+    fr = x.frame([buf(x, t) for t in (li["x"], li["scale"], li["offset"], wp, bp, wg, bg) + wb
+                  + (li["mask"],)], [buf(x, a), buf(x, b)], [("eps", F32, 1e-5)])
+    assert x.call(lib, "ClkLnGdp", fr) is None, x.errors
+    ra, rb = ops.ln_gated_dual_proj(li["x"], li["scale"], li["offset"], (wp, bp, wg, bg), wb,
+                                    li["mask"])
+    torch.cuda.synchronize()
+    assert torch.equal(a, ra) and torch.equal(b, rb)
