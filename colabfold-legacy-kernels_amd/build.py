@@ -64,6 +64,20 @@ def _asm(src):
     return out
 
 
+def check_ffi_layout(verbose=True):
+    """Static-assert csrc/xla_ffi_abi.h against XLA's c_api.h when FFI_INCLUDE names it."""
+    inc = os.environ.get("FFI_INCLUDE", "")
+    if not inc or not (Path(inc) / "xla" / "ffi" / "api" / "c_api.h").is_file():
+        if verbose:
+            print("ffi layout check skipped (FFI_INCLUDE does not hold xla/ffi/api/c_api.h)")
+        return False
+    _run([HIPCC, "-std=c++17", "-fsyntax-only", "-I" + inc, "-I" + str(CSRC),
+          str(CSRC / "xla_ffi_layout_check.cc")])
+    if verbose:
+        print("ffi layout check passed against", inc)
+    return True
+
+
 def build(jobs=None, asm=False, verbose=True):
     """Compile and link; returns the library path."""
     BUILD.mkdir(exist_ok=True)
@@ -80,6 +94,7 @@ def build(jobs=None, asm=False, verbose=True):
     os.replace(tmp, LIB)
     if verbose:
         print("built %s (%d units)" % (LIB, len(objs)))
+    check_ffi_layout(verbose)
     return LIB
 
 
