@@ -167,6 +167,74 @@ __device__ __forceinline__ float masked_logit_for_row(const uint8_t* mrow, int S
     return (mrow && !any) ? 0.f : kMaskedLogit;
 }
 
+// ---------------------------------------------------------------------------------------------
+// Swizzled LDS tiles filled with direct global->LDS loads (global_load_lds_dwordx4: lane i of a
+// wave instruction writes 16 bytes at the instruction's LDS base + 16*i).
+//
+// A tile row holds PL 16-byte pieces (PL = DV/8 >= 2; pieces past D/8 are zero padding used by
+// the transposed reads of D = 8). Logical piece p of row r sits in physical slot p ^ swz(r),
+// swz(r) = (r >> 3) & (PL - 1): the row reads of a 16-key operand (keys 8j + 0..3) and the 4x16
+// transposed reads then touch distinct bank groups.
+// ---------------------------------------------------------------------------------------------
+__device__ __attribute__((aligned(16))) const unsigned int kZero16[4] = {0u, 0u, 0u, 0u};
+
+template <int D>
+struct SwzTile {
+    static constexpr int DV = AttnGeom<D>::DV;
+    static constexpr int PL = DV / 8;
+    static constexpr int P = D / 8;
+    static constexpr int ROWB = PL * 16;
+    static __device__ __forceinline__ int swz(int row) { return (row >> 3) & (PL - 1); }
+    static __device__ __forceinline__ int off(int row, int piece) {
+        return row * ROWB + 16 * (piece ^ swz(row));
+    }
+};
+
+// Issues async loads of rows [g0, g0 + ROWS) of a row-major [S, D] tensor into a swizzled LDS
+// tile (rows past S and padding pieces read zeros). ROWS*PL must be a multiple of 64. Every thread
+// of the block calls it; completion is awaited with async_wait() before a barrier.
+template <int D, int ROWS, int NTHREADS, typename E>
+__device__ __forceinline__ void stage_rows_async(const E* src, int g0, int S, char* lds) {
+    using T = SwzTile<D>;
+    constexpr int SLOTS = ROWS * T::PL;
+    static_assert(SLOTS % 64 == 0, "tile must be whole wave instructions");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int base = wave * 64; base < SLOTS; base += NTHREADS) {
+        const int slot = base + lane;
+        const int row = slot / T::PL;
+        const int piece = (slot % T::PL) ^ T::swz(row);
+        const void* g = kZero16;
+        if (g0 + row < S && piece < T::P) g = src + (size_t)(g0 + row) * D + piece * 8;
+        __builtin_amdgcn_global_load_lds(
+            g, (__attribute__((address_space(3))) void*)(lds + base * 16), 16, 0, 0);
+    }
+}
+
+// Waits for this thread's outstanding global loads (including async LDS fills).
+__device__ __forceinline__ void async_wait() { __builtin_amdgcn_s_waitcnt(0); }
+
+// Row operand from a swizzled tile: row `row`, head dims 32*ks + 8*g + 0..7 (zero beyond D).
+template <typename V8, int D>
+__device__ __forceinline__ V8 swz_row_operand(const char* lds, int row, int ks, int g) {
+    const int piece = ks * 4 + g;
+    u32x4 raw = {0u, 0u, 0u, 0u};
+    if (piece * 8 < D) raw = *reinterpret_cast<const u32x4*>(lds + SwzTile<D>::off(row, piece));
+    return bits_as<V8>(raw);
+}
+
+// Transposed operand from a swizzled tile: lane (r16, g) gets column 16*dt + r16 of rows
+// rbase + 8g + 0..7 (rbase = 32*chunk).
+template <typename V8, int D>
+__device__ __forceinline__ V8 swz_tr_operand(const char* lds, int rbase, int dt, int r16, int g) {
+    const int row = rbase + 8 * g + (r16 >> 2);
+    const int col = 16 * dt + 4 * (r16 & 3);  // element column, a multiple of 4
+    const int piece = col >> 3, inner = (col & 7) * 2;
+    const char* lo = lds + SwzTile<D>::off(row, piece) + inner;
+    const char* hi = lds + SwzTile<D>::off(row + 4, piece) + inner;
+    return lds_tr8<V8>(lo, hi);
+}
+
 template <typename TR>
 __device__ __forceinline__ void store4(typename TR::elem* p, f32x4 v) {
     using E = typename TR::elem;

@@ -3,8 +3,10 @@
 // 47-311) with one kernel for f16 and bf16 on MFMA 16x16x32 with float32 accumulation.
 //
 // Work split: a block of 4 waves owns (query tile of 64*QT rows, head h, row n); each wave owns
-// 16*QT queries and streams the keys in tiles of 64 through LDS (K row-major, V row-major, both
-// double-staged through registers so the next tile's global loads overlap this tile's math).
+// 16*QT queries and streams the keys in tiles of 64 through double-buffered LDS: tile kt+1 is
+// fetched with direct global->LDS loads (and its bias rows into registers) while tile kt is
+// computed, so each tile costs one barrier. Which tiles contain an absent key is worked out once
+// per block from the mask row; the others skip the mask entirely.
 //
 // Per 64-key tile and 16-query sub-tile a wave computes S^T = K . Q^T with the keys of each
 // 32-key chunk permuted so that lane l's accumulator holds keys 8*(l/16)+0..7 of the chunk for
@@ -26,20 +28,83 @@
 namespace clk {
 namespace {
 
-template <typename TR, int D, int QT>
+// Per-tile "some key absent or past Sk" flags of one mask row, for up to kMaxFlagTiles tiles of
+// 64 keys (beyond that every tile takes the checked path). Also returns the row's masked logit.
+constexpr int kMaxFlagTiles = 128;
+
+__device__ __forceinline__ float tile_flags(const uint8_t* mrow, int Sk, int* flags) {
+    const int ntiles = (Sk + 63) / 64;
+    for (int t = threadIdx.x; t < kMaxFlagTiles; t += blockDim.x)
+        flags[t] = (t >= ntiles || 64 * (t + 1) > Sk) ? 1 : 0;
+    __syncthreads();
+    int any = 0;
+    if (mrow) {
+        for (int i = threadIdx.x; i < Sk; i += blockDim.x) {
+            const bool present = mrow[i] != 0;
+            any |= present;
+            if (!present && i / 64 < kMaxFlagTiles) flags[i / 64] = 1;
+        }
+    }
+    any = __syncthreads_or(any);
+    return (mrow && !any) ? 0.f : kMaskedLogit;
+}
+
+// Eight consecutive keys' bias values and mask bytes of one tile, as loaded. VEC: 16-byte bias
+// and 8-byte mask loads (Sk % 8 == 0, 8-byte aligned mask rows); a lane whose eight keys lie past
+// Sk reads the last eight instead (those keys are forced to -inf). Otherwise element loads.
+template <typename TR, bool VEC>
+struct KeyChunk {
+    u32x4 bias;
+    u32x2 mask;
+    __device__ __forceinline__ void load(const typename TR::elem* brow, const uint8_t* mrow,
+                                         int kk, int Sk) {
+        using E = typename TR::elem;
+        if constexpr (VEC) {
+            const int kc = min(kk, Sk - 8);
+            bias = ld16(brow + kc);
+            mask = mrow ? *reinterpret_cast<const u32x2*>(mrow + kc) : u32x2{~0u, ~0u};
+        } else {
+            E e[8];
+            uint8_t m[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const bool in = kk + j < Sk;
+                e[j] = in ? brow[kk + j] : E(0.f);
+                m[j] = in ? (mrow ? mrow[kk + j] : uint8_t(1)) : uint8_t(0);
+            }
+            __builtin_memcpy(&bias, e, 16);
+            __builtin_memcpy(&mask, m, 8);
+        }
+    }
+    // Bit j set when key kk + j is present.
+    __device__ __forceinline__ unsigned valid() const {
+        unsigned bits = 0;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            bits |= (((mask[0] >> (8 * j)) & 0xffu) != 0u ? 1u : 0u) << j;
+            bits |= (((mask[1] >> (8 * j)) & 0xffu) != 0u ? 1u : 0u) << (4 + j);
+        }
+        return bits;
+    }
+};
+
+template <typename TR, int D, int QT, bool VEC>
 __global__ __launch_bounds__(256) void attn_fwd_kernel(
     const typename TR::elem* __restrict__ q, const typename TR::elem* __restrict__ k,
     const typename TR::elem* __restrict__ v, const typename TR::elem* __restrict__ bias,
     const uint8_t* __restrict__ kmask, typename TR::elem* __restrict__ out,
-    float* __restrict__ lse, int H, int Sq, int Sk, float scale, int vec_ok) {
+    float* __restrict__ lse, int H, int Sq, int Sk, float scale) {
     using E = typename TR::elem;
     using V8 = typename TR::vec8;
     using G = AttnGeom<D>;
+    using T = SwzTile<D>;
+    using KC = KeyChunk<TR, VEC>;
     constexpr int BQ = 4 * 16 * QT;
     constexpr int BK = G::BK;
+    constexpr int TILE = BK * T::ROWB;  // bytes of one K or V tile
 
-    __shared__ __attribute__((aligned(16))) E k_lds[BK * G::KLD];
-    __shared__ __attribute__((aligned(16))) E v_lds[BK * G::VLD];
+    __shared__ __attribute__((aligned(16))) char kv_lds[2][2][TILE];  // [buffer][K, V]
+    __shared__ int flags[kMaxFlagTiles];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r16 = lane & 15, g = lane >> 4;
@@ -51,9 +116,13 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
     const E* bp = bias + (size_t)h * Sq * Sk;
     const uint8_t* mp = kmask ? kmask + (size_t)n * Sk : nullptr;
     const int qbase = q0 + wave * 16 * QT;
+    const int ntiles = (Sk + BK - 1) / BK;
 
-    zero_v_padding<E, D>(v_lds);
-    const float masked_logit = masked_logit_for_row(mp, Sk);
+    if (ntiles > 0) {
+        stage_rows_async<D, BK, 256>(kp, 0, Sk, kv_lds[0][0]);
+        stage_rows_async<D, BK, 256>(vp, 0, Sk, kv_lds[0][1]);
+    }
+    const float masked_logit = tile_flags(mp, Sk, flags);
 
     // B operand Q^T: lane (query r16, group g) holds head dims 32*ks + 8*g + 0..7.
     V8 qf[QT][G::KS];
@@ -69,6 +138,19 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
         }
     }
 
+    // Bias rows of the lane's queries (clamped inside [0, Sq)), keys 32c + 8g + 0..7 per tile.
+    const E* brow[QT];
+#pragma unroll
+    for (int qt = 0; qt < QT; ++qt) brow[qt] = bp + (size_t)min(qbase + qt * 16 + r16, Sq - 1) * Sk;
+    KC cur[QT][2], nxt[QT][2];
+    auto load_chunks = [&](int k0, KC (&kc)[QT][2]) {
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) kc[qt][c].load(brow[qt], mp, k0 + 32 * c + 8 * g, Sk);
+    };
+    if (ntiles > 0) load_chunks(0, cur);
+
     float m_run[QT], l_run[QT];
     f32x4 acc[QT][G::DT];
 #pragma unroll
@@ -79,76 +161,69 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
         for (int dt = 0; dt < G::DT; ++dt) acc[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    TileStager<E, D> stage;
-    const int ntiles = (Sk + BK - 1) / BK;
-    if (ntiles > 0) stage.load(kp, vp, 0, Sk);
     for (int kt = 0; kt < ntiles; ++kt) {
         const int k0 = kt * BK;
-        __syncthreads();
-        stage.store(k_lds, v_lds);
-        __syncthreads();
-        if (kt + 1 < ntiles) stage.load(kp, vp, k0 + BK, Sk);
+        const char* k_lds = kv_lds[kt & 1][0];
+        const char* v_lds = kv_lds[kt & 1][1];
+        async_wait();
+        __syncthreads();  // tile kt visible; every wave is done with the other buffer
 
-        // Bias (as float) and key validity for the lane's keys k0 + 32c + 8g + j.
-        float bv[QT][2][8];
+        // Everything this tile needs from LDS is read before the next tile's direct-to-LDS
+        // loads are issued, so no LDS read waits for them.
+        const bool need_mask = kt >= kMaxFlagTiles || flags[kt] != 0;
+        V8 kf[4][G::KS];
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-            const int brow = min(qbase + qt * 16 + r16, Sq - 1);
+        for (int t = 0; t < 4; ++t)
 #pragma unroll
-            for (int c = 0; c < 2; ++c)
-                load_bias8<TR>(bp + (size_t)brow * Sk, k0 + 32 * c + 8 * g, Sk, vec_ok,
-                               bv[qt][c]);
-        }
-        unsigned valid[2];
-        bool all_valid = true;
-#pragma unroll
-        for (int c = 0; c < 2; ++c) {
-            valid[c] = key_valid8(mp, k0 + 32 * c + 8 * g, Sk, vec_ok);
-            all_valid = all_valid && valid[c] == 0xffu && (k0 + 32 * c + 8 * g + 8 <= Sk);
-        }
-        const bool need_mask = !__all(all_valid);
-
-        // S^T = K . Q^T for the four 16-key sub-tiles (chunk c = t/2, half t%2).
-        f32x4 s[QT][4];
-#pragma unroll
-        for (int t = 0; t < 4; ++t) {
-            const int key = perm_key(t, r16);
-#pragma unroll
-            for (int ks = 0; ks < G::KS; ++ks) {
-                const V8 kf = lds_row_operand<V8, D>(k_lds, key, G::KLD, ks, g);
-#pragma unroll
-                for (int qt = 0; qt < QT; ++qt)
-                    s[qt][t] = TR::mfma(kf, qf[qt][ks], ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f}
-                                                               : s[qt][t]);
-            }
-        }
-
-        // A operand V^T (rows = head dims, k-slots = the chunk's keys in lane order).
+            for (int ks = 0; ks < G::KS; ++ks)
+                kf[t][ks] = swz_row_operand<V8, D>(k_lds, perm_key(t, r16), ks, g);
         V8 vf[G::DT][2];
 #pragma unroll
         for (int dt = 0; dt < G::DT; ++dt)
 #pragma unroll
-            for (int c = 0; c < 2; ++c) vf[dt][c] = lds_tr_operand<V8>(v_lds, G::VLD, c, dt, r16, g);
+            for (int c = 0; c < 2; ++c) vf[dt][c] = swz_tr_operand<V8, D>(v_lds, 32 * c, dt, r16, g);
+
+        if (kt + 1 < ntiles) {
+            stage_rows_async<D, BK, 256>(kp, k0 + BK, Sk, kv_lds[(kt + 1) & 1][0]);
+            stage_rows_async<D, BK, 256>(vp, k0 + BK, Sk, kv_lds[(kt + 1) & 1][1]);
+            load_chunks(k0 + BK, nxt);
+        }
+
+        // S^T = K . Q^T for the four 16-key sub-tiles (chunk c = t/2, half t%2).
+        f32x4 s[QT][4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+#pragma unroll
+            for (int ks = 0; ks < G::KS; ++ks)
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt)
+                    s[qt][t] = TR::mfma(kf[t][ks], qf[qt][ks],
+                                        ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : s[qt][t]);
 
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
             float x[2][8];
 #pragma unroll
-            for (int c = 0; c < 2; ++c)
+            for (int c = 0; c < 2; ++c) {
+                float bv[8];
+                unpack8<TR>(cur[qt][c].bias, bv);
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    x[c][j] = s[qt][2 * c][j] * scale + bv[qt][c][j];
-                    x[c][4 + j] = s[qt][2 * c + 1][j] * scale + bv[qt][c][4 + j];
+                    x[c][j] = fmaf(s[qt][2 * c][j], scale, bv[j]);
+                    x[c][4 + j] = fmaf(s[qt][2 * c + 1][j], scale, bv[4 + j]);
                 }
+            }
             if (need_mask) {
 #pragma unroll
-                for (int c = 0; c < 2; ++c)
+                for (int c = 0; c < 2; ++c) {
+                    const unsigned valid = cur[qt][c].valid();
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
                         const int key = k0 + 32 * c + 8 * g + j;
                         x[c][j] = key >= Sk ? -INFINITY
-                                            : (((valid[c] >> j) & 1u) ? x[c][j] : masked_logit);
+                                            : (((valid >> j) & 1u) ? x[c][j] : masked_logit);
                     }
+                }
             }
             float mt = x[0][0];
 #pragma unroll
@@ -178,6 +253,10 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
                 for (int c = 0; c < 2; ++c) acc[qt][dt] = TR::mfma(vf[dt][c], pf[c], acc[qt][dt]);
             }
         }
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+            for (int c = 0; c < 2; ++c) cur[qt][c] = nxt[qt][c];
     }
 
     // Normalise and store: lane holds O[row][16*dt + 4*g + i], i = 0..3.
@@ -197,24 +276,32 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
     }
 }
 
+template <typename TR, int D, int QT>
+void launch_fwd_qt(hipStream_t st, const void* q, const void* k, const void* v, const void* bias,
+                   const uint8_t* kmask, void* out, float* lse, int N, int H, int Sq, int Sk,
+                   float scale) {
+    using E = typename TR::elem;
+    const dim3 grid(ceil_div(Sq, 64 * QT), H, N);
+    const bool vec = Sk % 8 == 0 && (reinterpret_cast<uintptr_t>(kmask) & 7u) == 0;
+    if (vec)
+        attn_fwd_kernel<TR, D, QT, true><<<grid, 256, 0, st>>>(
+            (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (E*)out, lse, H, Sq, Sk,
+            scale);
+    else
+        attn_fwd_kernel<TR, D, QT, false><<<grid, 256, 0, st>>>(
+            (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (E*)out, lse, H, Sq, Sk,
+            scale);
+}
+
 template <typename TR, int D>
 void launch_fwd(hipStream_t st, const void* q, const void* k, const void* v, const void* bias,
                 const uint8_t* kmask, void* out, float* lse, int N, int H, int Sq, int Sk,
                 float scale) {
-    using E = typename TR::elem;
-    const int vec_ok = (Sk % 8 == 0) ? 1 : 0;
     KernelTimer timer("attn_fwd", st);
-    if (Sq <= 64) {
-        dim3 grid(ceil_div(Sq, 64), H, N);
-        attn_fwd_kernel<TR, D, 1><<<grid, 256, 0, st>>>(
-            (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (E*)out, lse, H, Sq,
-            Sk, scale, vec_ok);
-    } else {
-        dim3 grid(ceil_div(Sq, 128), H, N);
-        attn_fwd_kernel<TR, D, 2><<<grid, 256, 0, st>>>(
-            (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (E*)out, lse, H, Sq,
-            Sk, scale, vec_ok);
-    }
+    if (Sq <= 64)
+        launch_fwd_qt<TR, D, 1>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk, scale);
+    else
+        launch_fwd_qt<TR, D, 2>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk, scale);
 }
 
 template <typename TR>
