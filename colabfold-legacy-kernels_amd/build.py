@@ -31,11 +31,15 @@ ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # Packed-FP32 VALU forms are disabled for all device code: hipcc -O3 would otherwise form
-# v_pk_{add,mul,fma}_f32 from scalar float code.
+# v_pk_{add,mul,fma}_f32 from scalar float code. MFMA results are allocated to ordinary VGPRs
+# (not AGPRs): the kernels post-process every accumulator with VALU ops, which cannot read
+# AGPRs, so the AGPR form costs a v_accvgpr_read per element and often an extra wave of
+# register pressure.
 COMMON = [
     "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
     "--offload-arch=" + ARCH,
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-mllvm", "-amdgpu-mfma-vgpr-form=1",
     "-I" + str(REPO / "include"), "-I" + str(CSRC),
 ]
 

@@ -99,15 +99,29 @@ __device__ __forceinline__ V lds_tr8(const void* p_lo, const void* p_hi) {
 }
 
 // Cross-lane reductions among the four lanes l, l^16, l^32, l^48 (same column of a C tile).
+// v_permlane32_swap / v_permlane16_swap with both operands = v return, in each lane, v of that
+// lane and of the lane 32 (16) apart, as a pair: two VALU ops per step, no LDS round trip.
+__device__ __forceinline__ u32x2 pair_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return u32x2{r[0], r[1]};
+}
+__device__ __forceinline__ u32x2 pair_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                    false);
+    return u32x2{r[0], r[1]};
+}
 __device__ __forceinline__ float xgroup_max(float v) {
-    v = fmaxf(v, __shfl_xor(v, 16));
-    v = fmaxf(v, __shfl_xor(v, 32));
-    return v;
+    u32x2 p = pair_xor32(v);
+    v = fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
+    p = pair_xor16(v);
+    return fmaxf(__uint_as_float(p[0]), __uint_as_float(p[1]));
 }
 __device__ __forceinline__ float xgroup_sum(float v) {
-    v += __shfl_xor(v, 16);
-    v += __shfl_xor(v, 32);
-    return v;
+    u32x2 p = pair_xor32(v);
+    v = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    p = pair_xor16(v);
+    return __uint_as_float(p[0]) + __uint_as_float(p[1]);
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
