@@ -395,6 +395,509 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv(
     }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Head dims up to 32: a prep launch, a row-owner dQ + dBias launch and a column-owner dK/dV
+// launch whose operands all arrive by direct global->LDS loads into static double buffers.
+// ---------------------------------------------------------------------------------------------
+
+// True when some byte of the eight is zero (an absent key).
+__device__ __forceinline__ bool has_zero_byte(u32x2 w) {
+    const unsigned a = (w[0] - 0x01010101u) & ~w[0] & 0x80808080u;
+    const unsigned b = (w[1] - 0x01010101u) & ~w[1] & 0x80808080u;
+    return (a | b) != 0u;
+}
+
+// Bit j set when byte j of the eight is nonzero.
+__device__ __forceinline__ unsigned nonzero_bits8(u32x2 w) {
+    unsigned bits = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        bits |= (((w[0] >> (8 * j)) & 0xffu) != 0u ? 1u : 0u) << j;
+        bits |= (((w[1] >> (8 * j)) & 0xffu) != 0u ? 1u : 0u) << (4 + j);
+    }
+    return bits;
+}
+
+// Mask bytes of keys kk .. kk+7 of one mask row (0 past Sk; all present without a mask). VEC:
+// one 8-byte load (Sk % 8 == 0, 8-byte aligned rows), the address clamped into the row.
+template <bool VEC>
+__device__ __forceinline__ u32x2 mask_bytes8(const uint8_t* mrow, int kk, int Sk) {
+    if (!mrow) return u32x2{~0u, ~0u};
+    if constexpr (VEC) {
+        return *reinterpret_cast<const u32x2*>(mrow + min(kk, Sk - 8));
+    } else {
+        uint8_t b[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) b[j] = kk + j < Sk ? mrow[kk + j] : uint8_t(0);
+        u32x2 w;
+        __builtin_memcpy(&w, b, 8);
+        return w;
+    }
+}
+
+// Prep: bias [H][Sq][Sk] -> bias_t [H][Sk][SqP] (SqP = Sq rounded up to 8, padding zero) in
+// 64x64 tiles through LDS, and per mask row the logit its absent keys take (-1e9, or 0 when the
+// row has no present key). Blocks [0, ntiles) transpose, blocks [ntiles, ntiles + N) do rows.
+template <typename TR>
+__global__ __launch_bounds__(256) void attn_bwd_prep(const typename TR::elem* __restrict__ bias,
+                                                     typename TR::elem* __restrict__ bias_t,
+                                                     const uint8_t* __restrict__ kmask,
+                                                     float* __restrict__ row_logit, int Sq,
+                                                     int Sk, int SqP, int tiles_q, int tiles_k,
+                                                     int ntiles) {
+    using E = typename TR::elem;
+    __shared__ E tile[64][66];
+    if ((int)blockIdx.x >= ntiles) {
+        const int n = blockIdx.x - ntiles;
+        const uint8_t* m = kmask + (size_t)n * Sk;
+        int any = 0;
+        for (int i = threadIdx.x; i < Sk; i += 256) any |= m[i] != 0;
+        any = __syncthreads_or(any);
+        if (threadIdx.x == 0) row_logit[n] = any ? kMaskedLogit : 0.f;
+        return;
+    }
+    int t = blockIdx.x;
+    const int tk = t % tiles_k;
+    t /= tiles_k;
+    const int tq = t % tiles_q, h = t / tiles_q;
+    const int q0 = tq * 64, k0 = tk * 64;
+    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+        const int r = i >> 6, c = i & 63;  // r: query, c: key
+        const int qq = q0 + r, kk = k0 + c;
+        tile[c][r] = (qq < Sq && kk < Sk) ? bias[((size_t)h * Sq + qq) * Sk + kk] : E(0.f);
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
+        const int r = i >> 6, c = i & 63;  // r: key, c: query
+        const int kk = k0 + r, qq = q0 + c;
+        if (kk < Sk && qq < SqP) bias_t[((size_t)h * Sk + kk) * SqP + qq] = tile[r][c];
+    }
+}
+
+// Row owner. A block of 8 waves owns (64 queries, head h, rows n0..n1, key range [kbeg, kend)
+// of up to 128*KCW keys). Wave w = 4*qg + kq owns queries 32*qg + 0..31 (two 16-query
+// sub-tiles) and the 32-key chunks j = 4*i + kq, i < KCW, of the range. The bias of those
+// (query, key) pairs stays in registers for the whole block, and so does their dBias sum over
+// the block's rows. Per row n the K/V rows of the range and the Q/dO/O rows of the block's
+// queries sit in LDS (row n+1's are loaded directly into the other buffer meanwhile); per chunk
+// the wave computes S^T = K.Q^T and dP^T - D = V.dO^T - D (D_i = rowsum(dO*O) enters as the
+// accumulator input), dS, and dQ^T += K^T.dS^T. The four key-quarter waves of a query group
+// then add their dQ partials through LDS in a fixed order. Also writes lse*log2(e) and -D_i
+// per query for the column-owner pass.
+template <typename TR, int D, int KCW, bool VEC>
+__global__ __launch_bounds__(512) void attn_bwd_dq2(
+    const typename TR::elem* __restrict__ q, const typename TR::elem* __restrict__ k,
+    const typename TR::elem* __restrict__ v, const typename TR::elem* __restrict__ bias,
+    const uint8_t* __restrict__ kmask, const typename TR::elem* __restrict__ out,
+    const typename TR::elem* __restrict__ dout, const float* __restrict__ lse,
+    const float* __restrict__ row_logit, float* __restrict__ lse2_out,
+    float* __restrict__ ndi_out, typename TR::elem* __restrict__ dq,
+    float* __restrict__ dq_part, float* __restrict__ dbias_dst, int N, int H, int Sq, int Sk,
+    int NB, int nranges, float scale) {
+    using E = typename TR::elem;
+    using V8 = typename TR::vec8;
+    using T = SwzTile<D>;
+    static_assert(D <= 32, "row-owner kernel holds one 32-dim k-slot group");
+    constexpr int KQ = 4, BQ = 64, DT = AttnGeom<D>::DT;
+    constexpr int RK = KQ * KCW * 32;
+    constexpr int KVB = RK * T::ROWB;
+    constexpr int QB = BQ * T::ROWB;
+
+    __shared__ __attribute__((aligned(16))) char kv0[2 * KVB];
+    __shared__ __attribute__((aligned(16))) char kv1[2 * KVB];
+    __shared__ __attribute__((aligned(16))) char qd0[3 * QB];
+    __shared__ __attribute__((aligned(16))) char qd1[3 * QB];
+    __shared__ __attribute__((aligned(16))) f32x4 xch[8 * 2 * DT * 64];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int qg = wave >> 2, kq = wave & 3;
+    const int q0 = blockIdx.x * BQ, h = blockIdx.y;
+    const int chunk = blockIdx.z / nranges, range = blockIdx.z % nranges;
+    const int kbeg = range * RK, kend = min(Sk, kbeg + RK);
+    const int n0 = chunk * NB, n1 = min(N, n0 + NB);
+    int qrow[2];
+#pragma unroll
+    for (int qt = 0; qt < 2; ++qt) qrow[qt] = q0 + 32 * qg + 16 * qt + r16;
+
+    // Resident bias: chunk i, sub-tile qt -> bias[h][qrow][kbeg + 32j + 8g + 0..7].
+    u32x4 braw[KCW][2];
+#pragma unroll
+    for (int i = 0; i < KCW; ++i)
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+            const int kk = kbeg + 32 * (i * KQ + kq) + 8 * g;
+            const E* brow = bias + ((size_t)h * Sq + min(qrow[qt], Sq - 1)) * Sk;
+            if constexpr (VEC) {
+                braw[i][qt] = ld16(brow + min(kk, Sk - 8));
+            } else {
+                E e[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) e[j] = kk + j < Sk ? brow[kk + j] : E(0.f);
+                __builtin_memcpy(&braw[i][qt], e, 16);
+            }
+        }
+
+    f32x4 dbias[KCW][2][2];
+#pragma unroll
+    for (int i = 0; i < KCW; ++i)
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+            for (int t = 0; t < 2; ++t) dbias[i][qt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto stage = [&](int n, char* kv, char* qd) {
+        const size_t nh = (size_t)n * H + h;
+        stage_rows_async<D, RK, 512>(k + nh * Sk * D, kbeg, Sk, kv);
+        stage_rows_async<D, RK, 512>(v + nh * Sk * D, kbeg, Sk, kv + KVB);
+        stage_rows_async<D, BQ, 512>(q + nh * Sq * D, q0, Sq, qd);
+        stage_rows_async<D, BQ, 512>(dout + nh * Sq * D, q0, Sq, qd + QB);
+        stage_rows_async<D, BQ, 512>(out + nh * Sq * D, q0, Sq, qd + 2 * QB);
+    };
+    // Per-row values kept in registers one row ahead, raw: anything computed from them right
+    // after the load would wait for the row's direct-to-LDS loads too.
+    float lse_nx[2], ml_nx = kMaskedLogit;
+    u32x2 mask_nx[KCW];
+    auto prefetch = [&](int n) {
+        const size_t nh = (size_t)n * H + h;
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) lse_nx[qt] = lse[nh * Sq + min(qrow[qt], Sq - 1)];
+        const uint8_t* mrow = kmask ? kmask + (size_t)n * Sk : nullptr;
+#pragma unroll
+        for (int i = 0; i < KCW; ++i)
+            mask_nx[i] = mask_bytes8<VEC>(mrow, kbeg + 32 * (i * KQ + kq) + 8 * g, Sk);
+        ml_nx = kmask ? row_logit[n] : kMaskedLogit;
+    };
+
+    auto step = [&](int n, const char* kvc, const char* qdc, char* kvn, char* qdn) {
+        const size_t nh = (size_t)n * H + h;
+        async_wait();
+        __syncthreads();  // row n in (kvc, qdc); every wave is done with row n-1
+        // The packed bias is loop-invariant; hiding that keeps the compiler from hoisting its
+        // unpacked (twice as large) form out of the row loop.
+#pragma unroll
+        for (int i = 0; i < KCW; ++i)
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) asm volatile("" : "+v"(braw[i][qt]));
+        float lse2c[2];
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) lse2c[qt] = qrow[qt] < Sq ? lse_nx[qt] * kLog2e : INFINITY;
+        const float mlc = ml_nx;
+        u32x2 maskc[KCW];
+#pragma unroll
+        for (int i = 0; i < KCW; ++i) maskc[i] = mask_nx[i];
+        if (n + 1 < n1) {
+            stage(n + 1, kvn, qdn);
+            prefetch(n + 1);
+        }
+
+        V8 qf[2], dof[2];
+        float di[2];
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+            const int row = 32 * qg + 16 * qt + r16;
+            qf[qt] = swz_row_operand<V8, D>(qdc, row, 0, g);
+            dof[qt] = swz_row_operand<V8, D>(qdc + QB, row, 0, g);
+            const V8 of = swz_row_operand<V8, D>(qdc + 2 * QB, row, 0, g);
+            float part = 0.f;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) part = fmaf(TR::to_f(dof[qt][j]), TR::to_f(of[j]), part);
+            di[qt] = xgroup_sum(part);
+        }
+        if (range == 0 && kq == 0 && g == 0) {
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt)
+                if (qrow[qt] < Sq) {
+                    lse2_out[nh * Sq + qrow[qt]] = lse2c[qt];
+                    ndi_out[nh * Sq + qrow[qt]] = -di[qt];
+                }
+        }
+
+        f32x4 dqa[2][DT];
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) dqa[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#pragma unroll
+        for (int i = 0; i < KCW; ++i) {
+            const int c0 = 32 * (i * KQ + kq);  // chunk's first key, relative to kbeg
+            if (kbeg + c0 >= kend) continue;   // wave-uniform
+            // One chunk's operands live at a time; interleaving chunks only adds registers.
+            __builtin_amdgcn_sched_barrier(0);
+            V8 kf[2], vf[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int row = c0 + 8 * (r16 >> 2) + 4 * t + (r16 & 3);
+                kf[t] = swz_row_operand<V8, D>(kvc, row, 0, g);
+                vf[t] = swz_row_operand<V8, D>(kvc + KVB, row, 0, g);
+            }
+            f32x4 s[2][2], dp[2][2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt) {
+                    s[qt][t] = TR::mfma(kf[t], qf[qt], f32x4{0.f, 0.f, 0.f, 0.f});
+                    dp[qt][t] = TR::mfma(vf[t], dof[qt], f32x4{-di[qt], -di[qt], -di[qt], -di[qt]});
+                }
+            const bool nm = kbeg + c0 + 32 > Sk || __any(has_zero_byte(maskc[i]));
+            const unsigned valid = nm ? nonzero_bits8(maskc[i]) : 0xffu;
+            V8 dsf[2];
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+                float b[8];
+                unpack8<TR>(braw[i][qt], b);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int t = j >> 2, e = j & 3;
+                    float x = fmaf(s[qt][t][e], scale, b[j]);
+                    if (nm) {
+                        const int key = kbeg + c0 + 8 * g + j;
+                        x = key >= Sk ? -INFINITY : (((valid >> j) & 1u) ? x : mlc);
+                    }
+                    const float p = fast_exp2(fmaf(x, kLog2e, -lse2c[qt]));
+                    const float ds = p * dp[qt][t][e];
+                    dbias[i][qt][t][e] += ds;
+                    dsf[qt][j] = TR::from_f(ds);
+                }
+            }
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                const V8 kt = swz_tr_operand<V8, D>(kvc, c0, dt, r16, g);
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt) dqa[qt][dt] = TR::mfma(kt, dsf[qt], dqa[qt][dt]);
+            }
+        }
+
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) xch[((wave * 2 + qt) * DT + dt) * 64 + lane] = dqa[qt][dt];
+        __syncthreads();
+        if (kq < 2 * DT) {
+            const int qt = kq / DT, dt = kq % DT;
+            f32x4 acc = xch[(((qg * 4) * 2 + qt) * DT + dt) * 64 + lane];
+#pragma unroll
+            for (int w = 1; w < 4; ++w) acc += xch[(((qg * 4 + w) * 2 + qt) * DT + dt) * 64 + lane];
+            const int d = 16 * dt + 4 * g;
+            if (qrow[qt] < Sq && d < D) {
+                if (nranges == 1) {
+                    store4<TR>(dq + (nh * Sq + qrow[qt]) * D + d, acc * scale);
+                } else {
+                    float* o = dq_part + (((size_t)range * N + n) * H + h) * Sq * D +
+                               (size_t)qrow[qt] * D + d;
+                    *reinterpret_cast<f32x4*>(o) = acc * scale;
+                }
+            }
+        }
+    };
+
+    if (n0 < n1) {
+        stage(n0, kv0, qd0);
+        prefetch(n0);
+    }
+    for (int n = n0; n < n1; n += 2) {
+        step(n, kv0, qd0, kv1, qd1);
+        if (n + 1 < n1) step(n + 1, kv1, qd1, kv0, qd0);
+    }
+
+#pragma unroll
+    for (int i = 0; i < KCW; ++i) {
+        const int kk = kbeg + 32 * (i * KQ + kq) + 8 * g;
+        if (kbeg + 32 * (i * KQ + kq) >= kend) continue;
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) {
+            if (qrow[qt] >= Sq) continue;
+            float* drow = dbias_dst + (((size_t)chunk * H + h) * Sq + qrow[qt]) * Sk;
+            if (VEC) {
+                if (kk >= Sk) continue;  // kk % 8 == Sk % 8 == 0, so kk < Sk means kk + 8 <= Sk
+                *reinterpret_cast<f32x4*>(drow + kk) = dbias[i][qt][0];
+                *reinterpret_cast<f32x4*>(drow + kk + 4) = dbias[i][qt][1];
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (kk + j < Sk) drow[kk + j] = dbias[i][qt][j >> 2][j & 3];
+            }
+        }
+    }
+}
+
+// Column owner. A block of 8 waves owns (128*KSUB keys, head h, row n); wave w owns keys
+// k0 + 16*KSUB*w + 0..16*KSUB-1 with K and V held as MFMA B operands. The queries stream in
+// 64-row tiles: Q, dO, the transposed bias tile and lse*log2(e), -D_i arrive by direct
+// global->LDS loads into the other buffer while the current tile is computed (one barrier per
+// tile). Per 32-query chunk: S = Q.K^T and dP - D = dO.V^T with the queries permuted so that P
+// and dS are directly the B operands of dV^T += dO^T.P and dK^T += Q^T.dS.
+template <typename TR, int D, int KSUB, bool VEC>
+__global__ __launch_bounds__(512) void attn_bwd_dkv2(
+    const typename TR::elem* __restrict__ q, const typename TR::elem* __restrict__ k,
+    const typename TR::elem* __restrict__ v, const typename TR::elem* __restrict__ bias_t,
+    const uint8_t* __restrict__ kmask, const typename TR::elem* __restrict__ dout,
+    const float* __restrict__ lse2, const float* __restrict__ ndi,
+    const float* __restrict__ row_logit, typename TR::elem* __restrict__ dk,
+    typename TR::elem* __restrict__ dv, int H, int Sq, int Sk, int SqP, float scale) {
+    using E = typename TR::elem;
+    using V8 = typename TR::vec8;
+    using T = SwzTile<D>;
+    static_assert(D <= 32, "column-owner kernel holds one 32-dim k-slot group");
+    constexpr int DT = AttnGeom<D>::DT;
+    constexpr int KW = 16 * KSUB, KB = 8 * KW;
+    constexpr int QB = 64 * T::ROWB;
+    constexpr int BTB = KB * 128;  // bias^T tile: KB key rows of 64 queries
+
+    __shared__ __attribute__((aligned(16))) char qd0[2 * QB];
+    __shared__ __attribute__((aligned(16))) char qd1[2 * QB];
+    __shared__ __attribute__((aligned(16))) char bt0[BTB];
+    __shared__ __attribute__((aligned(16))) char bt1[BTB];
+    __shared__ __attribute__((aligned(16))) float st0[128];
+    __shared__ __attribute__((aligned(16))) float st1[128];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int k0 = blockIdx.x * KB, h = blockIdx.y, n = blockIdx.z;
+    const size_t nh = (size_t)n * H + h;
+    const int kw0 = k0 + wave * KW;
+    const bool active = kw0 < Sk;
+
+    const float ml = kmask ? row_logit[n] : kMaskedLogit;
+    V8 kf[KSUB], vf[KSUB];
+    bool present[KSUB];
+    float absent_logit[KSUB];
+#pragma unroll
+    for (int s = 0; s < KSUB; ++s) {
+        const int key = kw0 + 16 * s + r16;
+        const bool kin = key < Sk;
+        u32x4 rk = {0u, 0u, 0u, 0u}, rv = {0u, 0u, 0u, 0u};
+        if (kin && 8 * g < D) {
+            rk = ld16(k + (nh * Sk + key) * D + 8 * g);
+            rv = ld16(v + (nh * Sk + key) * D + 8 * g);
+        }
+        kf[s] = bits_as<V8>(rk);
+        vf[s] = bits_as<V8>(rv);
+        present[s] = kin && (kmask == nullptr || kmask[(size_t)n * Sk + key] != 0);
+        absent_logit[s] = kin ? ml : -INFINITY;
+    }
+
+    f32x4 dka[KSUB][DT], dva[KSUB][DT];
+#pragma unroll
+    for (int s = 0; s < KSUB; ++s)
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            dka[s][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+            dva[s][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+
+    auto stage = [&](int qs, char* qd, char* bt, float* st) {
+        stage_rows_async<D, 64, 512>(q + nh * Sq * D, qs, Sq, qd);
+        stage_rows_async<D, 64, 512>(dout + nh * Sq * D, qs, Sq, qd + QB);
+        // bias^T rows k0 .. k0+KB-1, eight 16-byte pieces of 8 queries each, piece p of row r
+        // at position p ^ (r & 7).
+#pragma unroll
+        for (int base = wave * 64; base < KB * 8; base += 512) {
+            const int slot = base + lane;
+            const int row = slot >> 3, piece = (slot & 7) ^ (row & 7);
+            const int key = k0 + row, qq = qs + 8 * piece;
+            const void* src = kZero16;
+            if (key < Sk && qq < SqP) src = bias_t + ((size_t)h * Sk + key) * SqP + qq;
+            __builtin_amdgcn_global_load_lds(
+                src, (__attribute__((address_space(3))) void*)(bt + base * 16), 16, 0, 0);
+        }
+        if (wave == 0) {
+            const int qq = qs + lane;
+            const void* a = kZero16;
+            const void* b = kZero16;
+            if (qq < Sq) {
+                a = lse2 + nh * Sq + qq;
+                b = ndi + nh * Sq + qq;
+            }
+            __builtin_amdgcn_global_load_lds(a, (__attribute__((address_space(3))) void*)st, 4,
+                                             0, 0);
+            __builtin_amdgcn_global_load_lds(
+                b, (__attribute__((address_space(3))) void*)(st + 64), 4, 0, 0);
+        }
+    };
+
+    auto compute = [&](const char* qd, const char* bt, const float* st) {
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            V8 qa[2], da[2];
+            f32x4 l4[2], n4[2];
+#pragma unroll
+            for (int t = 0; t < 2; ++t) {
+                const int row = 32 * c + 8 * (r16 >> 2) + 4 * t + (r16 & 3);
+                qa[t] = swz_row_operand<V8, D>(qd, row, 0, g);
+                da[t] = swz_row_operand<V8, D>(qd + QB, row, 0, g);
+                l4[t] = *reinterpret_cast<const f32x4*>(st + 32 * c + 8 * g + 4 * t);
+                n4[t] = *reinterpret_cast<const f32x4*>(st + 64 + 32 * c + 8 * g + 4 * t);
+            }
+            V8 doT[DT], qT[DT];
+#pragma unroll
+            for (int dt = 0; dt < DT; ++dt) {
+                doT[dt] = swz_tr_operand<V8, D>(qd + QB, 32 * c, dt, r16, g);
+                qT[dt] = swz_tr_operand<V8, D>(qd, 32 * c, dt, r16, g);
+            }
+#pragma unroll
+            for (int s = 0; s < KSUB; ++s) {
+                f32x4 S[2], dP[2];
+#pragma unroll
+                for (int t = 0; t < 2; ++t) {
+                    S[t] = TR::mfma(qa[t], kf[s], f32x4{0.f, 0.f, 0.f, 0.f});
+                    dP[t] = TR::mfma(da[t], vf[s], n4[t]);
+                }
+                const int row = wave * KW + 16 * s + r16;
+                float b[8];
+                unpack8<TR>(*reinterpret_cast<const u32x4*>(
+                                bt + row * 128 + 16 * ((4 * c + g) ^ (row & 7))),
+                            b);
+                V8 pf, dsf;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int t = j >> 2, e = j & 3;
+                    const float x = present[s] ? fmaf(S[t][e], scale, b[j]) : absent_logit[s];
+                    const float p = fast_exp2(fmaf(x, kLog2e, -l4[t][e]));
+                    const float ds = p * dP[t][e];
+                    pf[j] = TR::from_f(p);
+                    dsf[j] = TR::from_f(ds);
+                }
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    dva[s][dt] = TR::mfma(doT[dt], pf, dva[s][dt]);
+                    dka[s][dt] = TR::mfma(qT[dt], dsf, dka[s][dt]);
+                }
+            }
+        }
+    };
+
+    const int ntq = (Sq + 63) / 64;
+    if (ntq > 0) stage(0, qd0, bt0, st0);
+    for (int it = 0; it < ntq; it += 2) {
+        async_wait();
+        __syncthreads();
+        if (it + 1 < ntq) stage(64 * (it + 1), qd1, bt1, st1);
+        if (active) compute(qd0, bt0, st0);
+        if (it + 1 < ntq) {
+            async_wait();
+            __syncthreads();
+            if (it + 2 < ntq) stage(64 * (it + 2), qd0, bt0, st0);
+            if (active) compute(qd1, bt1, st1);
+        }
+    }
+
+#pragma unroll
+    for (int s = 0; s < KSUB; ++s) {
+        const int key = kw0 + 16 * s + r16;
+        if (key >= Sk) continue;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+            const int d = 16 * dt + 4 * g;
+            if (d < D) {
+                store4<TR>(dk + (nh * Sk + key) * D + d, dka[s][dt] * scale);
+                store4<TR>(dv + (nh * Sk + key) * D + d, dva[s][dt]);
+            }
+        }
+    }
+}
+
 // out[i] = sum over p = 0..nparts-1 (in order) of part[p*count + i]; nparts = 0 writes zeros.
 __global__ __launch_bounds__(256) void sum_partials_f32(const float* __restrict__ part,
                                                         size_t count, int nparts,
@@ -425,34 +928,67 @@ int grid_for(size_t count) {
 }
 
 // Work decomposition of the backward pass; a pure function of the sizes, so the workspace size
-// and the launches always agree and the reduction order is fixed.
+// and the launches always agree and the reduction order is fixed. Head dims up to 32 take the
+// prep / dq2 / dkv2 path (v2); D = 64 takes dot / dq / dkv.
+constexpr int kTargetBlocks = 256;  // one 8-wave row-owner block per CU of an MI355X
+
 struct BwdPlan {
-    int KT = 0, nranges = 0, NB = 0, nchunks = 0;
-    size_t off_di = 0, off_dbias = 0, off_dq = 0, bytes = 0;
+    bool v2 = false;
+    int KT = 0, KCW = 0, KSUB = 0, nranges = 0, NB = 0, nchunks = 0, SqP = 0;
+    size_t off_di = 0, off_bt = 0, off_rowl = 0, off_lse2 = 0, off_ndi = 0, off_dbias = 0,
+           off_dq = 0, bytes = 0;
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 BwdPlan plan_bwd(int64_t N, int64_t H, int64_t Sq, int64_t Sk, int64_t D) {
     BwdPlan p;
-    const int64_t ktiles = (Sk + 63) / 64;
-    p.KT = ktiles <= 2 ? 2 : ktiles <= 4 ? 4 : ktiles <= 6 ? 6 : 8;
-    p.nranges = (int)((ktiles + p.KT - 1) / p.KT);
-    const int64_t qtiles = (Sq + 63) / 64;
+    p.v2 = D <= 32;
+    int64_t range_keys;
+    int64_t qtiles;
+    if (p.v2) {
+        const int64_t chunks32 = (Sk + 31) / 32;
+        const int64_t kcw = (chunks32 + 3) / 4;
+        p.KCW = (int)(kcw < 1 ? 1 : kcw > 3 ? 3 : kcw);
+        range_keys = 128 * (int64_t)p.KCW;
+        const int64_t ksub = (Sk + 127) / 128;
+        p.KSUB = (int)(ksub < 1 ? 1 : ksub > 3 ? 3 : ksub);
+        p.SqP = (int)((Sq + 7) / 8 * 8);
+        qtiles = (Sq + 63) / 64;
+    } else {
+        const int64_t ktiles = (Sk + 63) / 64;
+        p.KT = ktiles <= 2 ? 2 : ktiles <= 4 ? 4 : ktiles <= 6 ? 6 : 8;
+        range_keys = 64 * (int64_t)p.KT;
+        qtiles = (Sq + 63) / 64;
+    }
+    p.nranges = (int)((Sk + range_keys - 1) / range_keys);
     const int64_t base = qtiles * H * (p.nranges > 0 ? p.nranges : 1);
-    int64_t chunks = base > 0 ? (512 + base - 1) / base : 1;
+    const int64_t target = p.v2 ? kTargetBlocks : 512;
+    int64_t chunks = base > 0 ? (p.v2 ? target / base : (target + base - 1) / base) : 1;
     if (chunks > N) chunks = N;
     if (chunks < 1) chunks = 1;
     p.NB = (int)((N + chunks - 1) / chunks);
     if (p.NB < 1) p.NB = 1;
     p.nchunks = (int)((N + p.NB - 1) / p.NB);
+    const size_t rows = (size_t)(N * H * Sq);
     size_t off = 0;
-    p.off_di = off;
-    off += align256((size_t)(N * H * Sq) * sizeof(float));
+    if (p.v2) {
+        p.off_bt = off;
+        off += align256((size_t)(H * Sk) * p.SqP * 2);
+        p.off_rowl = off;
+        off += align256((size_t)N * sizeof(float));
+        p.off_lse2 = off;
+        off += align256(rows * sizeof(float));
+        p.off_ndi = off;
+        off += align256(rows * sizeof(float));
+    } else {
+        p.off_di = off;
+        off += align256(rows * sizeof(float));
+    }
     p.off_dbias = off;
     if (p.nchunks > 1) off += align256((size_t)p.nchunks * H * Sq * Sk * sizeof(float));
     p.off_dq = off;
-    if (p.nranges > 1) off += align256((size_t)p.nranges * N * H * Sq * D * sizeof(float));
+    if (p.nranges > 1) off += align256((size_t)p.nranges * rows * D * sizeof(float));
     p.bytes = off;
     return p;
 }
@@ -469,18 +1005,34 @@ void launch_dq(hipStream_t st, dim3 grid, const void* q, const void* k, const vo
         (E*)dq, dq_part, dbias_dst, N, H, Sq, Sk, NB, nranges, scale, vec_ok);
 }
 
+// The partial sums (dBias over row chunks, dQ over key ranges) in fixed order.
+template <typename TR>
+void finish_partials(hipStream_t st, const BwdPlan& p, float* dbias_part, float* dq_part,
+                     float* dbias, void* dq, size_t dbias_count, size_t dq_count) {
+    using E = typename TR::elem;
+    if (p.nchunks > 1) {
+        KernelTimer timer("attn_bwd_dbias_sum", st);
+        sum_partials_f32<<<grid_for(dbias_count), 256, 0, st>>>(dbias_part, dbias_count,
+                                                                p.nchunks, dbias);
+    }
+    if (p.nranges > 1) {
+        KernelTimer timer("attn_bwd_dq_sum", st);
+        sum_partials_cast<TR><<<grid_for(dq_count), 256, 0, st>>>(dq_part, dq_count, p.nranges,
+                                                                  (E*)dq);
+    }
+}
+
 template <typename TR, int D>
-void run_bwd(hipStream_t st, const BwdPlan& p, const void* q, const void* k, const void* v,
-             const void* bias, const uint8_t* kmask, const void* out, const void* dout,
-             const float* lse, void* dq, void* dk, void* dv, float* dbias, char* ws, int N,
-             int H, int Sq, int Sk, float scale) {
+void run_bwd_v1(hipStream_t st, const BwdPlan& p, const void* q, const void* k, const void* v,
+                const void* bias, const uint8_t* kmask, const void* out, const void* dout,
+                const float* lse, void* dq, void* dk, void* dv, float* dbias, char* ws, int N,
+                int H, int Sq, int Sk, float scale) {
     using E = typename TR::elem;
     const int vec_ok = (Sk % 8 == 0) ? 1 : 0;
     float* di = reinterpret_cast<float*>(ws + p.off_di);
     float* dbias_part = reinterpret_cast<float*>(ws + p.off_dbias);
     float* dq_part = reinterpret_cast<float*>(ws + p.off_dq);
     const int64_t rows = (int64_t)N * H * Sq;
-    const size_t dbias_count = (size_t)H * Sq * Sk;
 
     {
         const int64_t threads = rows * (D / 8);
@@ -508,15 +1060,95 @@ void run_bwd(hipStream_t st, const BwdPlan& p, const void* q, const void* k, con
                                                   (const E*)bias, kmask, (const E*)dout, lse, di,
                                                   (E*)dk, (E*)dv, H, Sq, Sk, scale, vec_ok);
     }
-    if (p.nchunks > 1) {
-        KernelTimer timer("attn_bwd_dbias_sum", st);
-        sum_partials_f32<<<grid_for(dbias_count), 256, 0, st>>>(dbias_part, dbias_count,
-                                                                p.nchunks, dbias);
+    finish_partials<TR>(st, p, dbias_part, dq_part, dbias, dq, (size_t)H * Sq * Sk,
+                        (size_t)rows * D);
+}
+
+template <typename TR, int D, int KCW, bool VEC>
+void launch_dq2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, const void* v,
+                const void* bias, const uint8_t* kmask, const void* out, const void* dout,
+                const float* lse, const float* rowl, float* lse2, float* ndi, void* dq,
+                float* dq_part, float* dbias_dst, int N, int H, int Sq, int Sk, float scale) {
+    using E = typename TR::elem;
+    const dim3 grid(ceil_div(Sq, 64), H, p.nchunks * p.nranges);
+    KernelTimer timer("attn_bwd_dq", st);
+    attn_bwd_dq2<TR, D, KCW, VEC><<<grid, 512, 0, st>>>(
+        (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (const E*)out,
+        (const E*)dout, lse, rowl, lse2, ndi, (E*)dq, dq_part, dbias_dst, N, H, Sq, Sk, p.NB,
+        p.nranges, scale);
+}
+
+template <typename TR, int D, int KSUB, bool VEC>
+void launch_dkv2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, const void* v,
+                 const void* bias_t, const uint8_t* kmask, const void* dout, const float* lse2,
+                 const float* ndi, const float* rowl, void* dk, void* dv, int N, int H, int Sq,
+                 int Sk, float scale) {
+    using E = typename TR::elem;
+    const dim3 grid(ceil_div(Sk, 128 * KSUB), H, N);
+    KernelTimer timer("attn_bwd_dkv", st);
+    attn_bwd_dkv2<TR, D, KSUB, VEC><<<grid, 512, 0, st>>>(
+        (const E*)q, (const E*)k, (const E*)v, (const E*)bias_t, kmask, (const E*)dout, lse2,
+        ndi, rowl, (E*)dk, (E*)dv, H, Sq, Sk, p.SqP, scale);
+}
+
+template <typename TR, int D, bool VEC>
+void run_bwd_v2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, const void* v,
+                const void* bias, const uint8_t* kmask, const void* out, const void* dout,
+                const float* lse, void* dq, void* dk, void* dv, float* dbias, char* ws, int N,
+                int H, int Sq, int Sk, float scale) {
+    using E = typename TR::elem;
+    E* bias_t = reinterpret_cast<E*>(ws + p.off_bt);
+    float* rowl = reinterpret_cast<float*>(ws + p.off_rowl);
+    float* lse2 = reinterpret_cast<float*>(ws + p.off_lse2);
+    float* ndi = reinterpret_cast<float*>(ws + p.off_ndi);
+    float* dbias_part = reinterpret_cast<float*>(ws + p.off_dbias);
+    float* dq_part = reinterpret_cast<float*>(ws + p.off_dq);
+    {
+        const int tiles_q = ceil_div(p.SqP, 64), tiles_k = ceil_div(Sk, 64);
+        const int ntiles = H * tiles_q * tiles_k;
+        KernelTimer timer("attn_bwd_prep", st);
+        attn_bwd_prep<TR><<<ntiles + (kmask ? N : 0), 256, 0, st>>>(
+            (const E*)bias, bias_t, kmask, rowl, Sq, Sk, p.SqP, tiles_q, tiles_k, ntiles);
     }
-    if (p.nranges > 1) {
-        KernelTimer timer("attn_bwd_dq_sum", st);
-        sum_partials_cast<TR><<<grid_for((size_t)rows * D), 256, 0, st>>>(
-            dq_part, (size_t)rows * D, p.nranges, (E*)dq);
+    float* dbias_dst = p.nchunks > 1 ? dbias_part : dbias;
+    switch (p.KCW) {
+#define CLK_KCW(V)                                                                               \
+    case V:                                                                                      \
+        launch_dq2<TR, D, V, VEC>(st, p, q, k, v, bias, kmask, out, dout, lse, rowl, lse2, ndi,  \
+                                  dq, dq_part, dbias_dst, N, H, Sq, Sk, scale);                  \
+        break;
+        CLK_KCW(1) CLK_KCW(2) CLK_KCW(3)
+#undef CLK_KCW
+    }
+    switch (p.KSUB) {
+#define CLK_KSUB(V)                                                                              \
+    case V:                                                                                      \
+        launch_dkv2<TR, D, V, VEC>(st, p, q, k, v, bias_t, kmask, dout, lse2, ndi, rowl, dk, dv, \
+                                   N, H, Sq, Sk, scale);                                         \
+        break;
+        CLK_KSUB(1) CLK_KSUB(2) CLK_KSUB(3)
+#undef CLK_KSUB
+    }
+    finish_partials<TR>(st, p, dbias_part, dq_part, dbias, dq, (size_t)H * Sq * Sk,
+                        (size_t)N * H * Sq * D);
+}
+
+template <typename TR, int D>
+void run_bwd(hipStream_t st, const BwdPlan& p, const void* q, const void* k, const void* v,
+             const void* bias, const uint8_t* kmask, const void* out, const void* dout,
+             const float* lse, void* dq, void* dk, void* dv, float* dbias, char* ws, int N,
+             int H, int Sq, int Sk, float scale) {
+    if constexpr (D <= 32) {
+        const bool vec = Sk % 8 == 0 && (reinterpret_cast<uintptr_t>(kmask) & 7u) == 0;
+        if (vec)
+            run_bwd_v2<TR, D, true>(st, p, q, k, v, bias, kmask, out, dout, lse, dq, dk, dv,
+                                    dbias, ws, N, H, Sq, Sk, scale);
+        else
+            run_bwd_v2<TR, D, false>(st, p, q, k, v, bias, kmask, out, dout, lse, dq, dk, dv,
+                                     dbias, ws, N, H, Sq, Sk, scale);
+    } else {
+        run_bwd_v1<TR, D>(st, p, q, k, v, bias, kmask, out, dout, lse, dq, dk, dv, dbias, ws, N,
+                          H, Sq, Sk, scale);
     }
 }
 

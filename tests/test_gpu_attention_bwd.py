@@ -20,7 +20,9 @@ CASES = [
     (1, 1, 1, 1, 32, 0.0, 0),
     (5, 3, 257, 129, 32, 0.05, 2),
     (2, 2, 33, 300, 64, 0.0, 0),
-    (4, 2, 96, 600, 32, 0.1, 1),   # Sk > 512: two key ranges, dQ partials
+    (4, 2, 96, 600, 32, 0.1, 1),   # Sk > 384: two key ranges, dQ partials
+    (3, 2, 70, 456, 16, 0.1, 1),   # D = 16 over two key ranges
+    (2, 1, 16, 8, 8, 0.0, 0),
 ]
 
 
