@@ -641,23 +641,28 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
                     dp[qt][t] = TR::mfma(vf[t], dof[qt], f32x4{-di[qt], -di[qt], -di[qt], -di[qt]});
                 }
             const bool nm = kbeg + c0 + 32 > Sk || __any(has_zero_byte(maskc[i]));
-            const unsigned valid = nm ? nonzero_bits8(maskc[i]) : 0xffu;
             V8 dsf[2];
 #pragma unroll
             for (int qt = 0; qt < 2; ++qt) {
-                float b[8];
+                float b[8], x[8];
                 unpack8<TR>(braw[i][qt], b);
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int t = j >> 2, e = j & 3;
-                    float x = fmaf(s[qt][t][e], scale, b[j]);
-                    if (nm) {
+                for (int j = 0; j < 8; ++j) x[j] = fmaf(s[qt][j >> 2][j & 3], scale, b[j]);
+                if (nm) {
+                    // Opaque to speculation: keeps the selects out of the unmasked path.
+                    asm volatile("");
+                    const unsigned valid = nonzero_bits8(maskc[i]);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
                         const int key = kbeg + c0 + 8 * g + j;
-                        x = key >= Sk ? -INFINITY : (((valid >> j) & 1u) ? x : mlc);
+                        x[j] = key >= Sk ? -INFINITY : (((valid >> j) & 1u) ? x[j] : mlc);
                     }
-                    const float p = fast_exp2(fmaf(x, kLog2e, -lse2c[qt]));
-                    const float ds = p * dp[qt][t][e];
-                    dbias[i][qt][t][e] += ds;
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float p = fast_exp2(fmaf(x[j], kLog2e, -lse2c[qt]));
+                    const float ds = p * dp[qt][j >> 2][j & 3];
+                    dbias[i][qt][j >> 2][j & 3] += ds;
                     dsf[qt][j] = TR::from_f(ds);
                 }
             }
@@ -761,7 +766,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv2(
 
     const float ml = kmask ? row_logit[n] : kMaskedLogit;
     V8 kf[KSUB], vf[KSUB];
-    bool present[KSUB];
+    bool present[KSUB], clean[KSUB];
     float absent_logit[KSUB];
 #pragma unroll
     for (int s = 0; s < KSUB; ++s) {
@@ -776,6 +781,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv2(
         vf[s] = bits_as<V8>(rv);
         present[s] = kin && (kmask == nullptr || kmask[(size_t)n * Sk + key] != 0);
         absent_logit[s] = kin ? ml : -INFINITY;
+        clean[s] = __all(present[s]);  // wave-uniform: no absent key in the sub-tile
     }
 
     f32x4 dka[KSUB][DT], dva[KSUB][DT];
@@ -849,12 +855,20 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv2(
                 unpack8<TR>(*reinterpret_cast<const u32x4*>(
                                 bt + row * 128 + 16 * ((4 * c + g) ^ (row & 7))),
                             b);
+                float x[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) x[j] = fmaf(S[j >> 2][j & 3], scale, b[j]);
+                if (!clean[s]) {
+                    // Opaque to speculation: keeps the selects out of the common path.
+                    asm volatile("");
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) x[j] = present[s] ? x[j] : absent_logit[s];
+                }
                 V8 pf, dsf;
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const int t = j >> 2, e = j & 3;
-                    const float x = present[s] ? fmaf(S[t][e], scale, b[j]) : absent_logit[s];
-                    const float p = fast_exp2(fmaf(x, kLog2e, -l4[t][e]));
+                    const float p = fast_exp2(fmaf(x[j], kLog2e, -l4[t][e]));
                     const float ds = p * dP[t][e];
                     pf[j] = TR::from_f(p);
                     dsf[j] = TR::from_f(ds);

@@ -214,6 +214,8 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
                 }
             }
             if (need_mask) {
+                // Opaque to speculation: keeps the selects out of the unmasked path.
+                asm volatile("");
 #pragma unroll
                 for (int c = 0; c < 2; ++c) {
                     const unsigned valid = cur[qt][c].valid();

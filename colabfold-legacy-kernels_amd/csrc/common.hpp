@@ -20,6 +20,7 @@
 #include <cstdio>
 #include <cstdarg>
 #include <string>
+#include <type_traits>
 
 #include "clk.h"
 
