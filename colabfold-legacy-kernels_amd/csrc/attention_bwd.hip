@@ -641,31 +641,36 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
                     dp[qt][t] = TR::mfma(vf[t], dof[qt], f32x4{-di[qt], -di[qt], -di[qt], -di[qt]});
                 }
             const bool nm = kbeg + c0 + 32 > Sk || __any(has_zero_byte(maskc[i]));
-            V8 dsf[2];
+            float x[2][8];
 #pragma unroll
             for (int qt = 0; qt < 2; ++qt) {
-                float b[8], x[8];
+                float b[8];
                 unpack8<TR>(braw[i][qt], b);
 #pragma unroll
-                for (int j = 0; j < 8; ++j) x[j] = fmaf(s[qt][j >> 2][j & 3], scale, b[j]);
-                if (nm) {
-                    // Opaque to speculation: keeps the selects out of the unmasked path.
-                    asm volatile("");
-                    const unsigned valid = nonzero_bits8(maskc[i]);
+                for (int j = 0; j < 8; ++j) x[qt][j] = fmaf(s[qt][j >> 2][j & 3], scale, b[j]);
+            }
+            if (nm) {
+                // One block for the chunk, opaque to speculation: nothing of it is hoisted into
+                // (or merged across sub-tiles onto) the unmasked path.
+                asm volatile("");
+                const unsigned valid = nonzero_bits8(maskc[i]);
+                const int lim = Sk - (kbeg + c0 + 8 * g);  // keys j >= lim are past Sk
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const int key = kbeg + c0 + 8 * g + j;
-                        x[j] = key >= Sk ? -INFINITY : (((valid >> j) & 1u) ? x[j] : mlc);
-                    }
-                }
+                for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        x[qt][j] = j >= lim ? -INFINITY : (((valid >> j) & 1u) ? x[qt][j] : mlc);
+            }
+            V8 dsf[2];
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const float p = fast_exp2(fmaf(x[j], kLog2e, -lse2c[qt]));
+                    const float p = fast_exp2(fmaf(x[qt][j], kLog2e, -lse2c[qt]));
                     const float ds = p * dp[qt][j >> 2][j & 3];
                     dbias[i][qt][j >> 2][j & 3] += ds;
                     dsf[qt][j] = TR::from_f(ds);
                 }
-            }
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) {
                 const V8 kt = swz_tr_operand<V8, D>(kvc, c0, dt, r16, g);

@@ -49,47 +49,53 @@ __device__ __forceinline__ float tile_flags(const uint8_t* mrow, int Sk, int* fl
     return (mrow && !any) ? 0.f : kMaskedLogit;
 }
 
-// Eight consecutive keys' bias values and mask bytes of one tile, as loaded. VEC: 16-byte bias
-// and 8-byte mask loads (Sk % 8 == 0, 8-byte aligned mask rows); a lane whose eight keys lie past
-// Sk reads the last eight instead (those keys are forced to -inf). Otherwise element loads.
-template <typename TR, bool VEC>
-struct KeyChunk {
-    u32x4 bias;
-    u32x2 mask;
-    __device__ __forceinline__ void load(const typename TR::elem* brow, const uint8_t* mrow,
-                                         int kk, int Sk) {
+// Per-lane prefetch state of one key tile: the mask bytes of keys k0 + 32c + 8g + 0..7 (c = 0, 1)
+// and, unless the bias tile travels through LDS (VEC), the bias of those keys for each of the
+// lane's query rows. VEC (Sk % 8 == 0, 8-byte aligned mask rows): 8-byte mask loads whose address
+// is clamped into the row (keys past Sk are forced to -inf anyway); otherwise element loads.
+template <typename TR, int QT, bool VEC>
+struct TilePrefetch {
+    u32x2 mask[2];
+    u32x4 bias[VEC ? 1 : QT][2];
+    __device__ __forceinline__ void load(const typename TR::elem* const* brow,
+                                         const uint8_t* mrow, int k0, int g, int Sk) {
         using E = typename TR::elem;
-        if constexpr (VEC) {
-            const int kc = min(kk, Sk - 8);
-            bias = ld16(brow + kc);
-            mask = mrow ? *reinterpret_cast<const u32x2*>(mrow + kc) : u32x2{~0u, ~0u};
-        } else {
-            E e[8];
-            uint8_t m[8];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const bool in = kk + j < Sk;
-                e[j] = in ? brow[kk + j] : E(0.f);
-                m[j] = in ? (mrow ? mrow[kk + j] : uint8_t(1)) : uint8_t(0);
+        for (int c = 0; c < 2; ++c) {
+            const int kk = k0 + 32 * c + 8 * g;
+            if constexpr (VEC) {
+                mask[c] = mrow ? *reinterpret_cast<const u32x2*>(mrow + min(kk, Sk - 8))
+                               : u32x2{~0u, ~0u};
+            } else {
+                uint8_t m[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    m[j] = kk + j < Sk ? (mrow ? mrow[kk + j] : uint8_t(1)) : uint8_t(0);
+                __builtin_memcpy(&mask[c], m, 8);
+#pragma unroll
+                for (int qt = 0; qt < QT; ++qt) {
+                    E e[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) e[j] = kk + j < Sk ? brow[qt][kk + j] : E(0.f);
+                    __builtin_memcpy(&bias[qt][c], e, 16);
+                }
             }
-            __builtin_memcpy(&bias, e, 16);
-            __builtin_memcpy(&mask, m, 8);
         }
     }
-    // Bit j set when key kk + j is present.
-    __device__ __forceinline__ unsigned valid() const {
+    // Bit j set when key k0 + 32c + 8g + j is present.
+    __device__ __forceinline__ unsigned valid(int c) const {
         unsigned bits = 0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-            bits |= (((mask[0] >> (8 * j)) & 0xffu) != 0u ? 1u : 0u) << j;
-            bits |= (((mask[1] >> (8 * j)) & 0xffu) != 0u ? 1u : 0u) << (4 + j);
+            bits |= (((mask[c][0] >> (8 * j)) & 0xffu) != 0u ? 1u : 0u) << j;
+            bits |= (((mask[c][1] >> (8 * j)) & 0xffu) != 0u ? 1u : 0u) << (4 + j);
         }
         return bits;
     }
 };
 
 template <typename TR, int D, int QT, bool VEC>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && VEC ? 3 : 1))) void attn_fwd_kernel(
     const typename TR::elem* __restrict__ q, const typename TR::elem* __restrict__ k,
     const typename TR::elem* __restrict__ v, const typename TR::elem* __restrict__ bias,
     const uint8_t* __restrict__ kmask, typename TR::elem* __restrict__ out,
@@ -98,12 +104,16 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
     using V8 = typename TR::vec8;
     using G = AttnGeom<D>;
     using T = SwzTile<D>;
-    using KC = KeyChunk<TR, VEC>;
+    using PF = TilePrefetch<TR, QT, VEC>;
     constexpr int BQ = 4 * 16 * QT;
     constexpr int BK = G::BK;
     constexpr int TILE = BK * T::ROWB;  // bytes of one K or V tile
+    constexpr int BTILE = VEC ? BQ * 128 : 0;  // bias tile: BQ query rows of 64 keys
 
-    __shared__ __attribute__((aligned(16))) char kv_lds[2][2][TILE];  // [buffer][K, V]
+    // Two K/V buffers as separate LDS objects: the compiler then knows that reads of one do not
+    // wait for the direct-to-LDS loads into the other.
+    __shared__ __attribute__((aligned(16))) char kv0[2 * TILE + BTILE];  // K rows, V rows, bias
+    __shared__ __attribute__((aligned(16))) char kv1[2 * TILE + BTILE];
     __shared__ int flags[kMaxFlagTiles];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -118,10 +128,26 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
     const int qbase = q0 + wave * 16 * QT;
     const int ntiles = (Sk + BK - 1) / BK;
 
-    if (ntiles > 0) {
-        stage_rows_async<D, BK, 256>(kp, 0, Sk, kv_lds[0][0]);
-        stage_rows_async<D, BK, 256>(vp, 0, Sk, kv_lds[0][1]);
-    }
+    auto stage = [&](int k0, char* kv) {
+        stage_rows_async<D, BK, 256>(kp, k0, Sk, kv);
+        stage_rows_async<D, BK, 256>(vp, k0, Sk, kv + TILE);
+        if constexpr (VEC) {
+            // Bias rows q0 .. q0+BQ-1, keys k0 .. k0+63 as eight 16-byte pieces per row; piece
+            // p of row r sits at position p ^ (r & 7), so a 16-row operand read is conflict-free.
+#pragma unroll
+            for (int base = wave * 64; base < BQ * 8; base += 256) {
+                const int slot = base + lane;
+                const int row = slot >> 3, piece = (slot & 7) ^ (row & 7);
+                const int qq = q0 + row, kk = k0 + 8 * piece;
+                const void* src = kZero16;
+                if (qq < Sq && kk < Sk) src = bp + (size_t)qq * Sk + kk;
+                __builtin_amdgcn_global_load_lds(
+                    src, (__attribute__((address_space(3))) void*)(kv + 2 * TILE + base * 16), 16,
+                    0, 0);
+            }
+        }
+    };
+    if (ntiles > 0) stage(0, kv0);
     const float masked_logit = tile_flags(mp, Sk, flags);
 
     // B operand Q^T: lane (query r16, group g) holds head dims 32*ks + 8*g + 0..7.
@@ -142,52 +168,45 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
     const E* brow[QT];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) brow[qt] = bp + (size_t)min(qbase + qt * 16 + r16, Sq - 1) * Sk;
-    KC cur[QT][2], nxt[QT][2];
-    auto load_chunks = [&](int k0, KC (&kc)[QT][2]) {
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-            for (int c = 0; c < 2; ++c) kc[qt][c].load(brow[qt], mp, k0 + 32 * c + 8 * g, Sk);
-    };
-    if (ntiles > 0) load_chunks(0, cur);
+    PF ca, cb;
+    if (ntiles > 0) ca.load(brow, mp, 0, g, Sk);
 
-    float m_run[QT], l_run[QT];
-    f32x4 acc[QT][G::DT];
+    // Running max, and O^T plus one extra accumulator per sub-tile: the MFMA of an all-ones
+    // A operand with P^T, i.e. the row sum of the (rounded) P that the P.V product uses.
+    V8 ones;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ones[j] = TR::from_f(1.f);
+    float m_run[QT];
+    f32x4 acc[QT][G::DT], lsum[QT];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
         m_run[qt] = -INFINITY;
-        l_run[qt] = 0.f;
+        lsum[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int dt = 0; dt < G::DT; ++dt) acc[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     }
 
-    for (int kt = 0; kt < ntiles; ++kt) {
+    auto tile = [&](int kt, const char* kvc, char* kvn, PF& cur, PF& nxt) {
         const int k0 = kt * BK;
-        const char* k_lds = kv_lds[kt & 1][0];
-        const char* v_lds = kv_lds[kt & 1][1];
         async_wait();
         __syncthreads();  // tile kt visible; every wave is done with the other buffer
-
-        // Everything this tile needs from LDS is read before the next tile's direct-to-LDS
-        // loads are issued, so no LDS read waits for them.
         const bool need_mask = kt >= kMaxFlagTiles || flags[kt] != 0;
+        if (kt + 1 < ntiles) {
+            stage(k0 + BK, kvn);
+            nxt.load(brow, mp, k0 + BK, g, Sk);
+        }
         V8 kf[4][G::KS];
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
             for (int ks = 0; ks < G::KS; ++ks)
-                kf[t][ks] = swz_row_operand<V8, D>(k_lds, perm_key(t, r16), ks, g);
+                kf[t][ks] = swz_row_operand<V8, D>(kvc, perm_key(t, r16), ks, g);
         V8 vf[G::DT][2];
 #pragma unroll
         for (int dt = 0; dt < G::DT; ++dt)
 #pragma unroll
-            for (int c = 0; c < 2; ++c) vf[dt][c] = swz_tr_operand<V8, D>(v_lds, 32 * c, dt, r16, g);
-
-        if (kt + 1 < ntiles) {
-            stage_rows_async<D, BK, 256>(kp, k0 + BK, Sk, kv_lds[(kt + 1) & 1][0]);
-            stage_rows_async<D, BK, 256>(vp, k0 + BK, Sk, kv_lds[(kt + 1) & 1][1]);
-            load_chunks(k0 + BK, nxt);
-        }
+            for (int c = 0; c < 2; ++c)
+                vf[dt][c] = swz_tr_operand<V8, D>(kvc + TILE, 32 * c, dt, r16, g);
 
         // S^T = K . Q^T for the four 16-key sub-tiles (chunk c = t/2, half t%2).
         f32x4 s[QT][4];
@@ -200,54 +219,63 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
                     s[qt][t] = TR::mfma(kf[t][ks], qf[qt][ks],
                                         ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : s[qt][t]);
 
+        float x[QT][2][8];
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) {
-            float x[2][8];
+        for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
                 float bv[8];
-                unpack8<TR>(cur[qt][c].bias, bv);
+                if constexpr (VEC) {
+                    const int row = wave * 16 * QT + 16 * qt + r16;
+                    unpack8<TR>(*reinterpret_cast<const u32x4*>(
+                                    kvc + 2 * TILE + row * 128 + 16 * ((4 * c + g) ^ (row & 7))),
+                                bv);
+                } else {
+                    unpack8<TR>(cur.bias[qt][c], bv);
+                }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    x[c][j] = fmaf(s[qt][2 * c][j], scale, bv[j]);
-                    x[c][4 + j] = fmaf(s[qt][2 * c + 1][j], scale, bv[4 + j]);
+                    x[qt][c][j] = fmaf(s[qt][2 * c][j], scale, bv[j]);
+                    x[qt][c][4 + j] = fmaf(s[qt][2 * c + 1][j], scale, bv[4 + j]);
                 }
             }
-            if (need_mask) {
-                // Opaque to speculation: keeps the selects out of the unmasked path.
-                asm volatile("");
+        if (need_mask) {
+            // One block for the whole tile, opaque to speculation: nothing of it is hoisted
+            // into (or merged across sub-tiles onto) the unmasked path.
+            asm volatile("");
 #pragma unroll
-                for (int c = 0; c < 2; ++c) {
-                    const unsigned valid = cur[qt][c].valid();
+            for (int c = 0; c < 2; ++c) {
+                const int lim = Sk - (k0 + 32 * c + 8 * g);  // keys j >= lim are past Sk
+                const unsigned valid = cur.valid(c);
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const int key = k0 + 32 * c + 8 * g + j;
-                        x[c][j] = key >= Sk ? -INFINITY
-                                            : (((valid >> j) & 1u) ? x[c][j] : masked_logit);
-                    }
-                }
+                for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        x[qt][c][j] = j >= lim ? -INFINITY
+                                               : (((valid >> j) & 1u) ? x[qt][c][j] : masked_logit);
             }
-            float mt = x[0][0];
+        }
+
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+            float mt = x[qt][0][0];
 #pragma unroll
             for (int c = 0; c < 2; ++c)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) mt = fmaxf(mt, x[c][j]);
+                for (int j = 0; j < 8; ++j) mt = fmaxf(mt, x[qt][c][j]);
             mt = xgroup_max(mt);
             const float m_new = fmaxf(m_run[qt], mt);
             const float alpha = fast_exp2((m_run[qt] - m_new) * kLog2e);
             const float neg = -m_new * kLog2e;
-            float psum = 0.f;
             V8 pf[2];
 #pragma unroll
             for (int c = 0; c < 2; ++c)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float p = fast_exp2(fmaf(x[c][j], kLog2e, neg));
-                    psum += p;
-                    pf[c][j] = TR::from_f(p);
-                }
-            l_run[qt] = l_run[qt] * alpha + psum;
+                for (int j = 0; j < 8; ++j) pf[c][j] = TR::from_f(fast_exp2(fmaf(x[qt][c][j], kLog2e, neg)));
             m_run[qt] = m_new;
+            lsum[qt][0] *= alpha;  // only component 0 is read
+#pragma unroll
+            for (int c = 0; c < 2; ++c) lsum[qt] = TR::mfma(ones, pf[c], lsum[qt]);
 #pragma unroll
             for (int dt = 0; dt < G::DT; ++dt) {
                 acc[qt][dt] *= alpha;
@@ -255,16 +283,16 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(
                 for (int c = 0; c < 2; ++c) acc[qt][dt] = TR::mfma(vf[dt][c], pf[c], acc[qt][dt]);
             }
         }
-#pragma unroll
-        for (int qt = 0; qt < QT; ++qt)
-#pragma unroll
-            for (int c = 0; c < 2; ++c) cur[qt][c] = nxt[qt][c];
+    };
+    for (int kt = 0; kt < ntiles; kt += 2) {
+        tile(kt, kv0, kv1, ca, cb);
+        if (kt + 1 < ntiles) tile(kt + 1, kv1, kv0, cb, ca);
     }
 
     // Normalise and store: lane holds O[row][16*dt + 4*g + i], i = 0..3.
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-        const float l_tot = xgroup_sum(l_run[qt]);
+        const float l_tot = lsum[qt][0];
         const float inv = 1.0f / fmaxf(l_tot, 1e-30f);
         const int row = qbase + qt * 16 + r16;
         if (row >= Sq) continue;
