@@ -12,6 +12,11 @@ LayerNorm + gated dual projection on the 512x512x128 pair representation, in HBM
 The roofline block names the kernel with the most time per step, its algorithmic work per launch
 divided by its average duration from per-launch HIP events on the launch stream (the library's
 clk_profile_* hooks), against MI355X's dense bf16 MFMA peak (2516.6 TFLOP/s) or HBM (8 TB/s).
+roofline.traffic is the dominant kernel's HBM bytes per launch as recorded by the committed
+rocprofv3 FETCH_SIZE/WRITE_SIZE summaries in profiles/*hbm_traffic*.md (lines
+"traffic_bytes_per_launch[<kernel>]: <bytes>"), null when none covers the kernel. Those runs
+scale each counter by what it reads for a plain device copy of known size, which
+"--copy-calibration MIB" performs (and nothing else).
 cpu_baseline times the same math in torch float32 on the host cores (oracle/cpu_baseline.py) on
 a bounded sample of rows, scaled to the same unit.
 """
@@ -20,6 +25,7 @@ import argparse
 import json
 import math
 import os
+import re
 import sys
 import time
 from pathlib import Path
@@ -188,6 +194,34 @@ def bench_ln_gdp(torch, workloads, native, dev, stream, steps, warmup):
             "ln_gdp_TFLOPs": 4 * 2.0 * m * c * n / (t * 1e-3) / 1e12}
 
 
+def recorded_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summaries."""
+    pat = re.compile(r"^traffic_bytes_per_launch\[(\w+)\]:\s*([0-9.eE+]+)\s*$")
+    found = None
+    for f in sorted((ROOT / "profiles").glob("*hbm_traffic*.md")):
+        for line in f.read_text().splitlines():
+            m = pat.match(line.strip())
+            if m and m.group(1) == kernel:
+                found = float(m.group(2))
+    return found
+
+
+def copy_calibration(mib, reps=5):
+    """A plain device-to-device copy of `mib` MiB, `reps` times: the known-size reference that
+    the FETCH_SIZE / WRITE_SIZE counters are scaled by (reads and writes mib MiB each)."""
+    import torch
+    dev = torch.device("cuda:0")
+    n = mib * (1 << 20) // 4
+    a = torch.randn(n, device=dev)
+    b = torch.empty_like(a)
+    for _ in range(reps):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "reps": reps}),
+          flush=True)
+    return 0
+
+
 def cpu_baseline(torch, workloads, rows, min_seconds):
     from oracle import cpu_baseline as cb
     cores = _cores()
@@ -210,7 +244,11 @@ def main(argv=None):
     ap.add_argument("--cpu-rows", type=int, default=64)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-secondary", action="store_true")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (counter calibration)")
     args = ap.parse_args(argv)
+    if args.copy_calibration:
+        return copy_calibration(args.copy_calibration)
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the attention rows "
               "would shard across GPUs with one dBias all-reduce; not built). Use --gpus 1.",
@@ -243,7 +281,7 @@ def main(argv=None):
     achieved = dom_flops / (kernels[dom]["avg_ms"] * 1e-3) / 1e12 if dom_flops else None
     roofline = {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": MFMA_PEAK_BF16,
                 "unit": "TFLOP/s", "frac": (achieved / MFMA_PEAK_BF16) if achieved else None,
-                "traffic": None, "avg_ms": kernels[dom]["avg_ms"],
+                "traffic": recorded_traffic(dom), "avg_ms": kernels[dom]["avg_ms"],
                 "algorithmic_flops_per_launch": dom_flops}
 
     result = {

@@ -512,8 +512,13 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r16 = lane & 15, g = lane >> 4;
     const int qg = wave >> 2, kq = wave & 3;
-    const int q0 = blockIdx.x * BQ, h = blockIdx.y;
-    const int chunk = blockIdx.z / nranges, range = blockIdx.z % nranges;
+    // 1-D grid of (query tile, head, key range, row chunk) work items, query tile fastest,
+    // placed so that the query tiles that stream the same K/V rows share an XCD's L2.
+    const int qtiles = (Sq + BQ - 1) / BQ;
+    const int item = xcd_contiguous(blockIdx.x, gridDim.x);
+    const int q0 = (item % qtiles) * BQ, h = (item / qtiles) % H;
+    const int zr = item / (qtiles * H);
+    const int range = zr % nranges, chunk = zr / nranges;
     const int kbeg = range * RK, kend = min(Sk, kbeg + RK);
     const int n0 = chunk * NB, n1 = min(N, n0 + NB);
     int qrow[2];
@@ -1089,7 +1094,7 @@ void launch_dq2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, 
                 const float* lse, const float* rowl, float* lse2, float* ndi, void* dq,
                 float* dq_part, float* dbias_dst, int N, int H, int Sq, int Sk, float scale) {
     using E = typename TR::elem;
-    const dim3 grid(ceil_div(Sq, 64), H, p.nchunks * p.nranges);
+    const dim3 grid(ceil_div(Sq, 64) * H * p.nchunks * p.nranges);
     KernelTimer timer("attn_bwd_dq", st);
     attn_bwd_dq2<TR, D, KCW, VEC><<<grid, 512, 0, st>>>(
         (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (const E*)out,

@@ -118,7 +118,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r16 = lane & 15, g = lane >> 4;
-    const int q0 = blockIdx.x * BQ, h = blockIdx.y, n = blockIdx.z;
+    // 1-D grid of (query tile, head, row) work items, query tile fastest, placed so that the
+    // query tiles of one (row, head) -- which read the same K and V -- share an XCD's L2.
+    const int qtiles = (Sq + BQ - 1) / BQ;
+    const int item = xcd_contiguous(blockIdx.x, gridDim.x);
+    const int q0 = (item % qtiles) * BQ, h = (item / qtiles) % H, n = item / (qtiles * H);
     const size_t nh = (size_t)n * H + h;
     const E* qp = q + nh * Sq * D;
     const E* kp = k + nh * Sk * D;
@@ -311,7 +315,7 @@ void launch_fwd_qt(hipStream_t st, const void* q, const void* k, const void* v, 
                    const uint8_t* kmask, void* out, float* lse, int N, int H, int Sq, int Sk,
                    float scale) {
     using E = typename TR::elem;
-    const dim3 grid(ceil_div(Sq, 64 * QT), H, N);
+    const dim3 grid(ceil_div(Sq, 64 * QT) * H * N);
     const bool vec = Sk % 8 == 0 && (reinterpret_cast<uintptr_t>(kmask) & 7u) == 0;
     if (vec)
         attn_fwd_kernel<TR, D, QT, true><<<grid, 256, 0, st>>>(

@@ -125,6 +125,17 @@ __device__ __forceinline__ float xgroup_sum(float v) {
     return __uint_as_float(p[0]) + __uint_as_float(p[1]);
 }
 
+// Work item of workgroup L out of T so that each XCD runs a contiguous range of work items.
+// The dispatcher hands workgroup L to XCD L % 8 (each XCD has its own L2), so with the identity
+// mapping neighbouring work items -- which share inputs -- land on different L2s. A bijection
+// of [0, T): results never depend on it, only the L2 hit rate does.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_contiguous(int L, int T) {
+    const int xcd = L % kXcds, slot = L / kXcds;
+    const int per = T / kXcds, rem = T % kXcds;
+    return xcd * per + min(xcd, rem) + slot;
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_rcp(float x) { return __builtin_amdgcn_rcpf(x); }
 
