@@ -446,7 +446,7 @@ __global__ __launch_bounds__(256) void attn_bwd_prep(const typename TR::elem* __
                                                      int Sk, int SqP, int tiles_q, int tiles_k,
                                                      int ntiles) {
     using E = typename TR::elem;
-    __shared__ E tile[64][66];
+    __shared__ __attribute__((aligned(16))) E tile[64][72];  // rows 144 B: 16-byte reads
     if ((int)blockIdx.x >= ntiles) {
         const int n = blockIdx.x - ntiles;
         const uint8_t* m = kmask + (size_t)n * Sk;
@@ -461,16 +461,37 @@ __global__ __launch_bounds__(256) void attn_bwd_prep(const typename TR::elem* __
     t /= tiles_k;
     const int tq = t % tiles_q, h = t / tiles_q;
     const int q0 = tq * 64, k0 = tk * 64;
-    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
-        const int r = i >> 6, c = i & 63;  // r: query, c: key
-        const int qq = q0 + r, kk = k0 + c;
-        tile[c][r] = (qq < Sq && kk < Sk) ? bias[((size_t)h * Sq + qq) * Sk + kk] : E(0.f);
+    // Loads: 16-byte pieces of 8 keys of one query row (two per thread) when the piece lies
+    // inside the row and the rows are 16-byte aligned; element loads otherwise.
+    const bool vec = Sk % 8 == 0;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int ch = threadIdx.x + 256 * i;
+        const int r = ch >> 3, c8 = (ch & 7) * 8;  // r: query, c8: first key
+        const int qq = q0 + r, kk = k0 + c8;
+        E e[8];
+        if (vec && qq < Sq && kk + 8 <= Sk) {
+            const u32x4 raw = ld16(bias + ((size_t)h * Sq + qq) * Sk + kk);
+            __builtin_memcpy(e, &raw, 16);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                e[j] = (qq < Sq && kk + j < Sk) ? bias[((size_t)h * Sq + qq) * Sk + kk + j]
+                                                : E(0.f);
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) tile[c8 + j][r] = e[j];
     }
     __syncthreads();
-    for (int i = threadIdx.x; i < 64 * 64; i += 256) {
-        const int r = i >> 6, c = i & 63;  // r: key, c: query
-        const int kk = k0 + r, qq = q0 + c;
-        if (kk < Sk && qq < SqP) bias_t[((size_t)h * Sk + kk) * SqP + qq] = tile[r][c];
+    // Stores: 16-byte pieces of 8 queries of one key row (SqP % 8 == 0 keeps them aligned).
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int ch = threadIdx.x + 256 * i;
+        const int r = ch >> 3, c8 = (ch & 7) * 8;  // r: key, c8: first query
+        const int kk = k0 + r, qq = q0 + c8;
+        if (kk < Sk && qq < SqP)
+            st16(bias_t + ((size_t)h * Sk + kk) * SqP + qq,
+                 *reinterpret_cast<const u32x4*>(&tile[r][c8]));
     }
 }
 
@@ -934,6 +955,30 @@ __global__ __launch_bounds__(256) void sum_partials_f32(const float* __restrict_
     }
 }
 
+// The same sum four elements at a time (count4 = count / 4, 16-byte aligned arrays), with four
+// partials in flight; the additions keep the order p = 0, 1, 2, ...
+__global__ __launch_bounds__(256) void sum_partials_f32x4(const f32x4* __restrict__ part,
+                                                          size_t count4, int nparts,
+                                                          f32x4* __restrict__ out) {
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < count4;
+         i += (size_t)gridDim.x * 256) {
+        f32x4 a = {0.f, 0.f, 0.f, 0.f};
+        int p = 0;
+        for (; p + 4 <= nparts; p += 4) {
+            const f32x4 v0 = part[(size_t)p * count4 + i];
+            const f32x4 v1 = part[(size_t)(p + 1) * count4 + i];
+            const f32x4 v2 = part[(size_t)(p + 2) * count4 + i];
+            const f32x4 v3 = part[(size_t)(p + 3) * count4 + i];
+            a += v0;
+            a += v1;
+            a += v2;
+            a += v3;
+        }
+        for (; p < nparts; ++p) a += part[(size_t)p * count4 + i];
+        out[i] = a;
+    }
+}
+
 template <typename TR>
 __global__ __launch_bounds__(256) void sum_partials_cast(const float* __restrict__ part,
                                                          size_t count, int nparts,
@@ -1036,8 +1081,13 @@ void finish_partials(hipStream_t st, const BwdPlan& p, float* dbias_part, float*
     using E = typename TR::elem;
     if (p.nchunks > 1) {
         KernelTimer timer("attn_bwd_dbias_sum", st);
-        sum_partials_f32<<<grid_for(dbias_count), 256, 0, st>>>(dbias_part, dbias_count,
-                                                                p.nchunks, dbias);
+        if (dbias_count % 4 == 0)  // partial arrays are then 16-byte aligned
+            sum_partials_f32x4<<<grid_for(dbias_count / 4), 256, 0, st>>>(
+                reinterpret_cast<const f32x4*>(dbias_part), dbias_count / 4, p.nchunks,
+                reinterpret_cast<f32x4*>(dbias));
+        else
+            sum_partials_f32<<<grid_for(dbias_count), 256, 0, st>>>(dbias_part, dbias_count,
+                                                                    p.nchunks, dbias);
     }
     if (p.nranges > 1) {
         KernelTimer timer("attn_bwd_dq_sum", st);
