@@ -435,7 +435,7 @@ __device__ __forceinline__ u32x2 mask_bytes8(const uint8_t* mrow, int kk, int Sk
     }
 }
 
-// Prep: bias [H][Sq][Sk] -> bias_t [H][Sk][SqP] (SqP = Sq rounded up to 8, padding zero) in
+// Prep: bias [H][Sq][Sk] -> bias_t [H][Sk][SqP] (SqP = Sq rounded up to 64, padding zero) in
 // 64x64 tiles through LDS, and per mask row the logit its absent keys take (-1e9, or 0 when the
 // row has no present key). Blocks [0, ntiles) transpose, blocks [ntiles, ntiles + N) do rows.
 template <typename TR>
@@ -574,11 +574,12 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
 
     auto stage = [&](int n, char* kv, char* qd) {
         const size_t nh = (size_t)n * H + h;
-        stage_rows_async<D, RK, 512>(k + nh * Sk * D, kbeg, Sk, kv);
-        stage_rows_async<D, RK, 512>(v + nh * Sk * D, kbeg, Sk, kv + KVB);
-        stage_rows_async<D, BQ, 512>(q + nh * Sq * D, q0, Sq, qd);
-        stage_rows_async<D, BQ, 512>(dout + nh * Sq * D, q0, Sq, qd + QB);
-        stage_rows_async<D, BQ, 512>(out + nh * Sq * D, q0, Sq, qd + 2 * QB);
+        const uint32_t kb = (uint32_t)Sk * D * 2, qb = (uint32_t)Sq * D * 2;
+        stage_rows<D, RK, 512>(buffer_rsrc(k + nh * Sk * D, kb), kbeg, kv);
+        stage_rows<D, RK, 512>(buffer_rsrc(v + nh * Sk * D, kb), kbeg, kv + KVB);
+        stage_rows<D, BQ, 512>(buffer_rsrc(q + nh * Sq * D, qb), q0, qd);
+        stage_rows<D, BQ, 512>(buffer_rsrc(dout + nh * Sq * D, qb), q0, qd + QB);
+        stage_rows<D, BQ, 512>(buffer_rsrc(out + nh * Sq * D, qb), q0, qd + 2 * QB);
     };
     // Per-row values kept in registers one row ahead, raw: anything computed from them right
     // after the load would wait for the row's direct-to-LDS loads too.
@@ -824,33 +825,30 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv2(
             dva[s][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
 
+    const uint32_t qbytes = (uint32_t)Sq * D * 2;
+    const Rsrc rq = buffer_rsrc(q + nh * Sq * D, qbytes);
+    const Rsrc rdo = buffer_rsrc(dout + nh * Sq * D, qbytes);
+    // The block's transposed-bias rows (keys k0 .. k0+KB-1 that exist) and the two per-query
+    // vectors of (n, h).
+    const Rsrc rbt = buffer_rsrc(bias_t + ((size_t)h * Sk + k0) * SqP,
+                                 (uint32_t)(min(KB, Sk - k0) * SqP * 2));
+    const Rsrc rl = buffer_rsrc(lse2 + nh * Sq, (uint32_t)Sq * 4);
+    const Rsrc rn = buffer_rsrc(ndi + nh * Sq, (uint32_t)Sq * 4);
     auto stage = [&](int qs, char* qd, char* bt, float* st) {
-        stage_rows_async<D, 64, 512>(q + nh * Sq * D, qs, Sq, qd);
-        stage_rows_async<D, 64, 512>(dout + nh * Sq * D, qs, Sq, qd + QB);
+        stage_rows<D, 64, 512>(rq, qs, qd);
+        stage_rows<D, 64, 512>(rdo, qs, qd + QB);
         // bias^T rows k0 .. k0+KB-1, eight 16-byte pieces of 8 queries each, piece p of row r
-        // at position p ^ (r & 7).
+        // at position p ^ (r & 7). Keys past Sk read zeros; SqP is a multiple of 64, so a tile
+        // never runs past its row.
 #pragma unroll
-        for (int base = wave * 64; base < KB * 8; base += 512) {
-            const int slot = base + lane;
+        for (int b = wave * 64; b < KB * 8; b += 512) {
+            const int slot = b + lane;
             const int row = slot >> 3, piece = (slot & 7) ^ (row & 7);
-            const int key = k0 + row, qq = qs + 8 * piece;
-            const void* src = kZero16;
-            if (key < Sk && qq < SqP) src = bias_t + ((size_t)h * Sk + key) * SqP + qq;
-            __builtin_amdgcn_global_load_lds(
-                src, (__attribute__((address_space(3))) void*)(bt + base * 16), 16, 0, 0);
+            buf_dma16(rbt, (row * SqP + 8 * piece) * 2, qs * 2, bt + b * 16);
         }
-        if (wave == 0) {
-            const int qq = qs + lane;
-            const void* a = kZero16;
-            const void* b = kZero16;
-            if (qq < Sq) {
-                a = lse2 + nh * Sq + qq;
-                b = ndi + nh * Sq + qq;
-            }
-            __builtin_amdgcn_global_load_lds(a, (__attribute__((address_space(3))) void*)st, 4,
-                                             0, 0);
-            __builtin_amdgcn_global_load_lds(
-                b, (__attribute__((address_space(3))) void*)(st + 64), 4, 0, 0);
+        if (wave == 0) {  // queries past Sq read zeros
+            buf_dma4(rl, lane * 4, qs * 4, reinterpret_cast<char*>(st));
+            buf_dma4(rn, lane * 4, qs * 4, reinterpret_cast<char*>(st + 64));
         }
     };
 
@@ -1022,7 +1020,7 @@ BwdPlan plan_bwd(int64_t N, int64_t H, int64_t Sq, int64_t Sk, int64_t D) {
         range_keys = 128 * (int64_t)p.KCW;
         const int64_t ksub = (Sk + 127) / 128;
         p.KSUB = (int)(ksub < 1 ? 1 : ksub > 3 ? 3 : ksub);
-        p.SqP = (int)((Sq + 7) / 8 * 8);
+        p.SqP = (int)((Sq + 63) / 64 * 64);
         qtiles = (Sq + 63) / 64;
     } else {
         const int64_t ktiles = (Sk + 63) / 64;

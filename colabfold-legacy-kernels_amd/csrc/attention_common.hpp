@@ -176,7 +176,6 @@ __device__ __forceinline__ float masked_logit_for_row(const uint8_t* mrow, int S
 // swz(r) = (r >> 3) & (PL - 1): the row reads of a 16-key operand (keys 8j + 0..3) and the 4x16
 // transposed reads then touch distinct bank groups.
 // ---------------------------------------------------------------------------------------------
-__device__ __attribute__((aligned(16))) const unsigned int kZero16[4] = {0u, 0u, 0u, 0u};
 
 template <int D>
 struct SwzTile {
@@ -190,24 +189,45 @@ struct SwzTile {
     }
 };
 
-// Issues async loads of rows [g0, g0 + ROWS) of a row-major [S, D] tensor into a swizzled LDS
-// tile (rows past S and padding pieces read zeros). ROWS*PL must be a multiple of 64. Every thread
-// of the block calls it; completion is awaited with async_wait() before a barrier.
-template <int D, int ROWS, int NTHREADS, typename E>
-__device__ __forceinline__ void stage_rows_async(const E* src, int g0, int S, char* lds) {
+// Raw buffer resource over `bytes` bytes at `base` (stride 0). Buffer loads check the whole
+// offset (VGPR offset + SGPR offset) against `bytes` and return zeros past it, so tiles that run
+// off the end of a slice need no per-lane selects, and the per-lane offsets stay the same from
+// tile to tile (only the scalar offset moves).
+using Rsrc = __amdgpu_buffer_rsrc_t;
+__device__ __forceinline__ Rsrc buffer_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+// A per-lane offset that every slice resource treats as out of range (resources cover < 2^30).
+constexpr int kPastEnd = 1 << 30;
+
+// Direct buffer->LDS loads: lane i's 16 (4) bytes at byte voff + soff of the resource land at
+// lds_window + 16*i (4*i); lds_window must be wave-uniform.
+__device__ __forceinline__ void buf_dma16(Rsrc r, int voff, int soff, char* lds_window) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, (__attribute__((address_space(3))) void*)lds_window, 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void buf_dma4(Rsrc r, int voff, int soff, char* lds_window) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, (__attribute__((address_space(3))) void*)lds_window, 4, voff, soff, 0, 0);
+}
+
+// Issues async loads of rows [r0, r0 + ROWS) of a row-major [S, D] 2-byte slice (the resource
+// covers its S rows, so rows past S read zeros, as do the padding pieces of D < 16) into a
+// swizzled LDS tile. ROWS*PL must be a multiple of 64. Every thread of the block calls it;
+// completion is awaited with async_wait() before a barrier.
+template <int D, int ROWS, int NTHREADS>
+__device__ __forceinline__ void stage_rows(Rsrc r, int r0, char* lds) {
     using T = SwzTile<D>;
     constexpr int SLOTS = ROWS * T::PL;
     static_assert(SLOTS % 64 == 0, "tile must be whole wave instructions");
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
-    for (int base = wave * 64; base < SLOTS; base += NTHREADS) {
-        const int slot = base + lane;
+    for (int b = wave * 64; b < SLOTS; b += NTHREADS) {
+        const int slot = b + lane;
         const int row = slot / T::PL;
         const int piece = (slot % T::PL) ^ T::swz(row);
-        const void* g = kZero16;
-        if (g0 + row < S && piece < T::P) g = src + (size_t)(g0 + row) * D + piece * 8;
-        __builtin_amdgcn_global_load_lds(
-            g, (__attribute__((address_space(3))) void*)(lds + base * 16), 16, 0, 0);
+        const int voff = piece < T::P ? (row * D + piece * 8) * 2 : kPastEnd;
+        buf_dma16(r, voff, r0 * D * 2, lds + b * 16);
     }
 }
 

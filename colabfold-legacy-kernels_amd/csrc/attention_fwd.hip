@@ -132,22 +132,23 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
     const int qbase = q0 + wave * 16 * QT;
     const int ntiles = (Sk + BK - 1) / BK;
 
+    const Rsrc rk = buffer_rsrc(kp, (uint32_t)Sk * D * 2);
+    const Rsrc rv = buffer_rsrc(vp, (uint32_t)Sk * D * 2);
+    // The block's bias rows (queries q0 .. q0+BQ-1 that exist).
+    const Rsrc rb = buffer_rsrc(bp + (size_t)q0 * Sk, (uint32_t)(min(BQ, Sq - q0) * Sk * 2));
     auto stage = [&](int k0, char* kv) {
-        stage_rows_async<D, BK, 256>(kp, k0, Sk, kv);
-        stage_rows_async<D, BK, 256>(vp, k0, Sk, kv + TILE);
+        stage_rows<D, BK, 256>(rk, k0, kv);
+        stage_rows<D, BK, 256>(rv, k0, kv + TILE);
         if constexpr (VEC) {
             // Bias rows q0 .. q0+BQ-1, keys k0 .. k0+63 as eight 16-byte pieces per row; piece
             // p of row r sits at position p ^ (r & 7), so a 16-row operand read is conflict-free.
+            // Rows past Sq read zeros; keys past Sk (last tile) read whatever follows, and are
+            // forced to -inf.
 #pragma unroll
-            for (int base = wave * 64; base < BQ * 8; base += 256) {
-                const int slot = base + lane;
+            for (int b = wave * 64; b < BQ * 8; b += 256) {
+                const int slot = b + lane;
                 const int row = slot >> 3, piece = (slot & 7) ^ (row & 7);
-                const int qq = q0 + row, kk = k0 + 8 * piece;
-                const void* src = kZero16;
-                if (qq < Sq && kk < Sk) src = bp + (size_t)qq * Sk + kk;
-                __builtin_amdgcn_global_load_lds(
-                    src, (__attribute__((address_space(3))) void*)(kv + 2 * TILE + base * 16), 16,
-                    0, 0);
+                buf_dma16(rb, (row * Sk + 8 * piece) * 2, k0 * 2, kv + 2 * TILE + b * 16);
             }
         }
     };
