@@ -759,14 +759,14 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
     }
 }
 
-// Column owner. A block of 8 waves owns (128*KSUB keys, head h, row n); wave w owns keys
+// Column owner. A block of NW waves owns (16*KSUB*NW keys, head h, row n); wave w owns keys
 // k0 + 16*KSUB*w + 0..16*KSUB-1 with K and V held as MFMA B operands. The queries stream in
 // 64-row tiles: Q, dO, the transposed bias tile and lse*log2(e), -D_i arrive by direct
 // global->LDS loads into the other buffer while the current tile is computed (one barrier per
 // tile). Per 32-query chunk: S = Q.K^T and dP - D = dO.V^T with the queries permuted so that P
 // and dS are directly the B operands of dV^T += dO^T.P and dK^T += Q^T.dS.
-template <typename TR, int D, int KSUB, bool VEC>
-__global__ __launch_bounds__(512) void attn_bwd_dkv2(
+template <typename TR, int D, int KSUB, int NW, bool VEC>
+__global__ __launch_bounds__(64 * NW) void attn_bwd_dkv2(
     const typename TR::elem* __restrict__ q, const typename TR::elem* __restrict__ k,
     const typename TR::elem* __restrict__ v, const typename TR::elem* __restrict__ bias_t,
     const uint8_t* __restrict__ kmask, const typename TR::elem* __restrict__ dout,
@@ -778,7 +778,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv2(
     using T = SwzTile<D>;
     static_assert(D <= 32, "column-owner kernel holds one 32-dim k-slot group");
     constexpr int DT = AttnGeom<D>::DT;
-    constexpr int KW = 16 * KSUB, KB = 8 * KW;
+    constexpr int KW = 16 * KSUB, KB = NW * KW, NT = 64 * NW;
     constexpr int QB = 64 * T::ROWB;
     constexpr int BTB = KB * 128;  // bias^T tile: KB key rows of 64 queries
 
@@ -835,13 +835,13 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv2(
     const Rsrc rl = buffer_rsrc(lse2 + nh * Sq, (uint32_t)Sq * 4);
     const Rsrc rn = buffer_rsrc(ndi + nh * Sq, (uint32_t)Sq * 4);
     auto stage = [&](int qs, char* qd, char* bt, float* st) {
-        stage_rows<D, 64, 512>(rq, qs, qd);
-        stage_rows<D, 64, 512>(rdo, qs, qd + QB);
+        stage_rows<D, 64, NT>(rq, qs, qd);
+        stage_rows<D, 64, NT>(rdo, qs, qd + QB);
         // bias^T rows k0 .. k0+KB-1, eight 16-byte pieces of 8 queries each, piece p of row r
         // at position p ^ (r & 7). Keys past Sk read zeros; SqP is a multiple of 64, so a tile
         // never runs past its row.
 #pragma unroll
-        for (int b = wave * 64; b < KB * 8; b += 512) {
+        for (int b = wave * 64; b < KB * 8; b += NT) {
             const int slot = b + lane;
             const int row = slot >> 3, piece = (slot & 7) ^ (row & 7);
             buf_dma16(rbt, (row * SqP + 8 * piece) * 2, qs * 2, bt + b * 16);
@@ -1001,7 +1001,7 @@ constexpr int kTargetBlocks = 256;  // one 8-wave row-owner block per CU of an M
 
 struct BwdPlan {
     bool v2 = false;
-    int KT = 0, KCW = 0, KSUB = 0, nranges = 0, NB = 0, nchunks = 0, SqP = 0;
+    int KT = 0, KCW = 0, KSUB = 0, KNW = 0, nranges = 0, NB = 0, nchunks = 0, SqP = 0;
     size_t off_di = 0, off_bt = 0, off_rowl = 0, off_lse2 = 0, off_ndi = 0, off_dbias = 0,
            off_dq = 0, bytes = 0;
 };
@@ -1018,8 +1018,19 @@ BwdPlan plan_bwd(int64_t N, int64_t H, int64_t Sq, int64_t Sk, int64_t D) {
         const int64_t kcw = (chunks32 + 3) / 4;
         p.KCW = (int)(kcw < 1 ? 1 : kcw > 3 ? 3 : kcw);
         range_keys = 128 * (int64_t)p.KCW;
-        const int64_t ksub = (Sk + 127) / 128;
-        p.KSUB = (int)(ksub < 1 ? 1 : ksub > 3 ? 3 : ksub);
+        // dK/dV blocks: 16*KSUB keys per wave, KNW waves (128, 256 or 384 keys per block).
+        // 32 keys x 12 waves fits 168 VGPRs, i.e. three waves per SIMD; measured faster at
+        // Sk = 384 than 48 keys x 8 waves (two waves per SIMD).
+        if (Sk <= 128) {
+            p.KSUB = 1;
+            p.KNW = 8;
+        } else if (Sk <= 256) {
+            p.KSUB = 2;
+            p.KNW = 8;
+        } else {
+            p.KSUB = 2;
+            p.KNW = 12;
+        }
         p.SqP = (int)((Sq + 63) / 64 * 64);
         qtiles = (Sq + 63) / 64;
     } else {
@@ -1150,15 +1161,15 @@ void launch_dq2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, 
         p.nranges, scale);
 }
 
-template <typename TR, int D, int KSUB, bool VEC>
+template <typename TR, int D, int KSUB, int NW, bool VEC>
 void launch_dkv2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, const void* v,
                  const void* bias_t, const uint8_t* kmask, const void* dout, const float* lse2,
                  const float* ndi, const float* rowl, void* dk, void* dv, int N, int H, int Sq,
                  int Sk, float scale) {
     using E = typename TR::elem;
-    const dim3 grid(ceil_div(Sk, 128 * KSUB), H, N);
+    const dim3 grid(ceil_div(Sk, 16 * KSUB * NW), H, N);
     KernelTimer timer("attn_bwd_dkv", st);
-    attn_bwd_dkv2<TR, D, KSUB, VEC><<<grid, 512, 0, st>>>(
+    attn_bwd_dkv2<TR, D, KSUB, NW, VEC><<<grid, 64 * NW, 0, st>>>(
         (const E*)q, (const E*)k, (const E*)v, (const E*)bias_t, kmask, (const E*)dout, lse2,
         ndi, rowl, (E*)dk, (E*)dv, H, Sq, Sk, p.SqP, scale);
 }
@@ -1192,13 +1203,13 @@ void run_bwd_v2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, 
         CLK_KCW(1) CLK_KCW(2) CLK_KCW(3)
 #undef CLK_KCW
     }
-    switch (p.KSUB) {
-#define CLK_KSUB(V)                                                                              \
-    case V:                                                                                      \
-        launch_dkv2<TR, D, V, VEC>(st, p, q, k, v, bias_t, kmask, dout, lse2, ndi, rowl, dk, dv, \
-                                   N, H, Sq, Sk, scale);                                         \
+    switch (p.KSUB * 100 + p.KNW) {
+#define CLK_KSUB(V, W)                                                                           \
+    case V * 100 + W:                                                                            \
+        launch_dkv2<TR, D, V, W, VEC>(st, p, q, k, v, bias_t, kmask, dout, lse2, ndi, rowl, dk,  \
+                                      dv, N, H, Sq, Sk, scale);                                  \
         break;
-        CLK_KSUB(1) CLK_KSUB(2) CLK_KSUB(3)
+        CLK_KSUB(1, 8) CLK_KSUB(2, 8) CLK_KSUB(2, 12)
 #undef CLK_KSUB
     }
     finish_partials<TR>(st, p, dbias_part, dq_part, dbias, dq, (size_t)H * Sq * Sk,
