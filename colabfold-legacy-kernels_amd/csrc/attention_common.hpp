@@ -108,15 +108,6 @@ __device__ __forceinline__ void zero_v_padding(E* lds) {
     }
 }
 
-// Eight elements of a 16-byte vector as float.
-template <typename TR>
-__device__ __forceinline__ void unpack8(u32x4 raw, float* out) {
-    typename TR::elem e[8];
-    __builtin_memcpy(e, &raw, 16);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) out[j] = TR::to_f(e[j]);
-}
-
 // Eight bias values bias_row[kk .. kk+7] as float (zero past Sk).
 template <typename TR>
 __device__ __forceinline__ void load_bias8(const typename TR::elem* row, int kk, int Sk,
@@ -189,28 +180,6 @@ struct SwzTile {
     }
 };
 
-// Raw buffer resource over `bytes` bytes at `base` (stride 0). Buffer loads check the whole
-// offset (VGPR offset + SGPR offset) against `bytes` and return zeros past it, so tiles that run
-// off the end of a slice need no per-lane selects, and the per-lane offsets stay the same from
-// tile to tile (only the scalar offset moves).
-using Rsrc = __amdgpu_buffer_rsrc_t;
-__device__ __forceinline__ Rsrc buffer_rsrc(const void* base, uint32_t bytes) {
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
-}
-// A per-lane offset that every slice resource treats as out of range (resources cover < 2^30).
-constexpr int kPastEnd = 1 << 30;
-
-// Direct buffer->LDS loads: lane i's 16 (4) bytes at byte voff + soff of the resource land at
-// lds_window + 16*i (4*i); lds_window must be wave-uniform.
-__device__ __forceinline__ void buf_dma16(Rsrc r, int voff, int soff, char* lds_window) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        r, (__attribute__((address_space(3))) void*)lds_window, 16, voff, soff, 0, 0);
-}
-__device__ __forceinline__ void buf_dma4(Rsrc r, int voff, int soff, char* lds_window) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(
-        r, (__attribute__((address_space(3))) void*)lds_window, 4, voff, soff, 0, 0);
-}
-
 // Issues async loads of rows [r0, r0 + ROWS) of a row-major [S, D] 2-byte slice (the resource
 // covers its S rows, so rows past S read zeros, as do the padding pieces of D < 16) into a
 // swizzled LDS tile. ROWS*PL must be a multiple of 64. Every thread of the block calls it;
@@ -231,8 +200,6 @@ __device__ __forceinline__ void stage_rows(Rsrc r, int r0, char* lds) {
     }
 }
 
-// Waits for this thread's outstanding global loads (including async LDS fills).
-__device__ __forceinline__ void async_wait() { __builtin_amdgcn_s_waitcnt(0); }
 
 // Row operand from a swizzled tile: row `row`, head dims 32*ks + 8*g + 0..7 (zero beyond D).
 template <typename V8, int D>

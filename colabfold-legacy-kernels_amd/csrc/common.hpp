@@ -99,6 +99,40 @@ __device__ __forceinline__ V lds_tr8(const void* p_lo, const void* p_hi) {
     return __builtin_bit_cast(V, r);
 }
 
+// Eight 2-byte elements (one 16-byte load) as floats.
+template <typename TR>
+__device__ __forceinline__ void unpack8(u32x4 raw, float* out) {
+    typename TR::elem e[8];
+    __builtin_memcpy(e, &raw, 16);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) out[j] = TR::to_f(e[j]);
+}
+
+// Raw buffer resource over `bytes` bytes at `base` (stride 0). Buffer loads check the whole
+// offset (VGPR offset + SGPR offset) against `bytes` and return zeros past it, so tiles that run
+// off the end of a slice need no per-lane selects, and the per-lane offsets stay the same from
+// tile to tile (only the scalar offset moves).
+using Rsrc = __amdgpu_buffer_rsrc_t;
+__device__ __forceinline__ Rsrc buffer_rsrc(const void* base, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+// A per-lane offset that every slice resource treats as out of range (resources cover < 2^30).
+constexpr int kPastEnd = 1 << 30;
+
+// Direct buffer->LDS loads: lane i's 16 (4) bytes at byte voff + soff of the resource land at
+// lds_window + 16*i (4*i); lds_window must be wave-uniform.
+__device__ __forceinline__ void buf_dma16(Rsrc r, int voff, int soff, char* lds_window) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, (__attribute__((address_space(3))) void*)lds_window, 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void buf_dma4(Rsrc r, int voff, int soff, char* lds_window) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, (__attribute__((address_space(3))) void*)lds_window, 4, voff, soff, 0, 0);
+}
+
+// Waits for this thread's outstanding global loads (including async LDS fills).
+__device__ __forceinline__ void async_wait() { __builtin_amdgcn_s_waitcnt(0); }
+
 // Cross-lane reductions among the four lanes l, l^16, l^32, l^48 (same column of a C tile).
 // v_permlane32_swap / v_permlane16_swap with both operands = v return, in each lane, v of that
 // lane and of the lane 32 (16) apart, as a pair: two VALU ops per step, no LDS round trip.

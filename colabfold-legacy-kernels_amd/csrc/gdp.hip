@@ -155,13 +155,19 @@ __global__ __launch_bounds__(256) void gdp_kernel(const typename TR::elem* __res
 }
 
 // ---------------------------------------------------------------------------------------------
-// LayerNorm + both gated branches. The LN affine is folded into the weights while they are
-// staged: (xhat*gamma + beta).W + b = xhat.(diag(gamma) W) + (beta.W + b). A block keeps all four
-// folded weights [C][N] in LDS and walks row tiles of 8 waves x 32 rows; each wave normalises
-// its rows in registers (the row of C values is spread over the four lanes l, l^16, l^32, l^48)
-// and feeds them as the B operand.
+// LayerNorm + both gated branches (the two inputs of the triangle multiplication). Wave w of the
+// N/16 waves owns the 32 output columns 32*cb + 0..31 (cb = w % (N/32)) of branch w / (N/32) and
+// holds the matching columns of that branch's projection and gate weights as MFMA A operands in
+// registers for the whole kernel, with the LN affine folded in:
+//   (xhat*gamma + beta).W + b = xhat.(diag(gamma) W) + (beta.W + b),
+// the folded biases being the accumulators' starting values. The block walks 64-row tiles of z:
+// the rows arrive by direct buffer->LDS loads one tile ahead, one LayerNorm pass writes xhat (in
+// the input type) into a swizzled LDS tile, and every wave reads it as the B operand of
+// out^T = W^T . xhat^T. A-tile row r of column half h stands for output column
+// 32cb + 8*(r/4) + 4h + r%4, so a lane's accumulators hold 8 consecutive output columns of one
+// row and the epilogue (bias, sigmoid gate, row mask) ends in one 16-byte store per lane and
+// 16-row sub-tile. HBM traffic is one read of z and the mask and one write of a and b.
 // ---------------------------------------------------------------------------------------------
-constexpr int kLnGdpThreads = 512;
 
 // Weights and biases of the two branches, passed by value: w = {wpa, wga, wpb, wgb}, same for b.
 template <typename E>
@@ -170,133 +176,172 @@ struct LnGdpWeights {
     const E* b[4];
 };
 
+constexpr int kLnGdpRows = 64;  // rows per tile
+
+template <int PL>
+struct LnGdpGeom {
+    // XOR swizzle of 16-byte pieces within a row: the largest power-of-two group that divides PL.
+    static constexpr int SWZ = (PL % 16 == 0) ? 15 : (PL % 8 == 0) ? 7 : 3;
+    // LayerNorm lanes per row: PL rounded up to a power of two (C = 96 leaves 4 lanes idle).
+    static constexpr int LPR = PL <= 4 ? 4 : PL <= 8 ? 8 : 16;
+};
+
 template <typename TR, int C, int N>
-__global__ __launch_bounds__(kLnGdpThreads) void ln_gdp_kernel(
+__global__ __launch_bounds__(4 * N) void ln_gdp_kernel(
     const typename TR::elem* __restrict__ z, const float* __restrict__ gamma,
     const float* __restrict__ beta, LnGdpWeights<typename TR::elem> wb,
     const typename TR::elem* __restrict__ mask, typename TR::elem* __restrict__ outa,
     typename TR::elem* __restrict__ outb, int M, float eps) {
     using E = typename TR::elem;
     using V8 = typename TR::vec8;
-    constexpr int LD = N + 8;
+    constexpr int NW = N / 16, NT = 64 * NW;
     constexpr int KS = C / 32;
-    constexpr int NC = N / 32;  // 32-column chunks
-    constexpr int RT = 2;
-    extern __shared__ __attribute__((aligned(16))) char smem[];
-    E* w_lds = reinterpret_cast<E*>(smem);                  // [4][C][LD]: pa, ga, pb, gb
-    float* b_lds = reinterpret_cast<float*>(w_lds + 4 * C * LD);  // [4][N]
+    constexpr int R = kLnGdpRows, SUB = R / 16;
+    constexpr int PL = C / 8;
+    using GM = LnGdpGeom<PL>;
+    constexpr int LPR = GM::LPR, RPP = NT / LPR, PASSES = (R + RPP - 1) / RPP;
+    constexpr int ZB = R * C * 2;
 
-    const int tid = threadIdx.x;
-    const int lane = tid & 63, wave = tid >> 6;
+    __shared__ __attribute__((aligned(16))) char z0[ZB];
+    __shared__ __attribute__((aligned(16))) char z1[ZB];
+    __shared__ __attribute__((aligned(16))) char xh[ZB];
+    __shared__ float mk[R];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int r16 = lane & 15, g = lane >> 4;
-    constexpr int NW = kLnGdpThreads / 64;
+    const int br = wave / (N / 32), cb = wave % (N / 32);
+    E* const out = br == 0 ? outa : outb;
 
-    // Fold and stage: W'[k][n] = gamma[k] * W[k][n]; b'[n] = b[n] + sum_k beta[k] * W[k][n].
-    for (int i = tid; i < 4 * C * N; i += kLnGdpThreads) {
-        const int w = i / (C * N), r = i % (C * N), k = r / N, n = r % N;
-        const float v = TR::to_f(wb.w[w][(size_t)k * N + n]);
-        w_lds[(w * C + k) * LD + n] = TR::from_f(gamma[k] * v);
-    }
-    for (int i = tid; i < 4 * N; i += kLnGdpThreads) {
-        const int w = i / N, n = i % N;
-        float s = TR::to_f(wb.b[w][n]);
-        for (int k = 0; k < C; ++k) s += beta[k] * TR::to_f(wb.w[w][(size_t)k * N + n]);
-        b_lds[w * N + n] = s;
-    }
-    __syncthreads();
-
-    const int rows_per_iter = NW * 16 * RT;
-    for (int r0 = blockIdx.x * rows_per_iter; r0 < M; r0 += gridDim.x * rows_per_iter) {
-        const int rbase = r0 + wave * 16 * RT;
-        V8 xf[RT][KS];
-        float mv[RT];
+    // Resident A operands W'^T and the folded biases.
+    V8 wa[2][2][KS];
+    f32x4 binit[2][2];
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-            const int row = rbase + 16 * rt + r16;
-            const bool in = row < M;
-            float v[KS][8];
-            float sum = 0.f;
+    for (int mat = 0; mat < 2; ++mat) {
+        const E* W = wb.w[2 * br + mat];
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                u32x4 raw = {0u, 0u, 0u, 0u};
-                if (in) raw = ld16(z + (size_t)row * C + ks * 32 + 8 * g);
-                E e[8];
-                __builtin_memcpy(e, &raw, 16);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    v[ks][j] = TR::to_f(e[j]);
-                    sum += v[ks][j];
-                }
-            }
-            const float mean = xgroup_sum(sum) * (1.f / C);
-            float m2 = 0.f;
+        for (int h = 0; h < 2; ++h) {
+            const int col = 32 * cb + 8 * (r16 >> 2) + 4 * h + (r16 & 3);
+            float part = 0.f;
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const float d = v[ks][j] - mean;
-                    m2 += d * d;
+                    const int k = 32 * ks + 8 * g + j;
+                    const float v = TR::to_f(W[(size_t)k * N + col]);
+                    wa[mat][h][ks][j] = TR::from_f(gamma[k] * v);
+                    part = fmaf(beta[k], v, part);
                 }
-            const float rstd = rsqrtf(xgroup_sum(m2) * (1.f / C) + eps);
+            // The four lane groups hold disjoint k-slots of the same column.
+            const float bcol = xgroup_sum(part) + TR::to_f(wb.b[2 * br + mat][col]);
+            // C lane (r16, g) needs the columns 32cb + 8g + 4h + i, held by lanes r16' = 4g + i.
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) {
-                E e[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) e[j] = TR::from_f((v[ks][j] - mean) * rstd);
-                u32x4 raw;
-                __builtin_memcpy(&raw, e, 16);
-                xf[rt][ks] = bits_as<V8>(raw);
-            }
-            mv[rt] = in ? TR::to_f(mask[row]) : 0.f;
+            for (int i = 0; i < 4; ++i) binit[mat][h][i] = __shfl(bcol, 4 * g + i);
         }
+    }
+
+    const int ntiles = (M + R - 1) / R;
+    auto stage = [&](int t, char* zb) {
+        const int rows = min(R, M - t * R);
+        const Rsrc rz = buffer_rsrc(z + (size_t)t * R * C, (uint32_t)rows * C * 2);
+#pragma unroll
+        for (int b = wave * 64; b < R * PL; b += NT) buf_dma16(rz, (b + lane) * 16, 0, zb + b * 16);
+    };
+    const int lr = tid % LPR;
+    auto load_mask = [&](int t, float (&mv)[PASSES]) {
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int row = t * R + p * RPP + tid / LPR;
+            mv[p] = row < M ? TR::to_f(mask[row]) : 0.f;
+        }
+    };
+
+    auto tile = [&](int t, const char* zc, char* zn, const float (&mc)[PASSES],
+                    float (&mn)[PASSES]) {
+        async_wait();
+        __syncthreads();  // z tile t in zc; every wave is done with xh and mk of the last tile
+        const int tn = t + gridDim.x;
+        if (tn < ntiles) {
+            stage(tn, zn);
+            load_mask(tn, mn);
+        }
+        // LayerNorm: LPR lanes per row, 8 channels each; xhat into the swizzled tile.
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int row = p * RPP + tid / LPR;
+            if (row >= R) break;  // whole LPR groups: the shuffles stay within active lanes
+            float v[8];
+            float sum = 0.f;
+            if (lr < PL) {
+                unpack8<TR>(*reinterpret_cast<const u32x4*>(zc + row * C * 2 + lr * 16), v);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) sum += v[j];
+            }
+#pragma unroll
+            for (int off = 1; off < LPR; off <<= 1) sum += __shfl_xor(sum, off);
+            const float mean = sum * (1.f / C);
+            float m2 = 0.f;
+            if (lr < PL) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float d = v[j] - mean;
+                    m2 = fmaf(d, d, m2);
+                }
+            }
+#pragma unroll
+            for (int off = 1; off < LPR; off <<= 1) m2 += __shfl_xor(m2, off);
+            const float rstd = rsqrtf(m2 * (1.f / C) + eps);
+            if (lr < PL) {
+                float x[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) x[j] = (v[j] - mean) * rstd;
+                *reinterpret_cast<u32x4*>(xh + row * PL * 16 + 16 * (lr ^ (row & GM::SWZ))) =
+                    pack8<TR>(x);
+            }
+            if (lr == 0) mk[row] = mc[p];
+        }
+        __syncthreads();  // xhat and the row mask of tile t ready
 
 #pragma unroll
-        for (int br = 0; br < 2; ++br) {
-            const E* wpl = w_lds + (2 * br) * C * LD;
-            const E* wgl = w_lds + (2 * br + 1) * C * LD;
-            const float* bpl = b_lds + (2 * br) * N;
-            const float* bgl = b_lds + (2 * br + 1) * N;
-            E* out = br == 0 ? outa : outb;
+        for (int sub = 0; sub < SUB; ++sub) {
+            const int xrow = 16 * sub + r16;
+            f32x4 acc[2][2];
 #pragma unroll
-            for (int c = 0; c < NC; ++c) {
-                f32x4 ap[RT][2], ag[RT][2];
+            for (int mat = 0; mat < 2; ++mat)
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    // Bias of columns 32c + 8g + 4h + 0..3 as the accumulator's starting value.
-                    const f32x4 pb = *reinterpret_cast<const f32x4*>(bpl + 32 * c + 8 * g + 4 * h);
-                    const f32x4 gb = *reinterpret_cast<const f32x4*>(bgl + 32 * c + 8 * g + 4 * h);
+                for (int h = 0; h < 2; ++h) acc[mat][h] = binit[mat][h];
 #pragma unroll
-                    for (int rt = 0; rt < RT; ++rt) {
-                        ap[rt][h] = pb;
-                        ag[rt][h] = gb;
-                    }
+            for (int ks = 0; ks < KS; ++ks) {
+                const V8 xb = *reinterpret_cast<const V8*>(
+                    xh + xrow * PL * 16 + 16 * ((4 * ks + g) ^ (xrow & GM::SWZ)));
+#pragma unroll
+                for (int mat = 0; mat < 2; ++mat)
+#pragma unroll
+                    for (int h = 0; h < 2; ++h)
+                        acc[mat][h] = TR::mfma(wa[mat][h][ks], xb, acc[mat][h]);
+            }
+            const int row = t * R + xrow;
+            if (row < M) {
+                const float m = mk[xrow];
+                float o[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int h = j >> 2, i = j & 3;
+                    o[j] = m * acc[0][h][i] * sigmoid(acc[1][h][i]);
                 }
-#pragma unroll
-                for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-                    for (int h = 0; h < 2; ++h) {
-                        const V8 pa = w_operand<V8>(wpl, LD, ks * 32, c, h, r16, g);
-                        const V8 ga = w_operand<V8>(wgl, LD, ks * 32, c, h, r16, g);
-#pragma unroll
-                        for (int rt = 0; rt < RT; ++rt) {
-                            ap[rt][h] = TR::mfma(pa, xf[rt][ks], ap[rt][h]);
-                            ag[rt][h] = TR::mfma(ga, xf[rt][ks], ag[rt][h]);
-                        }
-                    }
-#pragma unroll
-                for (int rt = 0; rt < RT; ++rt) {
-                    const int row = rbase + 16 * rt + r16;
-                    if (row >= M) continue;
-                    float o[8];
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const int h = j >> 2, i = j & 3;
-                        o[j] = mv[rt] * ap[rt][h][i] * sigmoid(ag[rt][h][i]);
-                    }
-                    st16(out + (size_t)row * N + 32 * c + 8 * g, pack8<TR>(o));
-                }
+                st16(out + (size_t)row * N + 32 * cb + 8 * g, pack8<TR>(o));
             }
         }
+    };
+
+    float ma[PASSES], mb[PASSES];
+    int t = blockIdx.x;
+    if (t < ntiles) {
+        stage(t, z0);
+        load_mask(t, ma);
+    }
+    for (; t < ntiles; t += 2 * gridDim.x) {
+        tile(t, z0, z1, ma, mb);
+        if (t + (int)gridDim.x < ntiles) tile(t + gridDim.x, z1, z0, mb, ma);
     }
 }
 
@@ -349,14 +394,14 @@ clk_status launch_ln_gdp(hipStream_t st, const void* z, const float* gamma, cons
                          const LnGdpWeights<typename TR::elem>& wb, const void* mask, void* a,
                          void* b, int M, float eps) {
     using E = typename TR::elem;
-    const size_t lds = (size_t)4 * C * (N + 8) * sizeof(E) + 4 * N * sizeof(float);
-    static_assert((size_t)4 * C * (N + 8) * 2 + 4 * N * 4 <= kMaxLds, "weights exceed LDS");
-    allow_lds(ln_gdp_kernel<TR, C, N>, kMaxLds);
-    const int grid = row_blocks(M, kLnGdpThreads / 64 * 32, 256);
+    // One 8-wave block per CU at N = 128 (registers allow two waves per SIMD); narrower N runs
+    // more, smaller blocks per CU.
+    const int ntiles = (M + kLnGdpRows - 1) / kLnGdpRows;
+    const int per_cu = 128 / N;
+    const int grid = ntiles < 256 * per_cu ? ntiles : 256 * per_cu;
     KernelTimer timer("ln_gdp", st);
-    ln_gdp_kernel<TR, C, N><<<grid, kLnGdpThreads, lds, st>>>((const E*)z, gamma, beta, wb,
-                                                              (const E*)mask, (E*)a, (E*)b, M,
-                                                              eps);
+    ln_gdp_kernel<TR, C, N><<<grid, 4 * N, 0, st>>>((const E*)z, gamma, beta, wb,
+                                                     (const E*)mask, (E*)a, (E*)b, M, eps);
     return check_launch("ln_gated_dual_proj");
 }
 
