@@ -528,7 +528,8 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
     __shared__ __attribute__((aligned(16))) char kv1[2 * KVB];
     __shared__ __attribute__((aligned(16))) char qd0[3 * QB];
     __shared__ __attribute__((aligned(16))) char qd1[3 * QB];
-    __shared__ __attribute__((aligned(16))) f32x4 xch[8 * 2 * DT * 64];
+    __shared__ __attribute__((aligned(16))) char xch_raw[8 * 2 * DT * 64 * 16];
+    f32x4* const xch = reinterpret_cast<f32x4*>(xch_raw);
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r16 = lane & 15, g = lane >> 4;
@@ -596,6 +597,26 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
         ml_nx = kmask ? row_logit[n] : kMaskedLogit;
     };
 
+    // dQ of the last row (this wave's slice), stored at the start of the next step.
+    f32x4 pend_dq = {0.f, 0.f, 0.f, 0.f};
+    int pend_n = -1;
+    auto flush_dq = [&]() {
+        if (pend_n < 0) return;
+        const int qt = kq / DT, dt = kq % DT;
+        const int d = 16 * dt + 4 * g;
+        if (qrow[qt] < Sq && d < D) {
+            const size_t pnh = (size_t)pend_n * H + h;
+            if (nranges == 1) {
+                store4<TR>(dq + (pnh * Sq + qrow[qt]) * D + d, pend_dq);
+            } else {
+                float* o = dq_part + (((size_t)range * N + pend_n) * H + h) * Sq * D +
+                           (size_t)qrow[qt] * D + d;
+                *reinterpret_cast<f32x4*>(o) = pend_dq;
+            }
+        }
+        pend_n = -1;
+    };
+
     auto step = [&](int n, const char* kvc, const char* qdc, char* kvn, char* qdn) {
         const size_t nh = (size_t)n * H + h;
         async_wait();
@@ -613,10 +634,6 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
         u32x2 maskc[KCW];
 #pragma unroll
         for (int i = 0; i < KCW; ++i) maskc[i] = mask_nx[i];
-        if (n + 1 < n1) {
-            stage(n + 1, kvn, qdn);
-            prefetch(n + 1);
-        }
 
         V8 qf[2], dof[2];
         float di[2];
@@ -638,6 +655,13 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
                     lse2_out[nh * Sq + qrow[qt]] = lse2c[qt];
                     ndi_out[nh * Sq + qrow[qt]] = -di[qt];
                 }
+        }
+        // The stores of this row and the last go out before row n+1's loads are issued, so the
+        // next barrier's wait for those loads finds them long written.
+        flush_dq();
+        if (n + 1 < n1) {
+            stage(n + 1, kvn, qdn);
+            prefetch(n + 1);
         }
 
         f32x4 dqa[2][DT];
@@ -710,22 +734,14 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
         for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) xch[((wave * 2 + qt) * DT + dt) * 64 + lane] = dqa[qt][dt];
-        __syncthreads();
+        lds_barrier();  // the exchange is LDS only
         if (kq < 2 * DT) {
             const int qt = kq / DT, dt = kq % DT;
             f32x4 acc = xch[(((qg * 4) * 2 + qt) * DT + dt) * 64 + lane];
 #pragma unroll
             for (int w = 1; w < 4; ++w) acc += xch[(((qg * 4 + w) * 2 + qt) * DT + dt) * 64 + lane];
-            const int d = 16 * dt + 4 * g;
-            if (qrow[qt] < Sq && d < D) {
-                if (nranges == 1) {
-                    store4<TR>(dq + (nh * Sq + qrow[qt]) * D + d, acc * scale);
-                } else {
-                    float* o = dq_part + (((size_t)range * N + n) * H + h) * Sq * D +
-                               (size_t)qrow[qt] * D + d;
-                    *reinterpret_cast<f32x4*>(o) = acc * scale;
-                }
-            }
+            pend_dq = acc * scale;
+            pend_n = n;
         }
     };
 
@@ -737,6 +753,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
         step(n, kv0, qd0, kv1, qd1);
         if (n + 1 < n1) step(n + 1, kv1, qd1, kv0, qd0);
     }
+    flush_dq();
 
 #pragma unroll
     for (int i = 0; i < KCW; ++i) {

@@ -133,6 +133,18 @@ __device__ __forceinline__ void buf_dma4(Rsrc r, int voff, int soff, char* lds_w
 // Waits for this thread's outstanding global loads (including async LDS fills).
 __device__ __forceinline__ void async_wait() { __builtin_amdgcn_s_waitcnt(0); }
 
+// Workgroup barrier that publishes LDS only: waits for this wave's LDS operations, not for its
+// outstanding global loads and stores (the fence of __syncthreads waits for those too, so a
+// barrier right after a batch of stores would stall for their write-back).
+__device__ __forceinline__ void lds_barrier() {
+    // Compiler-only fences keep memory accesses on their side of the barrier; the hardware wait
+    // is for LDS (lgkmcnt) alone: vmcnt and expcnt fields at their maxima in the encoding.
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __builtin_amdgcn_s_barrier();
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // Cross-lane reductions among the four lanes l, l^16, l^32, l^48 (same column of a C tile).
 // v_permlane32_swap / v_permlane16_swap with both operands = v return, in each lane, v of that
 // lane and of the lane 32 (16) apart, as a pair: two VALU ops per step, no LDS round trip.

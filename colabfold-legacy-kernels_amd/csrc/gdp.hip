@@ -247,23 +247,33 @@ __global__ __launch_bounds__(4 * N) void ln_gdp_kernel(
         for (int b = wave * 64; b < R * PL; b += NT) buf_dma16(rz, (b + lane) * 16, 0, zb + b * 16);
     };
     const int lr = tid % LPR;
-    auto load_mask = [&](int t, float (&mv)[PASSES]) {
+    // Raw mask values of the rows this thread normalises, loaded a tile ahead (clamped inside
+    // [0, M); rows past M never reach the output). Converted when used: converting here would
+    // wait for the tile's direct-to-LDS loads as well.
+    auto load_mask = [&](int t, uint32_t (&mv)[PASSES]) {
+        const uint16_t* m16 = reinterpret_cast<const uint16_t*>(mask);
 #pragma unroll
-        for (int p = 0; p < PASSES; ++p) {
-            const int row = t * R + p * RPP + tid / LPR;
-            mv[p] = row < M ? TR::to_f(mask[row]) : 0.f;
+        for (int p = 0; p < PASSES; ++p) mv[p] = m16[min(t * R + p * RPP + tid / LPR, M - 1)];
+    };
+
+    // Outputs of the previous tile, stored after the next barrier and before the next tile's
+    // loads are issued: the barrier's wait for the loads then never waits for fresh stores.
+    u32x4 pend[SUB];
+    int pend_row = -1;
+    auto flush = [&]() {
+        if (pend_row < 0) return;
+#pragma unroll
+        for (int sub = 0; sub < SUB; ++sub) {
+            const int row = pend_row + 16 * sub + r16;
+            if (row < M) st16(out + (size_t)row * N + 32 * cb + 8 * g, pend[sub]);
         }
     };
 
-    auto tile = [&](int t, const char* zc, char* zn, const float (&mc)[PASSES],
-                    float (&mn)[PASSES]) {
+    auto tile = [&](int t, const char* zc, char* zn, const uint32_t (&mc)[PASSES],
+                    uint32_t (&mn)[PASSES]) {
         async_wait();
         __syncthreads();  // z tile t in zc; every wave is done with xh and mk of the last tile
-        const int tn = t + gridDim.x;
-        if (tn < ntiles) {
-            stage(tn, zn);
-            load_mask(tn, mn);
-        }
+        flush();
         // LayerNorm: LPR lanes per row, 8 channels each; xhat into the swizzled tile.
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
@@ -297,9 +307,16 @@ __global__ __launch_bounds__(4 * N) void ln_gdp_kernel(
                 *reinterpret_cast<u32x4*>(xh + row * PL * 16 + 16 * (lr ^ (row & GM::SWZ))) =
                     pack8<TR>(x);
             }
-            if (lr == 0) mk[row] = mc[p];
+            if (lr == 0) mk[row] = TR::to_f(__builtin_bit_cast(E, (uint16_t)mc[p]));
         }
-        __syncthreads();  // xhat and the row mask of tile t ready
+        lds_barrier();  // xhat and the row mask of tile t ready; zn is free (read before it)
+        // The next tile's rows go out after the barrier: an LDS read behind a barrier would
+        // otherwise wait for them.
+        const int tn = t + gridDim.x;
+        if (tn < ntiles) {
+            stage(tn, zn);
+            load_mask(tn, mn);
+        }
 
 #pragma unroll
         for (int sub = 0; sub < SUB; ++sub) {
@@ -319,21 +336,19 @@ __global__ __launch_bounds__(4 * N) void ln_gdp_kernel(
                     for (int h = 0; h < 2; ++h)
                         acc[mat][h] = TR::mfma(wa[mat][h][ks], xb, acc[mat][h]);
             }
-            const int row = t * R + xrow;
-            if (row < M) {
-                const float m = mk[xrow];
-                float o[8];
+            const float m = mk[xrow];
+            float o[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int h = j >> 2, i = j & 3;
-                    o[j] = m * acc[0][h][i] * sigmoid(acc[1][h][i]);
-                }
-                st16(out + (size_t)row * N + 32 * cb + 8 * g, pack8<TR>(o));
+            for (int j = 0; j < 8; ++j) {
+                const int h = j >> 2, i = j & 3;
+                o[j] = m * acc[0][h][i] * sigmoid(acc[1][h][i]);
             }
+            pend[sub] = pack8<TR>(o);
         }
+        pend_row = t * R;
     };
 
-    float ma[PASSES], mb[PASSES];
+    uint32_t ma[PASSES], mb[PASSES];
     int t = blockIdx.x;
     if (t < ntiles) {
         stage(t, z0);
@@ -343,6 +358,7 @@ __global__ __launch_bounds__(4 * N) void ln_gdp_kernel(
         tile(t, z0, z1, ma, mb);
         if (t + (int)gridDim.x < ntiles) tile(t + gridDim.x, z1, z0, mb, ma);
     }
+    flush();
 }
 
 template <typename F>
