@@ -41,8 +41,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dot(const typename TR::elem* __r
 #pragma unroll
         for (int j = 0; j < 8; ++j) s += o[j] * d[j];
     }
-#pragma unroll
-    for (int off = 1; off < LPR; off <<= 1) s += __shfl_xor(s, off);
+    s = group_sum<LPR>(s);
     if (row < rows && part == 0) di[row] = s;
 }
 

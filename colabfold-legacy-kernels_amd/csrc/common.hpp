@@ -171,6 +171,39 @@ __device__ __forceinline__ float xgroup_sum(float v) {
     return __uint_as_float(p[0]) + __uint_as_float(p[1]);
 }
 
+// Lane exchanges for reductions over aligned groups of G lanes (G a power of two, 2..64), as
+// (own value, partner value) pairs. Step s pairs the lanes s apart in the butterfly sense. Steps
+// 1 and 2 are DPP quad permutations (lane ^ 1, lane ^ 2); steps 4 and 8 are row_half_mirror and
+// row_mirror, which pair a lane with one of the other quad (half row) -- equivalent to lane ^ 4
+// (^ 8) once the earlier steps have made every quad (half row) hold identical values; steps 16
+// and 32 are permlane swaps. All are VALU moves, no LDS round trip. A reduction that combines
+// each pair symmetrically (a + b, max, Chan's merge) therefore leaves identical bits in every
+// lane of the group.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+template <int STEP>
+__device__ __forceinline__ u32x2 lane_pair(float v) {
+    static_assert(STEP == 1 || STEP == 2 || STEP == 4 || STEP == 8 || STEP == 16 || STEP == 32,
+                  "butterfly step");
+    if constexpr (STEP == 16) return pair_xor16(v);
+    else if constexpr (STEP == 32) return pair_xor32(v);
+    else {
+        constexpr int ctrl = STEP == 1 ? 0xB1 : STEP == 2 ? 0x4E : STEP == 4 ? 0x141 : 0x140;
+        return u32x2{__float_as_uint(v), __float_as_uint(dpp_move<ctrl>(v))};
+    }
+}
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+    static_assert(G >= 1 && G <= 64 && (G & (G - 1)) == 0, "group of 2^k lanes");
+    if constexpr (G >= 2) {
+        const u32x2 p = lane_pair<G / 2>(group_sum<G / 2>(v));
+        return __uint_as_float(p[0]) + __uint_as_float(p[1]);
+    }
+    return v;
+}
+
 // Work item of workgroup L out of T so that each XCD runs a contiguous range of work items.
 // The dispatcher hands workgroup L to XCD L % 8 (each XCD has its own L2), so with the identity
 // mapping neighbouring work items -- which share inputs -- land on different L2s. A bijection

@@ -278,7 +278,7 @@ __global__ __launch_bounds__(4 * N) void ln_gdp_kernel(
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const int row = p * RPP + tid / LPR;
-            if (row >= R) break;  // whole LPR groups: the shuffles stay within active lanes
+            if (row >= R) break;  // whole LPR groups: the lane exchanges stay within active lanes
             float v[8];
             float sum = 0.f;
             if (lr < PL) {
@@ -286,8 +286,7 @@ __global__ __launch_bounds__(4 * N) void ln_gdp_kernel(
 #pragma unroll
                 for (int j = 0; j < 8; ++j) sum += v[j];
             }
-#pragma unroll
-            for (int off = 1; off < LPR; off <<= 1) sum += __shfl_xor(sum, off);
+            sum = group_sum<LPR>(sum);
             const float mean = sum * (1.f / C);
             float m2 = 0.f;
             if (lr < PL) {
@@ -297,8 +296,7 @@ __global__ __launch_bounds__(4 * N) void ln_gdp_kernel(
                     m2 = fmaf(d, d, m2);
                 }
             }
-#pragma unroll
-            for (int off = 1; off < LPR; off <<= 1) m2 += __shfl_xor(m2, off);
+            m2 = group_sum<LPR>(m2);
             const float rstd = rsqrtf(m2 * (1.f / C) + eps);
             if (lr < PL) {
                 float x[8];

@@ -42,26 +42,24 @@ __device__ __forceinline__ u32x4 pack(const float* in) {
     return raw;
 }
 
-// Chan's merge of (mean, M2) between lanes that own equal element counts; every lane of the row
-// ends with bit-identical values (each step is symmetric in its two operands).
+// Chan's merge of (mean, M2) over the LPR lanes of a row, each lane starting from `count`
+// elements. Every step combines the pair symmetrically (the pair's order only flips the sign of
+// d), so every lane of the row ends with bit-identical values.
 template <int LPR>
 __device__ __forceinline__ void merge_stats(float& mean, float& m2, float count) {
-#pragma unroll
-    for (int off = 1; off < LPR; off <<= 1) {
-        const float om = __shfl_xor(mean, off);
-        const float o2 = __shfl_xor(m2, off);
-        const float d = om - mean;
-        mean = (mean + om) * 0.5f;
-        m2 = (m2 + o2) + d * d * (count * 0.5f);
-        count *= 2.f;
+    if constexpr (LPR >= 2) {
+        merge_stats<LPR / 2>(mean, m2, count);
+        const u32x2 pm = lane_pair<LPR / 2>(mean), p2 = lane_pair<LPR / 2>(m2);
+        const float a = __uint_as_float(pm[0]), b = __uint_as_float(pm[1]);
+        const float d = b - a;
+        mean = (a + b) * 0.5f;
+        m2 = (__uint_as_float(p2[0]) + __uint_as_float(p2[1])) + d * d * (count * (LPR / 4.f));
     }
 }
 
 template <int LPR>
 __device__ __forceinline__ float row_sum(float v) {
-#pragma unroll
-    for (int off = 1; off < LPR; off <<= 1) v += __shfl_xor(v, off);
-    return v;
+    return group_sum<LPR>(v);
 }
 
 template <typename TR, int LPR, int NV>
