@@ -133,6 +133,22 @@ __device__ __forceinline__ void buf_dma4(Rsrc r, int voff, int soff, char* lds_w
 // Waits for this thread's outstanding global loads (including async LDS fills).
 __device__ __forceinline__ void async_wait() { __builtin_amdgcn_s_waitcnt(0); }
 
+// Waits until at most N of this thread's vector memory operations (loads, direct-to-LDS loads
+// and stores, which retire in issue order for this count) are outstanding. Memory accesses stay
+// on their side of the wait.
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+    static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+// 16-byte buffer store; a store whose offset falls past the resource's range is dropped.
+__device__ __forceinline__ void buf_st16(Rsrc r, int voff, int soff, u32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, soff, 0);
+}
+
 // Workgroup barrier that publishes LDS only: waits for this wave's LDS operations, not for its
 // outstanding global loads and stores (the fence of __syncthreads waits for those too, so a
 // barrier right after a batch of stores would stall for their write-back).

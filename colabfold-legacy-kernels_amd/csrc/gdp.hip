@@ -161,7 +161,7 @@ __global__ __launch_bounds__(256) void gdp_kernel(const typename TR::elem* __res
 // registers for the whole kernel, with the LN affine folded in:
 //   (xhat*gamma + beta).W + b = xhat.(diag(gamma) W) + (beta.W + b),
 // the folded biases being the accumulators' starting values. The block walks 64-row tiles of z:
-// the rows arrive by direct buffer->LDS loads one tile ahead, one LayerNorm pass writes xhat (in
+// the rows arrive by direct buffer->LDS loads two tiles ahead, one LayerNorm pass writes xhat (in
 // the input type) into a swizzled LDS tile, and every wave reads it as the B operand of
 // out^T = W^T . xhat^T. A-tile row r of column half h stands for output column
 // 32cb + 8*(r/4) + 4h + r%4, so a lane's accumulators hold 8 consecutive output columns of one
@@ -201,13 +201,21 @@ __global__ __launch_bounds__(4 * N) void ln_gdp_kernel(
     using GM = LnGdpGeom<PL>;
     constexpr int LPR = GM::LPR, RPP = NT / LPR, PASSES = (R + RPP - 1) / RPP;
     constexpr int ZB = R * C * 2;
+    constexpr int DPW = (R * PL + NT - 1) / NT;  // 16-byte loads per lane and tile
+    constexpr int ZBP = DPW * NT * 16;
 
-    __shared__ __attribute__((aligned(16))) char z0[ZB];
-    __shared__ __attribute__((aligned(16))) char z1[ZB];
+    // Three z tiles (the one being normalised and the next two in flight), each padded to whole
+    // rounds of the block's 16-byte loads, and the normalised tile.
+    __shared__ __attribute__((aligned(16))) char z0[ZBP];
+    __shared__ __attribute__((aligned(16))) char z1[ZBP];
+    __shared__ __attribute__((aligned(16))) char z2[ZBP];
     __shared__ __attribute__((aligned(16))) char xh[ZB];
     __shared__ float mk[R];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    // Wave-uniform by construction; readfirstlane lets the compiler keep it (and the output
+    // resources derived from it) in scalar registers.
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r16 = lane & 15, g = lane >> 4;
     const int br = wave / (N / 32), cb = wave % (N / 32);
     E* const out = br == 0 ? outa : outb;
@@ -218,6 +226,10 @@ __global__ __launch_bounds__(4 * N) void ln_gdp_kernel(
 #pragma unroll
     for (int mat = 0; mat < 2; ++mat) {
         const E* W = wb.w[2 * br + mat];
+        // The gate is carried as -log2(e) * (its pre-activation), the argument of exp2 in the
+        // sigmoid: the scale rides on the folded weights and bias instead of one multiply per
+        // output.
+        const float fold = mat == 1 ? -kLog2e : 1.f;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int col = 32 * cb + 8 * (r16 >> 2) + 4 * h + (r16 & 3);
@@ -228,11 +240,11 @@ __global__ __launch_bounds__(4 * N) void ln_gdp_kernel(
                 for (int j = 0; j < 8; ++j) {
                     const int k = 32 * ks + 8 * g + j;
                     const float v = TR::to_f(W[(size_t)k * N + col]);
-                    wa[mat][h][ks][j] = TR::from_f(gamma[k] * v);
+                    wa[mat][h][ks][j] = TR::from_f(gamma[k] * v * fold);
                     part = fmaf(beta[k], v, part);
                 }
             // The four lane groups hold disjoint k-slots of the same column.
-            const float bcol = xgroup_sum(part) + TR::to_f(wb.b[2 * br + mat][col]);
+            const float bcol = (xgroup_sum(part) + TR::to_f(wb.b[2 * br + mat][col])) * fold;
             // C lane (r16, g) needs the columns 32cb + 8g + 4h + i, held by lanes r16' = 4g + i.
 #pragma unroll
             for (int i = 0; i < 4; ++i) binit[mat][h][i] = __shfl(bcol, 4 * g + i);
@@ -240,39 +252,52 @@ __global__ __launch_bounds__(4 * N) void ln_gdp_kernel(
     }
 
     const int ntiles = (M + R - 1) / R;
+    // Every tile issues the same vector memory operations in every wave, whatever its position:
+    // DPW direct-to-LDS loads (pieces past the tile read zeros into the padding of the buffer),
+    // PASSES mask loads (rows clamped into [0, M)) and SUB stores (rows past M fall outside the
+    // store resource and are dropped); tiles past the end load from an empty resource. The wait
+    // for a tile's rows can then count the operations issued after them.
     auto stage = [&](int t, char* zb) {
-        const int rows = min(R, M - t * R);
-        const Rsrc rz = buffer_rsrc(z + (size_t)t * R * C, (uint32_t)rows * C * 2);
+        const int rows = t < ntiles ? min(R, M - t * R) : 0;
+        const Rsrc rz = buffer_rsrc(rows > 0 ? z + (size_t)t * R * C : z, (uint32_t)rows * C * 2);
 #pragma unroll
-        for (int b = wave * 64; b < R * PL; b += NT) buf_dma16(rz, (b + lane) * 16, 0, zb + b * 16);
+        for (int k = 0; k < DPW; ++k) {
+            const int b = wave * 64 + k * NT;
+            buf_dma16(rz, (b + lane) * 16, 0, zb + b * 16);
+        }
     };
     const int lr = tid % LPR;
-    // Raw mask values of the rows this thread normalises, loaded a tile ahead (clamped inside
-    // [0, M); rows past M never reach the output). Converted when used: converting here would
-    // wait for the tile's direct-to-LDS loads as well.
+    // Raw mask values of the rows this thread normalises. Converted when used: converting here
+    // would wait for the tile's direct-to-LDS loads as well.
     auto load_mask = [&](int t, uint32_t (&mv)[PASSES]) {
         const uint16_t* m16 = reinterpret_cast<const uint16_t*>(mask);
 #pragma unroll
-        for (int p = 0; p < PASSES; ++p) mv[p] = m16[min(t * R + p * RPP + tid / LPR, M - 1)];
-    };
-
-    // Outputs of the previous tile, stored after the next barrier and before the next tile's
-    // loads are issued: the barrier's wait for the loads then never waits for fresh stores.
-    u32x4 pend[SUB];
-    int pend_row = -1;
-    auto flush = [&]() {
-        if (pend_row < 0) return;
-#pragma unroll
-        for (int sub = 0; sub < SUB; ++sub) {
-            const int row = pend_row + 16 * sub + r16;
-            if (row < M) st16(out + (size_t)row * N + 32 * cb + 8 * g, pend[sub]);
+        for (int p = 0; p < PASSES; ++p) {
+            const int64_t r = (int64_t)t * R + p * RPP + tid / LPR;
+            mv[p] = m16[r < M ? r : M - 1];
         }
     };
+    auto out_rsrc = [&](int t) {
+        const int rows = t < ntiles ? min(R, M - t * R) : 0;
+        return buffer_rsrc(rows > 0 ? out + (size_t)t * R * N : out, (uint32_t)rows * N * 2);
+    };
 
+    // Outputs of the previous tile, stored after the next barrier: the barrier then never waits
+    // for fresh stores.
+    u32x4 pend[SUB] = {};
+    Rsrc pend_out = out_rsrc(ntiles);  // empty: the first flush stores nothing
+    auto flush = [&]() {
+#pragma unroll
+        for (int sub = 0; sub < SUB; ++sub)
+            buf_st16(pend_out, ((16 * sub + r16) * N + 32 * cb + 8 * g) * 2, 0, pend[sub]);
+    };
+
+    // Tile t is read from zc; tile t + 2*gridDim.x goes into zn, which held tile t - gridDim.x.
+    // Issued after zc's loads: at least the SUB stores and the DPW loads of the tile before.
     auto tile = [&](int t, const char* zc, char* zn, const uint32_t (&mc)[PASSES],
                     uint32_t (&mn)[PASSES]) {
-        async_wait();
-        __syncthreads();  // z tile t in zc; every wave is done with xh and mk of the last tile
+        vm_wait<SUB + DPW>();
+        lds_barrier();  // z tile t in zc; every wave is done with xh and mk of the last tile
         flush();
         // LayerNorm: LPR lanes per row, 8 channels each; xhat into the swizzled tile.
 #pragma unroll
@@ -308,13 +333,13 @@ __global__ __launch_bounds__(4 * N) void ln_gdp_kernel(
             if (lr == 0) mk[row] = TR::to_f(__builtin_bit_cast(E, (uint16_t)mc[p]));
         }
         lds_barrier();  // xhat and the row mask of tile t ready; zn is free (read before it)
-        // The next tile's rows go out after the barrier: an LDS read behind a barrier would
-        // otherwise wait for them.
-        const int tn = t + gridDim.x;
-        if (tn < ntiles) {
-            stage(tn, zn);
-            load_mask(tn, mn);
-        }
+        // Tile loads go out after the barrier (an LDS read behind a barrier would otherwise wait
+        // for them), the mask loads first so that they never sit between a tile's loads and the
+        // wait that counts them.
+        const int tn = t + 2 * gridDim.x;
+        load_mask(tn, mn);
+        stage(tn, zn);
+        pend_out = out_rsrc(t);
 
 #pragma unroll
         for (int sub = 0; sub < SUB; ++sub) {
@@ -339,24 +364,36 @@ __global__ __launch_bounds__(4 * N) void ln_gdp_kernel(
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const int h = j >> 2, i = j & 3;
-                o[j] = m * acc[0][h][i] * sigmoid(acc[1][h][i]);
+                o[j] = m * acc[0][h][i] * fast_rcp(1.f + fast_exp2(acc[1][h][i]));
             }
             pend[sub] = pack8<TR>(o);
         }
-        pend_row = t * R;
     };
 
-    uint32_t ma[PASSES], mb[PASSES];
+    uint32_t ma[PASSES], mb[PASSES], mc[PASSES];
+    const int G = gridDim.x;
     int t = blockIdx.x;
-    if (t < ntiles) {
-        stage(t, z0);
-        load_mask(t, ma);
-    }
-    for (; t < ntiles; t += 2 * gridDim.x) {
-        tile(t, z0, z1, ma, mb);
-        if (t + (int)gridDim.x < ntiles) tile(t + gridDim.x, z1, z0, mb, ma);
+    // Prologue: two tiles in flight, with a store batch (of nothing) between them so that the
+    // first wait counts as every later one does.
+    load_mask(t, ma);
+    stage(t, z0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    flush();
+    load_mask(t + G, mb);
+    stage(t + G, z1);
+    // The first two tiles' mask values are in registers before the loop starts (the compiler may
+    // sink their loads below the tile loads; the loop must not inherit a wait on those).
+#pragma unroll
+    for (int p = 0; p < PASSES; ++p) asm volatile("" ::"v"(ma[p]), "v"(mb[p]));
+    for (; t < ntiles; t += 3 * G) {
+        tile(t, z0, z2, ma, mc);
+        if (t + G >= ntiles) break;
+        tile(t + G, z1, z0, mb, ma);
+        if (t + 2 * G >= ntiles) break;
+        tile(t + 2 * G, z2, z1, mc, mb);
     }
     flush();
+    async_wait();  // no direct-to-LDS load may still be in flight when the workgroup ends
 }
 
 template <typename F>
