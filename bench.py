@@ -7,7 +7,9 @@ Headline (one JSON line on stdout): triangle attention forward + backward at N_r
 algorithmic work 12*N*H*Sq*Sk*D per step. A step is one forward and one backward over the whole
 batch, through the C ABI with preallocated buffers; inputs rotate over 3 sets (~0.9 GB) so the
 256 MB Infinity Cache cannot hold them. Secondary figures: LayerNorm forward/backward and
-LayerNorm + gated dual projection on the 512x512x128 pair representation, in HBM GB/s.
+LayerNorm + gated dual projection on the 512x512x128 pair representation, and the attention
+output gate of MSA row attention (512 rows x 256 queries, 8 x 32 heads, 256 channels), in HBM
+GB/s.
 
 The roofline block names the kernel with the most time per step, its algorithmic work per launch
 divided by its average duration from per-launch HIP events on the launch stream (the library's
@@ -194,6 +196,36 @@ def bench_ln_gdp(torch, workloads, native, dev, stream, steps, warmup):
             "ln_gdp_TFLOPs": 4 * 2.0 * m * c * n / (t * 1e-3) / 1e12}
 
 
+def bench_attn_gate(torch, native, dev, stream, steps, warmup):
+    """Attention output gate of MSA row attention: o [512,8,256,32], x [512,256,256] ~N(0,1),
+    wg [256,256] ~N(0,1/256), bg = 0, bf16 -> [512,256,256]; rotates 3 sets (600 MB)."""
+    n, h, sq, d, c = 512, 8, 256, 32, 256
+    lib = native.lib()
+    sets = []
+    for r in range(3):
+        g = torch.Generator(device="cpu").manual_seed(60 + r)
+        o = torch.randn((n, h, sq, d), generator=g).to(torch.bfloat16).to(dev)
+        x = torch.randn((n, sq, c), generator=g).to(torch.bfloat16).to(dev)
+        wg = (torch.randn((c, h * d), generator=g) / c ** 0.5).to(torch.bfloat16).to(dev)
+        bg = torch.zeros(h * d, dtype=torch.bfloat16, device=dev)
+        sets.append((o, x, wg, bg, torch.empty((n, sq, h * d), dtype=torch.bfloat16, device=dev)))
+
+    def run(i):
+        o, x, wg, bg, out = sets[i % len(sets)]
+        st = lib.clk_attention_gate(stream, native.BF16, o.data_ptr(), x.data_ptr(),
+                                    wg.data_ptr(), bg.data_ptr(), out.data_ptr(), n, h, sq, d, c)
+        if st != 0:
+            raise RuntimeError(native.last_error())
+
+    so = torch.cuda.current_stream(dev)
+    t = timed(torch, run, steps, warmup, so)
+    nbytes = 2.0 * n * sq * (2 * h * d + c) + 2.0 * c * h * d
+    k = per_kernel(torch, native, run, steps)
+    return {"attn_gate_GBps": nbytes / (t * 1e-3) / 1e9, "attn_gate_ms": t,
+            "attn_gate_kernel_ms": k.get("attn_gate", {}).get("avg_ms"),
+            "attn_gate_bytes": nbytes}
+
+
 def recorded_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summaries."""
     pat = re.compile(r"^traffic_bytes_per_launch\[(\w+)\]:\s*([0-9.eE+]+)\s*$")
@@ -305,6 +337,9 @@ def main(argv=None):
         print("bench: timing LayerNorm + gated dual projection", file=sys.stderr, flush=True)
         sec.update(bench_ln_gdp(torch, workloads, native, dev, stream, args.steps, args.warmup))
         sec["ln_gdp_frac_hbm"] = sec["ln_gdp_GBps"] / HBM_PEAK
+        print("bench: timing the attention output gate", file=sys.stderr, flush=True)
+        sec.update(bench_attn_gate(torch, native, dev, stream, args.steps, args.warmup))
+        sec["attn_gate_frac_hbm"] = sec["attn_gate_GBps"] / HBM_PEAK
         result["secondary"] = sec
     if not args.no_cpu_baseline:
         print("bench: timing CPU baseline", file=sys.stderr, flush=True)

@@ -42,6 +42,7 @@ _TABLE = {
     "attention_bwd": ((_ARCH, _LIB, "ClkAttentionBwd"),),
     "layer_norm_bwd": ((_ARCH, _LIB, "ClkLayerNormBwd"),),
     "ln_gated_dual_proj": ((_ARCH, _LIB, "ClkLnGdp"),),
+    "attention_gate": ((_ARCH, _LIB, "ClkAttentionGate"),),
 }
 
 KERNELS = tuple(_TABLE)

@@ -267,6 +267,27 @@ def ln_gated_dual_proj(z, ln_scale, ln_offset, branch_a, branch_b, mask, eps=1e-
     return a, b
 
 
+def attention_gate(o, x, wg, bg):
+    """o * sigmoid(x.wg + bg), transposed to the output projection's layout: o [N,H,Sq,D] (the
+    attention output), x [N,Sq,C], wg [C,H*D], bg [H*D] -> [N,Sq,H*D]."""
+    what = "attention_gate"
+    dev = _require([("o", o), ("x", x), ("wg", wg), ("bg", bg)], what)
+    _shape_check(o.dim() == 4, what, "o must be [N,H,Sq,D]")
+    n, h, sq, d = o.shape
+    _shape_check(x.dim() == 3 and tuple(x.shape[:2]) == (n, sq), what, "x must be [N,Sq,C]")
+    c = x.shape[2]
+    _shape_check(tuple(wg.shape) == (c, h * d), what, "wg must be [C,H*D]")
+    _shape_check(tuple(bg.shape) == (h * d,), what, "bg must be [H*D]")
+    _shape_check(all(t.dtype == o.dtype for t in (x, wg, bg)), what,
+                 "all operands must share one dtype")
+    code = _dtype_code(o, (_native.F16, _native.BF16), what)
+    out = torch.empty((n, sq, h * d), device=dev, dtype=o.dtype)
+    with torch.cuda.device(dev):
+        _check(_native.lib().clk_attention_gate(_stream(dev), code, _ptr(o), _ptr(x), _ptr(wg),
+                                                _ptr(bg), _ptr(out), n, h, sq, d, c))
+    return out
+
+
 class AttentionFunction(torch.autograd.Function):
     """Differentiable attention: forward saves (out, lse); backward calls attention_bwd."""
 

@@ -108,6 +108,17 @@ __device__ __forceinline__ void unpack8(u32x4 raw, float* out) {
     for (int j = 0; j < 8; ++j) out[j] = TR::to_f(e[j]);
 }
 
+// Eight floats rounded to the 2-byte element type, as one 16-byte value.
+template <typename TR>
+__device__ __forceinline__ u32x4 pack8(const float* v) {
+    typename TR::elem e[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) e[j] = TR::from_f(v[j]);
+    u32x4 raw;
+    __builtin_memcpy(&raw, e, 16);
+    return raw;
+}
+
 // Raw buffer resource over `bytes` bytes at `base` (stride 0). Buffer loads check the whole
 // offset (VGPR offset + SGPR offset) against `bytes` and return zeros past it, so tiles that run
 // off the end of a slice need no per-lane selects, and the per-lane offsets stay the same from

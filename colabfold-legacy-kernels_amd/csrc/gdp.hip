@@ -34,17 +34,6 @@ __device__ __forceinline__ float sigmoid(float x) {
     return fast_rcp(1.f + fast_exp2(-x * kLog2e));
 }
 
-template <typename TR>
-__device__ __forceinline__ u32x4 pack8(const float* v) {
-    using E = typename TR::elem;
-    E e[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) e[j] = TR::from_f(v[j]);
-    u32x4 raw;
-    __builtin_memcpy(&raw, e, 16);
-    return raw;
-}
-
 // Stages rows [0, KP) x columns [n0, n0 + BN) of a row-major [K, N] weight into LDS (row stride
 // ld); rows past K and columns past N read as zero.
 template <typename E>

@@ -18,6 +18,7 @@
 //   ClkLayerNormBwd   x, scale, dy -> dx, dscale, doffset, workspace (u8); attribute eps
 //   ClkLnGdp          z, ln_scale, ln_offset, wpa, bpa, wga, bga, wpb, bpb, wgb, bgb, mask
 //                     -> a, b; attribute eps
+//   ClkAttentionGate  o [N,H,Sq,D], x [N,Sq,C], wg [C,H*D], bg [H*D] -> out [N,Sq,H*D]
 #include <hip/hip_runtime.h>
 
 #include <cstring>
@@ -321,6 +322,25 @@ clk_status ln_gdp(const Frame& f) {
                                   N, eps);
 }
 
+clk_status attention_gate(const Frame& f) {
+    const char* who = "ClkAttentionGate";
+    if (f.nargs() != 4 || f.nrets() != 1)
+        return bad(who, "expects 4 operands (o, x, wg, bg) and 1 result");
+    const Buffer *o = f.arg(0), *x = f.arg(1), *wg = f.arg(2), *bg = f.arg(3), *out = f.ret(0);
+    if (!o || !x || !wg || !bg || !out) return bad(who, "operands must be buffers");
+    if (o->rank != 4) return bad(who, "o must be [N,H,Sq,D]");
+    const int64_t N = o->dims[0], H = o->dims[1], Sq = o->dims[2], D = o->dims[3];
+    if (x->rank != 3 || x->dims[0] != N || x->dims[1] != Sq) return bad(who, "x must be [N,Sq,C]");
+    const int64_t C = x->dims[2];
+    if (!dims_are(wg, {C, H * D}) || !dims_are(bg, {H * D}) || !dims_are(out, {N, Sq, H * D}))
+        return bad(who, "wg [C,H*D], bg [H*D], out [N,Sq,H*D] expected");
+    const DataType t = o->dtype;
+    if (!half_type(t) || x->dtype != t || wg->dtype != t || bg->dtype != t || out->dtype != t)
+        return bad(who, "all operands must be f16 or all bf16");
+    return clk_attention_gate(f.stream(), static_cast<clk_dtype>(t), o->data, x->data, wg->data,
+                              bg->data, out->data, N, H, Sq, D, C);
+}
+
 }  // namespace
 
 #define CLK_FFI_EXPORT extern "C" __attribute__((visibility("default")))
@@ -351,4 +371,7 @@ CLK_FFI_EXPORT Error* VoltaGdpWmma(CallFrame* frame) {
 }
 CLK_FFI_EXPORT Error* ClkLnGdp(CallFrame* frame) {
     return run(frame, [](const Frame& f) { return ln_gdp(f); });
+}
+CLK_FFI_EXPORT Error* ClkAttentionGate(CallFrame* frame) {
+    return run(frame, [](const Frame& f) { return attention_gate(f); });
 }

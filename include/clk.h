@@ -137,6 +137,17 @@ clk_status clk_ln_gated_dual_proj(hipStream_t stream, clk_dtype dtype, const voi
                                   const void* bgb, const void* mask, void* a, void* b, int64_t M,
                                   int64_t C, int64_t N, float eps);
 
+/*
+ * Gated attention output (new; the reference leaves the gate to the caller's jnp code):
+ *   out[n, s, h*D + d] = o[n, h, s, d] * sigmoid(x[n, s, :] . wg[:, h*D + d] + bg[h*D + d])
+ * with o [N,H,Sq,D] the attention output, x [N,Sq,C] the attention's query-side input, wg
+ * [C, H*D] row-major, bg [H*D], out [N,Sq,H*D] (the layout the output projection reads). All of
+ * dtype CLK_F16 or CLK_BF16. C and H*D must each be 64, 128 or 256; D a multiple of 8.
+ */
+clk_status clk_attention_gate(hipStream_t stream, clk_dtype dtype, const void* o, const void* x,
+                              const void* wg, const void* bg, void* out, int64_t N, int64_t H,
+                              int64_t Sq, int64_t D, int64_t C);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

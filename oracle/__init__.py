@@ -13,6 +13,8 @@ attention     flash attention with pair bias and key mask, forward and backward
 layer_norm    LayerNorm forward and backward (restates cuda/volta_ops.cu:28-60)
 gdp           gated dual projection and the LayerNorm-fused variant
               (restates cuda/volta_ops.cu:97-208 and cuda/volta_gdp_wmma.cu:16-97)
+gate          the attention output gate O * sigmoid(x.Wg + bg) (no reference code: the caller's
+              jnp step after the attention targets)
 evoformer     the pair micro-block composed from the three (LN -> GDP, LN -> bias -> attention)
 
 How each function is pinned (tests/test_oracle.py): against independent textbook routines
@@ -24,6 +26,6 @@ golden vectors or tests for this path, and its CUDA/CUTLASS/XLA build cannot run
 reference binary is used.
 """
 
-from . import attention, layer_norm, gdp, evoformer  # noqa: F401
+from . import attention, layer_norm, gdp, gate, evoformer  # noqa: F401
 
-__all__ = ["attention", "layer_norm", "gdp", "evoformer"]
+__all__ = ["attention", "layer_norm", "gdp", "gate", "evoformer"]

@@ -127,3 +127,13 @@ def test_ln_gdp_validation(c, n):
     lib = _native.lib()
     assert lib.clk_ln_gated_dual_proj(None, BF16, *([FAKE] * 14), 4, c, n, 1e-5) == INVALID
     assert "multiples of 32" in _native.last_error()
+
+
+@pytest.mark.parametrize("n,h,sq,d,c,msg", [(2, 8, 16, 32, 96, "64, 128 or 256"),
+                                            (2, 3, 16, 32, 128, "64, 128 or 256"),
+                                            (2, 4, 16, 12, 128, "multiple of 8"),
+                                            (-1, 4, 16, 32, 128, "bad dims")])
+def test_attention_gate_validation(n, h, sq, d, c, msg):
+    lib = _native.lib()
+    assert lib.clk_attention_gate(None, BF16, *([FAKE] * 5), n, h, sq, d, c) == INVALID
+    assert msg in _native.last_error()

@@ -12,7 +12,7 @@ from _xla_ffi import BF16, F16, F32, F64, S32, S64, U8, FakeXla, Metadata, Metad
 pytestmark = pytest.mark.skipif(not clk.available("gfx950"), reason="library not built")
 
 TARGETS = ["VoltaMma", "VoltaWmma", "ClkAttentionFwd", "ClkAttentionBwd", "VoltaLayerNorm",
-           "ClkLayerNormBwd", "VoltaGdp", "VoltaGdpWmma", "ClkLnGdp"]
+           "ClkLayerNormBwd", "VoltaGdp", "VoltaGdpWmma", "ClkLnGdp", "ClkAttentionGate"]
 FAKE = 0x100000
 
 
@@ -117,3 +117,15 @@ def test_ln_gdp_operand_count(lib):
                  [("eps", F32, 1e-5)])
     assert x.call(lib, "ClkLnGdp", fr) is not None
     assert "12 operands" in x.errors[-1][1]
+
+
+def test_attention_gate_decode_errors(lib):
+    x = FakeXla()
+    fr = x.frame([x.buffer(BF16, (2, 8, 16, 32), FAKE), x.buffer(BF16, (2, 16, 256), FAKE),
+                  x.buffer(BF16, (256, 128), FAKE), x.buffer(BF16, (256,), FAKE)],
+                 [x.buffer(BF16, (2, 16, 256), FAKE)], [])
+    assert x.call(lib, "ClkAttentionGate", fr) is not None
+    assert "wg [C,H*D]" in x.errors[-1][1]
+    fr = x.frame([x.buffer(BF16, (2, 8, 16, 32), FAKE)], [x.buffer(BF16, (2, 16, 256), FAKE)], [])
+    assert x.call(lib, "ClkAttentionGate", fr) is not None
+    assert "4 operands" in x.errors[-1][1]

@@ -17,6 +17,7 @@ import torch
 
 from oracle import attention as A
 from oracle import evoformer as EV
+from oracle import gate as GT
 from oracle import gdp as G
 from oracle import layer_norm as L
 
@@ -287,6 +288,41 @@ def test_ln_gdp_is_the_composition():
     np.testing.assert_allclose(a, ref_a.numpy(), rtol=1e-12, atol=1e-14)
     ref_b = T(mask)[:, None] * (y @ T(wg) + T(bg)) * torch.sigmoid(y @ T(wp) + T(bp))
     np.testing.assert_allclose(bb, ref_b.numpy(), rtol=1e-12, atol=1e-14)
+
+
+def gate_case(seed, n=2, h=3, sq=5, d=4, c=6):
+    r = np.random.default_rng(seed)
+    return (r.standard_normal((n, h, sq, d)), r.standard_normal((n, sq, c)),
+            r.standard_normal((c, h * d)), r.standard_normal(h * d))
+
+
+def test_gate_closed_forms():
+    """Closed forms fixed by the definition alone: a zero gate pre-activation halves the
+    transposed O, saturated biases pass it or zero it, and one large weight gates a single
+    column by the sign of one input channel (which pins the orientation of wg and of the
+    [N,H,Sq,D] -> [N,Sq,H*D] transpose)."""
+    o, x, wg, bg = gate_case(0)
+    n, h, sq, d = o.shape
+    ot = np.stack([np.concatenate([o[b, hh, s] for hh in range(h)]) for b in range(n)
+                   for s in range(sq)]).reshape(n, sq, h * d)
+    np.testing.assert_array_equal(GT.attention_gate(o, x, 0 * wg, 0 * bg), 0.5 * ot)
+    np.testing.assert_array_equal(GT.attention_gate(o, x, 0 * wg, 0 * bg + 800), ot)
+    assert not GT.attention_gate(o, x, 0 * wg, 0 * bg - 800).any()
+    w1 = np.zeros_like(wg)
+    c0, j0 = 4, 7
+    w1[c0, j0] = 1e4
+    out = GT.attention_gate(o, x, w1, 0 * bg)
+    want = 0.5 * ot
+    want[..., j0] = ot[..., j0] * (x[..., c0] > 0)
+    np.testing.assert_allclose(out, want, rtol=0, atol=1e-300)
+
+
+def test_gate_matches_torch():
+    o, x, wg, bg = gate_case(1, n=3, h=2, sq=4, d=8, c=5)
+    ref = T(o).permute(0, 2, 1, 3).reshape(3, 4, 16) * torch.sigmoid(
+        torch.einsum("nsc,cj->nsj", T(x), T(wg)) + T(bg))
+    np.testing.assert_allclose(GT.attention_gate(o, x, wg, bg), ref.numpy(), rtol=1e-13,
+                               atol=1e-15)
 
 
 def test_pair_block_composes_the_ops():
