@@ -288,6 +288,23 @@ def attention_gate(o, x, wg, bg):
     return out
 
 
+def triangle_einsum(a, b):
+    """x[c] = a[c] . b[c]^T for channel-major a, b [C,N,N] (the triangle-multiplication
+    contraction with the channel index first and the contracted index last); N % 8 == 0."""
+    what = "triangle_einsum"
+    dev = _require([("a", a), ("b", b)], what)
+    _shape_check(a.dim() == 3 and a.shape[1] == a.shape[2], what, "a must be [C,N,N]")
+    _shape_check(tuple(b.shape) == tuple(a.shape) and b.dtype == a.dtype, what,
+                 "b must match a")
+    c, n, _ = a.shape
+    code = _dtype_code(a, (_native.F16, _native.BF16), what)
+    x = torch.empty_like(a)
+    with torch.cuda.device(dev):
+        _check(_native.lib().clk_triangle_einsum(_stream(dev), code, _ptr(a), _ptr(b), _ptr(x), c,
+                                                 n))
+    return x
+
+
 class AttentionFunction(torch.autograd.Function):
     """Differentiable attention: forward saves (out, lse); backward calls attention_bwd."""
 

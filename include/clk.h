@@ -148,6 +148,16 @@ clk_status clk_attention_gate(hipStream_t stream, clk_dtype dtype, const void* o
                               const void* wg, const void* bg, void* out, int64_t N, int64_t H,
                               int64_t Sq, int64_t D, int64_t C);
 
+/*
+ * Triangle-multiplication contraction, per channel (new; the reference stops at the gated
+ * projection): x[c] = a[c] . b[c]^T for a, b, x [C][N][N] row-major, i.e. channel-major with the
+ * contraction index last. With a[c][i][k] = a_pair[i,k,c] this is the outgoing update
+ * x[i,j,c] = sum_k a[i,k,c] b[j,k,c]; with a[c][i][k] = a_pair[k,i,c] the incoming one. dtype
+ * CLK_F16 or CLK_BF16, float32 accumulation. N must be a multiple of 8.
+ */
+clk_status clk_triangle_einsum(hipStream_t stream, clk_dtype dtype, const void* a, const void* b,
+                               void* x, int64_t C, int64_t N);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

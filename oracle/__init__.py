@@ -15,6 +15,8 @@ gdp           gated dual projection and the LayerNorm-fused variant
               (restates cuda/volta_ops.cu:97-208 and cuda/volta_gdp_wmma.cu:16-97)
 gate          the attention output gate O * sigmoid(x.Wg + bg) (no reference code: the caller's
               jnp step after the attention targets)
+triangle      the triangle-multiplication contraction, outgoing and incoming (no reference code:
+              the step after the gated dual projection)
 evoformer     the pair micro-block composed from the three (LN -> GDP, LN -> bias -> attention)
 
 How each function is pinned (tests/test_oracle.py): against independent textbook routines
@@ -26,6 +28,6 @@ golden vectors or tests for this path, and its CUDA/CUTLASS/XLA build cannot run
 reference binary is used.
 """
 
-from . import attention, layer_norm, gdp, gate, evoformer  # noqa: F401
+from . import attention, layer_norm, gdp, gate, triangle, evoformer  # noqa: F401
 
-__all__ = ["attention", "layer_norm", "gdp", "gate", "evoformer"]
+__all__ = ["attention", "layer_norm", "gdp", "gate", "triangle", "evoformer"]

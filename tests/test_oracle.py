@@ -20,6 +20,7 @@ from oracle import evoformer as EV
 from oracle import gate as GT
 from oracle import gdp as G
 from oracle import layer_norm as L
+from oracle import triangle as TM
 
 
 
@@ -340,3 +341,35 @@ def test_pair_block_composes_the_ops():
                                                            attn_mask=bias[None], scale=0.5)
     np.testing.assert_allclose(out["o"], ref.numpy(), rtol=1e-11, atol=1e-12)
     np.testing.assert_allclose(out["a"], out["b"], rtol=0, atol=0)
+
+
+# ---- triangle multiplication -------------------------------------------------------------------
+
+def test_triangle_einsum_matches_torch():
+    r = np.random.default_rng(3)
+    a, b = r.standard_normal((5, 6, 3)), r.standard_normal((5, 6, 3))
+    out = TM.pair_einsum(a[:, :5], b[:, :5], outgoing=True)
+    ref = torch.einsum("ikc,jkc->ijc", T(a[:, :5]), T(b[:, :5]))
+    np.testing.assert_allclose(out, ref.numpy(), rtol=1e-13, atol=1e-14)
+    a, b = r.standard_normal((6, 6, 3)), r.standard_normal((6, 6, 3))
+    out = TM.pair_einsum(a, b, outgoing=False)
+    ref = torch.einsum("kjc,kic->ijc", T(b), T(a))
+    np.testing.assert_allclose(out, ref.numpy(), rtol=1e-13, atol=1e-14)
+    ac, bc = r.standard_normal((2, 7, 9)), r.standard_normal((2, 5, 9))
+    np.testing.assert_allclose(TM.einsum(ac, bc), torch.einsum("cik,cjk->cij", T(ac), T(bc)),
+                               rtol=1e-13, atol=1e-14)
+
+
+def test_triangle_einsum_closed_forms():
+    """b = 1 turns the contraction into row sums of a; permuting k in both changes nothing."""
+    r = np.random.default_rng(4)
+    a = r.standard_normal((7, 7, 2))
+    ones = np.ones_like(a)
+    out = TM.pair_einsum(a, ones, outgoing=True)
+    np.testing.assert_allclose(out, np.repeat(a.sum(1)[:, None, :], 7, axis=1), rtol=1e-13)
+    out = TM.pair_einsum(a, ones, outgoing=False)
+    np.testing.assert_allclose(out, np.repeat(a.sum(0)[:, None, :], 7, axis=1), rtol=1e-13)
+    b = r.standard_normal((7, 7, 2))
+    p = r.permutation(7)
+    np.testing.assert_allclose(TM.pair_einsum(a[:, p], b[:, p]), TM.pair_einsum(a, b),
+                               rtol=1e-12, atol=1e-13)
