@@ -49,6 +49,10 @@ PROTOTYPES = {
                                    c_void_p, c_i64, c_i64, c_i64, c_i64, c_i64]),
     "clk_triangle_einsum": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_i64,
                                     c_i64]),
+    "clk_triangle_multiply_workspace_size": (c_size, [c_i64, c_i64]),
+    "clk_triangle_multiply": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                                      c_void_p, c_void_p, c_void_p, c_size, c_i64, c_i64, c_int,
+                                      c_f32]),
 }
 
 # Status codes (clk_status) and dtype codes (clk_dtype).

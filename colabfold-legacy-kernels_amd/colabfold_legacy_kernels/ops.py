@@ -16,6 +16,7 @@ Torch is used only for device memory and the current stream; all arithmetic runs
 library, and a missing library raises FileNotFoundError (there is no fallback path).
 """
 
+import ctypes
 import math
 
 import torch
@@ -303,6 +304,41 @@ def triangle_einsum(a, b):
         _check(_native.lib().clk_triangle_einsum(_stream(dev), code, _ptr(a), _ptr(b), _ptr(x), c,
                                                  n))
     return x
+
+
+def triangle_multiply(z, mask, ln_in, weights, biases, ln_center, outgoing=True, eps=1e-5):
+    """AlphaFold's triangle multiplication on the pair representation z [N,N,C] with mask [N,N].
+    ln_in, ln_center: (scale, offset) float32 [C]; weights: the six [C,C] matrices (left
+    projection, right projection, left gate, right gate, output projection, output gate), biases
+    their [C] vectors, all of z's dtype. Returns [N,N,C]."""
+    what = "triangle_multiply"
+    ws6, bs6 = list(weights), list(biases)
+    _shape_check(len(ws6) == 6 and len(bs6) == 6, what, "six weights and six biases")
+    lns = [ln_in[0], ln_in[1], ln_center[0], ln_center[1]]
+    dev = _require([("z", z), ("mask", mask)] + [("w%d" % i, w) for i, w in enumerate(ws6)]
+                   + [("b%d" % i, b) for i, b in enumerate(bs6)]
+                   + [("ln%d" % i, t) for i, t in enumerate(lns)], what)
+    _shape_check(z.dim() == 3 and z.shape[0] == z.shape[1], what, "z must be [N,N,C]")
+    n, _, c = z.shape
+    _shape_check(tuple(mask.shape) == (n, n) and mask.dtype == z.dtype, what,
+                 "mask must be [N,N] of z's dtype")
+    _shape_check(all(tuple(w.shape) == (c, c) and w.dtype == z.dtype for w in ws6), what,
+                 "weights must be [C,C] of z's dtype")
+    _shape_check(all(tuple(b.shape) == (c,) and b.dtype == z.dtype for b in bs6), what,
+                 "biases must be [C] of z's dtype")
+    _shape_check(all(tuple(t.shape) == (c,) and t.dtype == torch.float32 for t in lns), what,
+                 "LayerNorm scales and offsets must be float32 [C]")
+    code = _dtype_code(z, (_native.F16, _native.BF16), what)
+    lib = _native.lib()
+    wsb = lib.clk_triangle_multiply_workspace_size(n, c)
+    ws = torch.empty(max(wsb, 1), device=dev, dtype=torch.uint8)
+    out = torch.empty_like(z)
+    arr = lambda ts: (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])  # noqa: E731
+    with torch.cuda.device(dev):
+        _check(lib.clk_triangle_multiply(_stream(dev), code, _ptr(z), _ptr(mask), arr(lns),
+                                         arr(ws6), arr(bs6), _ptr(out), _ptr(ws), wsb, n, c,
+                                         1 if outgoing else 0, float(eps)))
+    return out
 
 
 class AttentionFunction(torch.autograd.Function):

@@ -175,7 +175,11 @@ struct LnGdpGeom {
     static constexpr int LPR = PL <= 4 ? 4 : PL <= 8 ? 8 : 16;
 };
 
-template <typename TR, int C, int N>
+// CM = false: a and b are [M, N] row-major (the pair layout). CM = true: a and b are channel-
+// major [N, M] (a[n][m]), the operand layout of the triangle-multiplication contraction; the MFMA
+// operands swap roles (out = xhat . W') so that a lane's accumulators hold four consecutive rows
+// of one output column, stored as one 8-byte piece of that column's plane. CM needs M % 64 == 0.
+template <typename TR, int C, int N, bool CM>
 __global__ __launch_bounds__(4 * N) void ln_gdp_kernel(
     const typename TR::elem* __restrict__ z, const float* __restrict__ gamma,
     const float* __restrict__ beta, LnGdpWeights<typename TR::elem> wb,
@@ -234,9 +238,15 @@ __global__ __launch_bounds__(4 * N) void ln_gdp_kernel(
                 }
             // The four lane groups hold disjoint k-slots of the same column.
             const float bcol = (xgroup_sum(part) + TR::to_f(wb.b[2 * br + mat][col])) * fold;
-            // C lane (r16, g) needs the columns 32cb + 8g + 4h + i, held by lanes r16' = 4g + i.
+            if constexpr (CM) {
+                // The column is the lane's own (B operand column r16); all four rows share it.
+                binit[mat][h] = f32x4{bcol, bcol, bcol, bcol};
+            } else {
+                // C lane (r16, g) needs the columns 32cb + 8g + 4h + i, held by lanes
+                // r16' = 4g + i.
 #pragma unroll
-            for (int i = 0; i < 4; ++i) binit[mat][h][i] = __shfl(bcol, 4 * g + i);
+                for (int i = 0; i < 4; ++i) binit[mat][h][i] = __shfl(bcol, 4 * g + i);
+            }
         }
     }
 
@@ -272,20 +282,37 @@ __global__ __launch_bounds__(4 * N) void ln_gdp_kernel(
     };
 
     // Outputs of the previous tile, stored after the next barrier: the barrier then never waits
-    // for fresh stores.
+    // for fresh stores. Row-major: one 16-byte piece per sub-tile (8 columns of one row).
+    // Channel-major: one 8-byte piece per sub-tile and column half (4 rows of one column).
+    constexpr int NST = CM ? 2 * SUB : SUB;  // stores per lane and tile
     u32x4 pend[SUB] = {};
+    u32x2 pendc[SUB][2] = {};
     Rsrc pend_out = out_rsrc(ntiles);  // empty: the first flush stores nothing
+    int pend_row = 0;
+    const Rsrc plane_out = buffer_rsrc(out, CM ? (uint32_t)((size_t)M * N * 2) : 0u);
     auto flush = [&]() {
+        if constexpr (CM) {
 #pragma unroll
-        for (int sub = 0; sub < SUB; ++sub)
-            buf_st16(pend_out, ((16 * sub + r16) * N + 32 * cb + 8 * g) * 2, 0, pend[sub]);
+            for (int sub = 0; sub < SUB; ++sub)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int col = 32 * cb + 8 * (r16 >> 2) + 4 * h + (r16 & 3);
+                    __builtin_amdgcn_raw_buffer_store_b64(
+                        pendc[sub][h], pend_out, (col * M + pend_row + 16 * sub + 4 * g) * 2, 0,
+                        0);
+                }
+        } else {
+#pragma unroll
+            for (int sub = 0; sub < SUB; ++sub)
+                buf_st16(pend_out, ((16 * sub + r16) * N + 32 * cb + 8 * g) * 2, 0, pend[sub]);
+        }
     };
 
     // Tile t is read from zc; tile t + 2*gridDim.x goes into zn, which held tile t - gridDim.x.
     // Issued after zc's loads: at least the SUB stores and the DPW loads of the tile before.
     auto tile = [&](int t, const char* zc, char* zn, const uint32_t (&mc)[PASSES],
                     uint32_t (&mn)[PASSES]) {
-        vm_wait<SUB + DPW>();
+        vm_wait<NST + DPW>();
         lds_barrier();  // z tile t in zc; every wave is done with xh and mk of the last tile
         flush();
         // LayerNorm: LPR lanes per row, 8 channels each; xhat into the swizzled tile.
@@ -328,7 +355,12 @@ __global__ __launch_bounds__(4 * N) void ln_gdp_kernel(
         const int tn = t + 2 * gridDim.x;
         load_mask(tn, mn);
         stage(tn, zn);
-        pend_out = out_rsrc(t);
+        if constexpr (CM) {
+            pend_out = plane_out;
+            pend_row = t * R;
+        } else {
+            pend_out = out_rsrc(t);
+        }
 
 #pragma unroll
         for (int sub = 0; sub < SUB; ++sub) {
@@ -346,16 +378,30 @@ __global__ __launch_bounds__(4 * N) void ln_gdp_kernel(
                 for (int mat = 0; mat < 2; ++mat)
 #pragma unroll
                     for (int h = 0; h < 2; ++h)
-                        acc[mat][h] = TR::mfma(wa[mat][h][ks], xb, acc[mat][h]);
+                        acc[mat][h] = CM ? TR::mfma(xb, wa[mat][h][ks], acc[mat][h])
+                                         : TR::mfma(wa[mat][h][ks], xb, acc[mat][h]);
             }
-            const float m = mk[xrow];
-            float o[8];
+            if constexpr (CM) {
+                // Lane (r16, g) holds rows 16sub + 4g + i of its column in each half h.
 #pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int h = j >> 2, i = j & 3;
-                o[j] = m * acc[0][h][i] * fast_rcp(1.f + fast_exp2(acc[1][h][i]));
+                for (int h = 0; h < 2; ++h) {
+                    E e[4];
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        e[i] = TR::from_f(mk[16 * sub + 4 * g + i] * acc[0][h][i] *
+                                          fast_rcp(1.f + fast_exp2(acc[1][h][i])));
+                    __builtin_memcpy(&pendc[sub][h], e, 8);
+                }
+            } else {
+                const float m = mk[xrow];
+                float o[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int h = j >> 2, i = j & 3;
+                    o[j] = m * acc[0][h][i] * fast_rcp(1.f + fast_exp2(acc[1][h][i]));
+                }
+                pend[sub] = pack8<TR>(o);
             }
-            pend[sub] = pack8<TR>(o);
         }
     };
 
@@ -429,7 +475,7 @@ clk_status dispatch_gdp(hipStream_t st, const void* x, const void* wp, const voi
     return launch_gdp<TR, 64>(st, x, wp, bp, wg, bg, mask, out, M, K, N);
 }
 
-template <typename TR, int C, int N>
+template <typename TR, int C, int N, bool CM = false>
 clk_status launch_ln_gdp(hipStream_t st, const void* z, const float* gamma, const float* beta,
                          const LnGdpWeights<typename TR::elem>& wb, const void* mask, void* a,
                          void* b, int M, float eps) {
@@ -440,7 +486,7 @@ clk_status launch_ln_gdp(hipStream_t st, const void* z, const float* gamma, cons
     const int per_cu = 128 / N;
     const int grid = ntiles < 256 * per_cu ? ntiles : 256 * per_cu;
     KernelTimer timer("ln_gdp", st);
-    ln_gdp_kernel<TR, C, N><<<grid, 4 * N, 0, st>>>((const E*)z, gamma, beta, wb,
+    ln_gdp_kernel<TR, C, N, CM><<<grid, 4 * N, 0, st>>>((const E*)z, gamma, beta, wb,
                                                      (const E*)mask, (E*)a, (E*)b, M, eps);
     return check_launch("ln_gated_dual_proj");
 }
@@ -467,6 +513,30 @@ clk_status dispatch_ln_gdp(hipStream_t st, const void* z, const float* gamma, co
 }
 
 }  // namespace
+
+// LayerNorm + both gated branches with channel-major outputs a, b [N][M], for the triangle-
+// multiplication contraction. Arguments checked by the caller; M % 64 == 0 and M*N*2 < 2^31.
+clk_status ln_gdp_channel_major(hipStream_t st, clk_dtype dtype, const void* z,
+                                const float* gamma, const float* beta, const void* const* w,
+                                const void* const* bias, const void* mask, void* a, void* b, int M,
+                                int C, int N, float eps) {
+    auto run = [&](auto tr) -> clk_status {
+        using TR = decltype(tr);
+        using E = typename TR::elem;
+        LnGdpWeights<E> wb;
+        for (int i = 0; i < 4; ++i) {
+            wb.w[i] = static_cast<const E*>(w[i]);
+            wb.b[i] = static_cast<const E*>(bias[i]);
+        }
+        if (C == 128 && N == 128)
+            return launch_ln_gdp<TR, 128, 128, true>(st, z, gamma, beta, wb, mask, a, b, M, eps);
+        if (C == 64 && N == 64)
+            return launch_ln_gdp<TR, 64, 64, true>(st, z, gamma, beta, wb, mask, a, b, M, eps);
+        return fail(CLK_INVALID_ARGUMENT, "ln_gdp_channel_major: C=%d, N=%d not supported", C, N);
+    };
+    return dtype == CLK_BF16 ? run(BF16{}) : run(F16{});
+}
+
 }  // namespace clk
 
 using namespace clk;

@@ -159,6 +159,251 @@ __global__ __launch_bounds__(512) void tri_einsum_kernel(const typename TR::elem
     async_wait();  // no direct-to-LDS load may still be in flight when the workgroup ends
 }
 
+// ---------------------------------------------------------------------------------------------
+// Output stage of the triangle multiplication (AlphaFold's centre LayerNorm, output projection
+// and output gate), one pass over the contraction result x and the input z:
+//   out[p, o] = (LN_c(x[:, p]) . w_out[:, o] + b_out[o]) * sigmoid(LN_in(z[p, :]) . w_g[:, o] + b_g[o])
+// x is channel-major [C][M] (as the contraction writes it), z and out are [M][C] (M = N*N
+// positions, C channels, both LayerNorms over C). As in the fused LayerNorm + gated projection,
+// the LN affines fold into the weights and biases, the gate carries -log2(e), and each wave holds
+// its 32 output columns of both matrices as MFMA A operands. A block walks 64-position tiles:
+// x's [C][64] slab and z's [64][C] rows arrive by direct buffer->LDS loads two tiles ahead; four
+// waves normalise the x slab (lane = position, 32 channels per lane group, reduced across the
+// four groups) and four the z rows, both into swizzled [64][C] tiles that feed the MFMAs.
+// ---------------------------------------------------------------------------------------------
+template <typename E>
+struct TriOutParams {
+    const E* x;
+    const E* z;
+    const float* gin;    // LN_in scale [C]
+    const float* bin;    // LN_in offset [C]
+    const float* gc;     // LN_c scale [C]
+    const float* bc;     // LN_c offset [C]
+    const E* wout;       // [C][C]
+    const E* bout;       // [C]
+    const E* wg;         // [C][C]
+    const E* bg;         // [C]
+    E* out;
+    int M;
+    float eps;
+};
+
+template <typename TR, int C>
+__global__ __launch_bounds__(512) void tri_out_kernel(TriOutParams<typename TR::elem> pr) {
+    using E = typename TR::elem;
+    using V8 = typename TR::vec8;
+    constexpr int NT = 512, KS = C / 32, R = 64, SUB = R / 16, PL = C / 8;
+    constexpr int NCG = C / 32, NSPLIT = 8 / NCG, SUBW = SUB / NSPLIT;  // column groups, subs
+    static_assert(NSPLIT * NCG == 8 && SUBW * NSPLIT == SUB, "eight waves");
+    constexpr int SWZ = 15 & (PL - 1);
+    constexpr int LPR = PL;  // z LayerNorm: lanes per row (8 channels each)
+    constexpr int CPG = C / 4;  // x LayerNorm: channels per lane group
+    static_assert(LPR == 8 || LPR == 16, "C = 64 or 128");
+    constexpr int ZB = R * C * 2;
+    constexpr int DPZ = R * PL / NT;           // z loads per lane and tile
+    constexpr int XSLOTS = C * (R / 8);        // 16-byte pieces of the x slab
+    constexpr int DPX = XSLOTS / NT;           // x loads per lane and tile
+    static_assert(DPZ * NT == R * PL && DPX * NT == XSLOTS, "whole load rounds");
+    // x slab in LDS: channel row c holds 128 bytes; every 8 rows (one wave's load) are followed
+    // by 16 bytes of padding, so the four lane groups of a LayerNorm read hit distinct banks.
+    constexpr int XB = XSLOTS * 16 + (XSLOTS / 64) * 16;
+
+    __shared__ __attribute__((aligned(16))) char z0[ZB];
+    __shared__ __attribute__((aligned(16))) char z1[ZB];
+    __shared__ __attribute__((aligned(16))) char z2[ZB];
+    __shared__ __attribute__((aligned(16))) char x0[XB];
+    __shared__ __attribute__((aligned(16))) char x1[XB];
+    __shared__ __attribute__((aligned(16))) char x2[XB];
+    __shared__ __attribute__((aligned(16))) char xh1[ZB];  // LN_c(x), [64][C] swizzled
+    __shared__ __attribute__((aligned(16))) char xh2[ZB];  // LN_in(z), [64][C] swizzled
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r16 = lane & 15, g = lane >> 4;
+    const int cb = wave % NCG, sh = wave / NCG;
+    const int M = pr.M;
+
+    // Resident A operands: mat 0 = diag(gc) w_out, mat 1 = -log2(e) diag(gin) w_g, and the folded
+    // biases (bc . w_out + b_out, -log2(e) (bin . w_g + b_g)) in C-tile layout.
+    V8 wa[2][2][KS];
+    f32x4 binit[2][2];
+#pragma unroll
+    for (int mat = 0; mat < 2; ++mat) {
+        const E* W = mat == 0 ? pr.wout : pr.wg;
+        const float* gam = mat == 0 ? pr.gc : pr.gin;
+        const float* bet = mat == 0 ? pr.bc : pr.bin;
+        const float fold = mat == 1 ? -kLog2e : 1.f;
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int col = 32 * cb + 8 * (r16 >> 2) + 4 * h + (r16 & 3);
+            float part = 0.f;
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int k = 32 * ks + 8 * g + j;
+                    const float v = TR::to_f(W[k * C + col]);
+                    wa[mat][h][ks][j] = TR::from_f(gam[k] * v * fold);
+                    part = fmaf(bet[k], v, part);
+                }
+            const E* bias = mat == 0 ? pr.bout : pr.bg;
+            const float bcol = (xgroup_sum(part) + TR::to_f(bias[col])) * fold;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) binit[mat][h][i] = __shfl(bcol, 4 * g + i);
+        }
+    }
+
+    const int ntiles = M / R;
+    // Every tile issues DPX + DPZ direct-to-LDS loads and SUBW stores in every wave (tiles past
+    // the end load from empty resources; the first store batch goes to an empty resource).
+    auto stage = [&](int t, char* xb, char* zb) {
+        const bool live = t < ntiles;
+        const Rsrc rx = buffer_rsrc(live ? pr.x + (size_t)t * R : pr.x,
+                                    live ? (uint32_t)((size_t)(C - 1) * M * 2 + R * 2) : 0u);
+        const Rsrc rz = buffer_rsrc(live ? pr.z + (size_t)t * R * C : pr.z,
+                                    live ? (uint32_t)(R * C * 2) : 0u);
+#pragma unroll
+        for (int k = 0; k < DPX; ++k) {
+            const int b = k * NT + wave * 64, slot = b + lane;
+            const int c = slot / (R / 8), q = slot % (R / 8);
+            buf_dma16(rx, (c * M + q * 8) * 2, 0, xb + b * 16 + (b / 64) * 16);
+        }
+#pragma unroll
+        for (int k = 0; k < DPZ; ++k) {
+            const int b = k * NT + wave * 64;
+            buf_dma16(rz, (b + lane) * 16, 0, zb + b * 16);
+        }
+    };
+    const Rsrc out_all = buffer_rsrc(pr.out, (uint32_t)((size_t)M * C * 2));
+    u32x4 pend[SUBW] = {};
+    Rsrc pend_out = buffer_rsrc(pr.out, 0);
+    int pend_row = 0;
+    auto flush = [&]() {
+#pragma unroll
+        for (int s = 0; s < SUBW; ++s) {
+            const int row = pend_row + 16 * (sh * SUBW + s) + r16;
+            buf_st16(pend_out, (row * C + 32 * cb + 8 * g) * 2, 0, pend[s]);
+        }
+    };
+
+    auto tile = [&](int t, const char* xc, const char* zc, char* xn, char* zn) {
+        vm_wait<SUBW + DPX + DPZ>();
+        lds_barrier();  // tile t in xc, zc; every wave is done with xh1, xh2 of the last tile
+        flush();
+        if (wave < 4) {
+            // LN_c over the x slab: lane (r16, g) of wave w takes position 16w + r16, channels
+            // CPG*g .. CPG*g + CPG-1; the four lane groups of a position combine by permlane
+            // swaps.
+            const int p = 16 * wave + r16;
+            // Channel pairs packed two to a register (the values stay in the input type).
+            uint32_t vp[CPG / 2];
+            auto val = [&](int j) {
+                const uint32_t w2 = vp[j >> 1];
+                return TR::to_f(__builtin_bit_cast(E, (uint16_t)((j & 1) ? w2 >> 16 : w2)));
+            };
+            float sum = 0.f;
+#pragma unroll
+            for (int j = 0; j < CPG; j += 2) {
+                const char* at = xc + (CPG * g + j) * (R * 2) + ((CPG * g + j) / 8) * 16 + p * 2;
+                const uint32_t lo = *reinterpret_cast<const uint16_t*>(at);
+                const uint32_t hi = *reinterpret_cast<const uint16_t*>(at + R * 2);
+                vp[j >> 1] = lo | (hi << 16);
+                sum += val(j) + val(j + 1);
+            }
+            const float mean = xgroup_sum(sum) * (1.f / C);
+            float m2 = 0.f;
+#pragma unroll
+            for (int j = 0; j < CPG; ++j) {
+                const float d = val(j) - mean;
+                m2 = fmaf(d, d, m2);
+            }
+            const float rstd = rsqrtf(xgroup_sum(m2) * (1.f / C) + pr.eps);
+#pragma unroll
+            for (int q = 0; q < CPG / 8; ++q) {
+                float xo[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) xo[j] = (val(8 * q + j) - mean) * rstd;
+                const int piece = (CPG / 8) * g + q;
+                *reinterpret_cast<u32x4*>(xh1 + p * PL * 16 + 16 * (piece ^ (p & SWZ))) =
+                    pack8<TR>(xo);
+            }
+        } else {
+            // LN_in over the z rows: LPR lanes per row, 8 channels each.
+            const int lt = tid - 256, lr = lt % LPR;
+            constexpr int RPP = 256 / LPR;
+#pragma unroll
+            for (int pass = 0; pass < R / RPP; ++pass) {
+                const int row = pass * RPP + lt / LPR;
+                float v[8];
+                unpack8<TR>(*reinterpret_cast<const u32x4*>(zc + row * C * 2 + lr * 16), v);
+                float sum = 0.f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) sum += v[j];
+                const float mean = group_sum<LPR>(sum) * (1.f / C);
+                float m2 = 0.f;
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float d = v[j] - mean;
+                    m2 = fmaf(d, d, m2);
+                }
+                const float rstd = rsqrtf(group_sum<LPR>(m2) * (1.f / C) + pr.eps);
+                float xo[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) xo[j] = (v[j] - mean) * rstd;
+                *reinterpret_cast<u32x4*>(xh2 + row * PL * 16 + 16 * (lr ^ (row & SWZ))) =
+                    pack8<TR>(xo);
+            }
+        }
+        lds_barrier();  // xh1, xh2 of tile t ready; xn, zn are free
+        stage(t + 2 * gridDim.x, xn, zn);
+        pend_out = out_all;
+        pend_row = t * R;
+#pragma unroll
+        for (int s = 0; s < SUBW; ++s) {
+            const int xrow = 16 * (sh * SUBW + s) + r16;
+            f32x4 acc[2][2];
+#pragma unroll
+            for (int mat = 0; mat < 2; ++mat)
+#pragma unroll
+                for (int h = 0; h < 2; ++h) acc[mat][h] = binit[mat][h];
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const int off = xrow * PL * 16 + 16 * ((4 * ks + g) ^ (xrow & SWZ));
+                const V8 b1 = *reinterpret_cast<const V8*>(xh1 + off);
+                const V8 b2 = *reinterpret_cast<const V8*>(xh2 + off);
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    acc[0][h] = TR::mfma(wa[0][h][ks], b1, acc[0][h]);
+                    acc[1][h] = TR::mfma(wa[1][h][ks], b2, acc[1][h]);
+                }
+            }
+            float o[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int h = j >> 2, i = j & 3;
+                o[j] = acc[0][h][i] * fast_rcp(1.f + fast_exp2(acc[1][h][i]));
+            }
+            pend[s] = pack8<TR>(o);
+        }
+    };
+
+    const int G = gridDim.x;
+    int t = blockIdx.x;
+    stage(t, x0, z0);
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);
+    flush();
+    stage(t + G, x1, z1);
+    for (; t < ntiles; t += 3 * G) {
+        tile(t, x0, z0, x2, z2);
+        if (t + G >= ntiles) break;
+        tile(t + G, x1, z1, x0, z0);
+        if (t + 2 * G >= ntiles) break;
+        tile(t + 2 * G, x2, z2, x1, z1);
+    }
+    flush();
+    async_wait();  // no direct-to-LDS load may still be in flight when the workgroup ends
+}
+
 template <typename TR>
 clk_status launch_einsum(hipStream_t st, const void* a, const void* b, void* x, int C, int N) {
     using E = typename TR::elem;
@@ -169,7 +414,63 @@ clk_status launch_einsum(hipStream_t st, const void* a, const void* b, void* x, 
     return check_launch("triangle_einsum");
 }
 
+// Transposes each [N][N] plane of a [P][N][N] tensor (N % 8 == 0) through a 64 x 64 LDS tile:
+// 16-byte reads of rows, 2-byte LDS scatter, 16-byte writes of the transposed rows.
+template <typename E>
+__global__ __launch_bounds__(256) void plane_transpose_kernel(const E* __restrict__ in,
+                                                              E* __restrict__ out, int N, int T) {
+    __shared__ E tile[64][64 + 8];
+    const int tid = threadIdx.x;
+    const int w = blockIdx.x, plane = w / (T * T), ti = (w / T) % T, tj = w % T;
+    const size_t base = (size_t)plane * N * N;
+    const int r0 = ti * 64, c0 = tj * 64;
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+        const int idx = tid + it * 256, r = idx / 8, c8 = (idx % 8) * 8;
+        if (r0 + r < N && c0 + c8 < N) {
+            const u32x4 v = ld16(in + base + (size_t)(r0 + r) * N + c0 + c8);
+            E e[8];
+            __builtin_memcpy(e, &v, 16);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) tile[c8 + j][r] = e[j];
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int it = 0; it < 2; ++it) {
+        const int idx = tid + it * 256, r = idx / 8, c8 = (idx % 8) * 8;
+        // Output row c0 + r holds input column c0 + r, input rows r0 + c8 .. r0 + c8 + 7.
+        if (c0 + r < N && r0 + c8 < N)
+            st16(out + base + (size_t)(c0 + r) * N + r0 + c8,
+                 *reinterpret_cast<const u32x4*>(&tile[r][c8]));
+    }
+}
+
+template <typename TR>
+clk_status launch_transpose(hipStream_t st, const void* in, void* out, int P, int N) {
+    using E = typename TR::elem;
+    const int T = (N + 63) / 64;
+    KernelTimer timer("tri_transpose", st);
+    plane_transpose_kernel<E><<<P * T * T, 256, 0, st>>>((const E*)in, (E*)out, N, T);
+    return check_launch("triangle_multiply (transpose)");
+}
+
+template <typename TR, int C>
+clk_status launch_tri_out(hipStream_t st, const TriOutParams<typename TR::elem>& pr) {
+    const int ntiles = pr.M / 64;
+    const int grid = ntiles < 256 ? ntiles : 256;
+    KernelTimer timer("tri_out", st);
+    tri_out_kernel<TR, C><<<grid, 512, 0, st>>>(pr);
+    return check_launch("triangle_multiply (output)");
+}
+
 }  // namespace
+
+clk_status ln_gdp_channel_major(hipStream_t st, clk_dtype dtype, const void* z,
+                                const float* gamma, const float* beta, const void* const* w,
+                                const void* const* bias, const void* mask, void* a, void* b, int M,
+                                int C, int N, float eps);
+
 }  // namespace clk
 
 using namespace clk;
@@ -192,4 +493,87 @@ extern "C" clk_status clk_triangle_einsum(hipStream_t stream, clk_dtype dtype, c
         return fail(CLK_INVALID_ARGUMENT, "%s: a, b, x must be 16-byte aligned", who);
     if (dtype == CLK_BF16) return launch_einsum<BF16>(stream, a, b, x, (int)C, (int)N);
     return launch_einsum<F16>(stream, a, b, x, (int)C, (int)N);
+}
+
+extern "C" size_t clk_triangle_multiply_workspace_size(int64_t N, int64_t C) {
+    if (N <= 0 || C <= 0) return 0;
+    return (size_t)3 * (size_t)C * (size_t)N * (size_t)N * 2;
+}
+
+extern "C" clk_status clk_triangle_multiply(hipStream_t stream, clk_dtype dtype, const void* z,
+                                            const void* mask, const float* const* ln,
+                                            const void* const* w, const void* const* b, void* out,
+                                            void* workspace, size_t workspace_bytes, int64_t N,
+                                            int64_t C, int outgoing, float eps) {
+    const char* who = "triangle_multiply";
+    if (dtype != CLK_F16 && dtype != CLK_BF16)
+        return fail(CLK_INVALID_ARGUMENT, "%s: dtype %s not supported (f16, bf16)", who,
+                    dtype_name(dtype));
+    if (N < 0 || (C != 64 && C != 128))
+        return fail(CLK_INVALID_ARGUMENT, "%s: C must be 64 or 128 (C=%lld)", who, (long long)C);
+    if (N % 8) return fail(CLK_INVALID_ARGUMENT, "%s: N=%lld is not a multiple of 8", who,
+                           (long long)N);
+    if (N * N * C * 2 >= ((int64_t)1 << 31))
+        return fail(CLK_INVALID_ARGUMENT, "%s: N=%lld too large", who, (long long)N);
+    if (N == 0) return ok();
+    if (!z || !mask || !ln || !w || !b || !out || !workspace)
+        return fail(CLK_INVALID_ARGUMENT, "%s: null operand pointer", who);
+    for (int i = 0; i < 4; ++i)
+        if (!ln[i]) return fail(CLK_INVALID_ARGUMENT, "%s: null LayerNorm parameter", who);
+    for (int i = 0; i < 6; ++i)
+        if (!w[i] || !b[i]) return fail(CLK_INVALID_ARGUMENT, "%s: null weight or bias", who);
+    if (!aligned16(z) || !aligned16(out) || !aligned16(workspace))
+        return fail(CLK_INVALID_ARGUMENT, "%s: z, out, workspace must be 16-byte aligned", who);
+    const size_t need = clk_triangle_multiply_workspace_size(N, C);
+    if (workspace_bytes < need)
+        return fail(CLK_INVALID_ARGUMENT, "%s: workspace of %zu bytes, %zu needed", who,
+                    workspace_bytes, need);
+    const int M = (int)(N * N), n = (int)N, c = (int)C;
+    const size_t plane_set = (size_t)C * M * 2;
+    char* wa = static_cast<char*>(workspace);
+    char* wb = wa + plane_set;
+    char* wx = wb + plane_set;
+    // 1. LN_in(z) and the four projections -> left (wa), right (wb), channel-major [C][N][N].
+    const void* proj_w[4] = {w[0], w[2], w[1], w[3]};  // left proj, left gate, right proj, right gate
+    const void* proj_b[4] = {b[0], b[2], b[1], b[3]};
+    clk_status s = ln_gdp_channel_major(stream, dtype, z, ln[0], ln[1], proj_w, proj_b, mask, wa,
+                                        wb, M, c, c, eps);
+    if (s != CLK_OK) return s;
+    // 2. The contraction x[c] = A[c] . B[c]^T: outgoing A = left, B = right; incoming
+    //    A = right^T, B = left^T (x[i,j] = sum_k left[k,j] right[k,i]).
+    const void *A = wa, *B = wb;
+    void* X = wx;
+    auto transpose = [&](const void* in, void* o) {
+        return dtype == CLK_BF16 ? launch_transpose<BF16>(stream, in, o, c, n)
+                                 : launch_transpose<F16>(stream, in, o, c, n);
+    };
+    if (!outgoing) {
+        if ((s = transpose(wb, wx)) != CLK_OK) return s;  // right^T
+        if ((s = transpose(wa, wb)) != CLK_OK) return s;  // left^T
+        A = wx;
+        B = wb;
+        X = wa;
+    }
+    if ((s = clk_triangle_einsum(stream, dtype, A, B, X, C, N)) != CLK_OK) return s;
+    // 3. LN_c(x), output projection, output gate from LN_in(z).
+    auto finish = [&](auto tr) -> clk_status {
+        using TR = decltype(tr);
+        using E = typename TR::elem;
+        TriOutParams<E> pr;
+        pr.x = static_cast<const E*>(X);
+        pr.z = static_cast<const E*>(z);
+        pr.gin = ln[0];
+        pr.bin = ln[1];
+        pr.gc = ln[2];
+        pr.bc = ln[3];
+        pr.wout = static_cast<const E*>(w[4]);
+        pr.bout = static_cast<const E*>(b[4]);
+        pr.wg = static_cast<const E*>(w[5]);
+        pr.bg = static_cast<const E*>(b[5]);
+        pr.out = static_cast<E*>(out);
+        pr.M = M;
+        pr.eps = eps;
+        return c == 128 ? launch_tri_out<TR, 128>(stream, pr) : launch_tri_out<TR, 64>(stream, pr);
+    };
+    return dtype == CLK_BF16 ? finish(BF16{}) : finish(F16{});
 }

@@ -158,6 +158,26 @@ clk_status clk_attention_gate(hipStream_t stream, clk_dtype dtype, const void* o
 clk_status clk_triangle_einsum(hipStream_t stream, clk_dtype dtype, const void* a, const void* b,
                                void* x, int64_t C, int64_t N);
 
+/*
+ * Triangle multiplication (new; AlphaFold's TriangleMultiplication after the reference's gated
+ * projection): for the pair representation z [N,N,C] and mask [N,N],
+ *   y = LN_in(z); left = mask*(y.w[0]+b[0])*sigmoid(y.w[2]+b[2]);
+ *   right = mask*(y.w[1]+b[1])*sigmoid(y.w[3]+b[3]);
+ *   x = outgoing ? einsum('ikc,jkc->ijc', left, right) : einsum('kjc,kic->ijc', left, right);
+ *   out = (LN_c(x).w[4] + b[4]) * sigmoid(y.w[5] + b[5])
+ * w[0..5] = left projection, right projection, left gate, right gate, output projection, output
+ * gate, each [C,C] row-major (input channel first); b[0..5] their [C] biases; ln[0..3] = LN_in
+ * scale, offset, LN_c scale, offset (float32 [C]). z, mask, weights, biases and out of dtype
+ * CLK_F16 or CLK_BF16. C = 64 or 128; N a multiple of 8. The workspace holds left, right and x
+ * channel-major (clk_triangle_multiply_workspace_size bytes).
+ */
+size_t clk_triangle_multiply_workspace_size(int64_t N, int64_t C);
+clk_status clk_triangle_multiply(hipStream_t stream, clk_dtype dtype, const void* z,
+                                 const void* mask, const float* const* ln, const void* const* w,
+                                 const void* const* b, void* out, void* workspace,
+                                 size_t workspace_bytes, int64_t N, int64_t C, int outgoing,
+                                 float eps);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

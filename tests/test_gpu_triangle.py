@@ -25,18 +25,19 @@ def test_einsum_parity(cuda, c, n, dtype):
 
 
 def test_einsum_pair_directions(cuda):
-    """Both pair-layout directions through the channel-major kernel: outgoing takes a[c][i][k] =
-    a[i,k,c], incoming a[c][i][k] = a[k,i,c]."""
+    """Both pair-layout directions through the channel-major kernel (left = a, right = b)."""
     n, c = 72, 6
     g = torch.Generator().manual_seed(7)
     a = torch.randn((n, n, c), generator=g).to(torch.bfloat16)
     b = torch.randn((n, n, c), generator=g).to(torch.bfloat16)
     for outgoing in (True, False):
-        perm = (2, 0, 1) if outgoing else (2, 1, 0)
-        ac = a.permute(*perm).contiguous().to(cuda)
-        bc = b.permute(*perm).contiguous().to(cuda)
-        x = ops.triangle_einsum(ac, bc).permute(1, 2, 0)
-        assert_close("x", x, ref.pair_einsum(np64(a), np64(b), outgoing), TOL["bf16"]["o"])
+        if outgoing:   # A[c][i][k] = left[i,k,c], B[c][j][k] = right[j,k,c]
+            ac, bc = a.permute(2, 0, 1), b.permute(2, 0, 1)
+        else:          # A[c][i][k] = right[k,i,c], B[c][j][k] = left[k,j,c]
+            ac, bc = b.permute(2, 1, 0), a.permute(2, 1, 0)
+        x = ops.triangle_einsum(ac.contiguous().to(cuda), bc.contiguous().to(cuda))
+        assert_close("x", x.permute(1, 2, 0), ref.pair_einsum(np64(a), np64(b), outgoing),
+                     TOL["bf16"]["o"])
 
 
 def test_einsum_large_repeatable(cuda):
@@ -50,3 +51,41 @@ def test_einsum_large_repeatable(cuda):
     for ch in (0, 37, 127):
         assert_close("x[%d]" % ch, x[ch], ref.einsum(np64(a[ch:ch + 1]), np64(b[ch:ch + 1]))[0],
                      TOL["bf16"]["o"])
+
+
+def module_case(n, c, dtype, seed, dev):
+    g = torch.Generator().manual_seed(seed)
+    rnd = lambda *s, std=1.0: torch.randn(s, generator=g) * std  # noqa: E731
+    z = rnd(n, n, c).to(dtype)
+    mask = (torch.rand((n, n), generator=g) > 0.1).to(dtype)
+    ln_in = (1 + rnd(c, std=0.1), rnd(c, std=0.1))
+    ln_c = (1 + rnd(c, std=0.1), rnd(c, std=0.1))
+    ws = [rnd(c, c, std=c ** -0.5).to(dtype) for _ in range(6)]
+    bs = [rnd(c, std=0.3).to(dtype) for _ in range(6)]
+    d = lambda t: t.to(dev)  # noqa: E731
+    return (d(z), d(mask), tuple(map(d, ln_in)), [d(w) for w in ws], [d(b) for b in bs],
+            tuple(map(d, ln_c)))
+
+
+# (N, C): the pair stack's 128 channels and the template stack's 64, one 64-position tile,
+# several tiles, N not a multiple of 64 (ragged contraction tiles).
+MODULE_SHAPES = [(8, 128), (64, 128), (72, 128), (40, 64), (136, 64)]
+
+
+@pytest.mark.parametrize("outgoing", [True, False], ids=["outgoing", "incoming"])
+@pytest.mark.parametrize("n,c", MODULE_SHAPES)
+def test_triangle_multiply_parity(cuda, n, c, outgoing):
+    z, mask, ln_in, ws, bs, ln_c = module_case(n, c, torch.bfloat16, n + c, cuda)
+    out = ops.triangle_multiply(z, mask, ln_in, ws, bs, ln_c, outgoing)
+    r = ref.triangle_multiply(np64(z), np64(mask), tuple(map(np64, ln_in)), [np64(w) for w in ws],
+                              [np64(b) for b in bs], tuple(map(np64, ln_c)), outgoing)
+    assert_close("out", out, r, 2e-2)
+
+
+def test_triangle_multiply_f16_and_repeatable(cuda):
+    z, mask, ln_in, ws, bs, ln_c = module_case(64, 128, torch.float16, 3, cuda)
+    out = ops.triangle_multiply(z, mask, ln_in, ws, bs, ln_c, True)
+    assert torch.equal(out, ops.triangle_multiply(z, mask, ln_in, ws, bs, ln_c, True))
+    r = ref.triangle_multiply(np64(z), np64(mask), tuple(map(np64, ln_in)), [np64(w) for w in ws],
+                              [np64(b) for b in bs], tuple(map(np64, ln_c)), True)
+    assert_close("out", out, r, 1e-2)

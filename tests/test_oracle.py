@@ -353,7 +353,7 @@ def test_triangle_einsum_matches_torch():
     np.testing.assert_allclose(out, ref.numpy(), rtol=1e-13, atol=1e-14)
     a, b = r.standard_normal((6, 6, 3)), r.standard_normal((6, 6, 3))
     out = TM.pair_einsum(a, b, outgoing=False)
-    ref = torch.einsum("kjc,kic->ijc", T(b), T(a))
+    ref = torch.einsum("kjc,kic->ijc", T(a), T(b))
     np.testing.assert_allclose(out, ref.numpy(), rtol=1e-13, atol=1e-14)
     ac, bc = r.standard_normal((2, 7, 9)), r.standard_normal((2, 5, 9))
     np.testing.assert_allclose(TM.einsum(ac, bc), torch.einsum("cik,cjk->cij", T(ac), T(bc)),
@@ -367,9 +367,32 @@ def test_triangle_einsum_closed_forms():
     ones = np.ones_like(a)
     out = TM.pair_einsum(a, ones, outgoing=True)
     np.testing.assert_allclose(out, np.repeat(a.sum(1)[:, None, :], 7, axis=1), rtol=1e-13)
-    out = TM.pair_einsum(a, ones, outgoing=False)
+    out = TM.pair_einsum(ones, a, outgoing=False)   # x[i,j] = sum_k right[k,i]
     np.testing.assert_allclose(out, np.repeat(a.sum(0)[:, None, :], 7, axis=1), rtol=1e-13)
     b = r.standard_normal((7, 7, 2))
     p = r.permutation(7)
     np.testing.assert_allclose(TM.pair_einsum(a[:, p], b[:, p]), TM.pair_einsum(a, b),
                                rtol=1e-12, atol=1e-13)
+
+
+def test_triangle_multiply_matches_torch():
+    """The whole module against an independent torch float64 statement of AlphaFold's
+    TriangleMultiplication (layer_norm, linear layers, sigmoid gates, einsum)."""
+    r = np.random.default_rng(5)
+    n, c = 6, 4
+    z = r.standard_normal((n, n, c))
+    mask = (r.random((n, n)) > 0.2).astype(np.float64)
+    ln_in = (1 + 0.1 * r.standard_normal(c), 0.1 * r.standard_normal(c))
+    ln_c = (1 + 0.1 * r.standard_normal(c), 0.1 * r.standard_normal(c))
+    ws = [r.standard_normal((c, c)) / 2 for _ in range(6)]
+    bs = [r.standard_normal(c) / 2 for _ in range(6)]
+    F = torch.nn.functional
+    for outgoing, eq in ((True, "ikc,jkc->ijc"), (False, "kjc,kic->ijc")):
+        y = F.layer_norm(T(z), (c,), T(ln_in[0]), T(ln_in[1]), 1e-5)
+        m = T(mask)[..., None]
+        left = m * (y @ T(ws[0]) + T(bs[0])) * torch.sigmoid(y @ T(ws[2]) + T(bs[2]))
+        right = m * (y @ T(ws[1]) + T(bs[1])) * torch.sigmoid(y @ T(ws[3]) + T(bs[3]))
+        x = F.layer_norm(torch.einsum(eq, left, right), (c,), T(ln_c[0]), T(ln_c[1]), 1e-5)
+        ref = (x @ T(ws[4]) + T(bs[4])) * torch.sigmoid(y @ T(ws[5]) + T(bs[5]))
+        out = TM.triangle_multiply(z, mask, ln_in, ws, bs, ln_c, outgoing)
+        np.testing.assert_allclose(out, ref.numpy(), rtol=1e-12, atol=1e-13)
