@@ -9,7 +9,7 @@ batch, through the C ABI with preallocated buffers; inputs rotate over 3 sets (~
 256 MB Infinity Cache cannot hold them. Secondary figures: LayerNorm forward/backward and
 LayerNorm + gated dual projection on the 512x512x128 pair representation, and the attention
 output gate of MSA row attention (512 rows x 256 queries, 8 x 32 heads, 256 channels), in HBM
-GB/s.
+GB/s; the triangle multiplication (outgoing, incoming) on z [512,512,128] per kernel.
 
 The roofline block names the kernel with the most time per step, its algorithmic work per launch
 divided by its average duration from per-launch HIP events on the launch stream (the library's
@@ -226,6 +226,48 @@ def bench_attn_gate(torch, native, dev, stream, steps, warmup):
             "attn_gate_bytes": nbytes}
 
 
+def bench_triangle(torch, native, dev, stream, steps, warmup):
+    """Triangle multiplication (outgoing and incoming) on z [512,512,128] bf16 ~N(0,1), mask
+    Bernoulli(0.95), six 128x128 weights ~N(0,1/128), biases 0, LayerNorm scales 1 + N(0,0.1)
+    and offsets N(0,0.1); 2 rotating sets. Reports each kernel's time per call and the
+    contraction's TFLOP/s (2*N^3*C flops)."""
+    import ctypes
+    n, c = 512, 128
+    lib = native.lib()
+    g = torch.Generator(device="cpu").manual_seed(80)
+    rnd = lambda *s, std=1.0: (torch.randn(s, generator=g) * std)  # noqa: E731
+    wsb = lib.clk_triangle_multiply_workspace_size(n, c)
+    sets = []
+    for _ in range(2):
+        z = rnd(n, n, c).to(torch.bfloat16).to(dev)
+        mask = (torch.rand((n, n), generator=g) < 0.95).to(torch.bfloat16).to(dev)
+        lns = [(1 + rnd(c, std=0.1)).to(dev), rnd(c, std=0.1).to(dev),
+               (1 + rnd(c, std=0.1)).to(dev), rnd(c, std=0.1).to(dev)]
+        ws = [rnd(c, c, std=c ** -0.5).to(torch.bfloat16).to(dev) for _ in range(6)]
+        bs = [torch.zeros(c, dtype=torch.bfloat16, device=dev) for _ in range(6)]
+        sets.append((z, mask, lns, ws, bs, torch.empty_like(z),
+                     torch.empty(wsb, dtype=torch.uint8, device=dev)))
+    arr = lambda ts: (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])  # noqa: E731
+    out = {}
+    for outgoing, tag in ((1, "tri_out"), (0, "tri_in")):
+        def run(i, outgoing=outgoing):
+            z, mask, lns, ws, bs, o, w = sets[i % len(sets)]
+            st = lib.clk_triangle_multiply(stream, native.BF16, z.data_ptr(), mask.data_ptr(),
+                                           arr(lns), arr(ws), arr(bs), o.data_ptr(),
+                                           w.data_ptr(), wsb, n, c, outgoing, 1e-5)
+            if st != 0:
+                raise RuntimeError(native.last_error())
+        t = timed(torch, run, steps, warmup, torch.cuda.current_stream(dev))
+        k = per_kernel(torch, native, run, steps)
+        out[tag + "_ms"] = t
+        for name, v in k.items():
+            out["%s_%s_ms_per_call" % (tag, name)] = v["avg_ms"] * v["launches_per_step"]
+        ke = k.get("tri_einsum", {}).get("avg_ms")
+        if ke:
+            out[tag + "_einsum_TFLOPs"] = 2.0 * n ** 3 * c / (ke * 1e-3) / 1e12
+    return out
+
+
 def recorded_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summaries."""
     pat = re.compile(r"^traffic_bytes_per_launch\[(\w+)\]:\s*([0-9.eE+]+)\s*$")
@@ -340,6 +382,8 @@ def main(argv=None):
         print("bench: timing the attention output gate", file=sys.stderr, flush=True)
         sec.update(bench_attn_gate(torch, native, dev, stream, args.steps, args.warmup))
         sec["attn_gate_frac_hbm"] = sec["attn_gate_GBps"] / HBM_PEAK
+        print("bench: timing the triangle multiplication", file=sys.stderr, flush=True)
+        sec.update(bench_triangle(torch, native, dev, stream, args.steps, args.warmup))
         result["secondary"] = sec
     if not args.no_cpu_baseline:
         print("bench: timing CPU baseline", file=sys.stderr, flush=True)
