@@ -9,7 +9,8 @@ batch, through the C ABI with preallocated buffers; inputs rotate over 3 sets (~
 256 MB Infinity Cache cannot hold them. Secondary figures: LayerNorm forward/backward and
 LayerNorm + gated dual projection on the 512x512x128 pair representation, and the attention
 output gate of MSA row attention (512 rows x 256 queries, 8 x 32 heads, 256 channels), in HBM
-GB/s; the triangle multiplication (outgoing, incoming) on z [512,512,128] per kernel.
+GB/s; the pair-bias projection LN(z).w -> [4,512,512] in GB/s; the triangle multiplication
+(outgoing, incoming) on z [512,512,128] per kernel.
 
 The roofline block names the kernel with the most time per step, its algorithmic work per launch
 divided by its average duration from per-launch HIP events on the launch stream (the library's
@@ -196,6 +197,29 @@ def bench_ln_gdp(torch, workloads, native, dev, stream, steps, warmup):
             "ln_gdp_TFLOPs": 4 * 2.0 * m * c * n / (t * 1e-3) / 1e12}
 
 
+def bench_pair_bias(torch, workloads, native, dev, stream, steps, warmup):
+    """Pair-bias projection LN(z).w -> [4, 512, 512] on z [512*512, 128] bf16; 4 rotating sets."""
+    m, c, h = 512 * 512, 128, 4
+    lib = native.lib()
+    sets = []
+    for r in range(4):
+        li = workloads.layer_norm_inputs(m, c, torch.bfloat16, seed=7 + r, device=dev)
+        w = (torch.randn((c, h)) / c ** 0.5).to(torch.bfloat16).to(dev)
+        sets.append((li, w, torch.empty((h, m), dtype=torch.bfloat16, device=dev)))
+
+    def run(i):
+        li, w, out = sets[i % len(sets)]
+        st = lib.clk_ln_pair_bias(stream, native.BF16, li["x"].data_ptr(), li["scale"].data_ptr(),
+                                  li["offset"].data_ptr(), w.data_ptr(), out.data_ptr(), m, c, h,
+                                  1e-5)
+        if st != 0:
+            raise RuntimeError(native.last_error())
+
+    t = timed(torch, run, steps, warmup, torch.cuda.current_stream(dev))
+    nbytes = m * c * 2.0 + h * m * 2.0
+    return {"pair_bias_GBps": nbytes / (t * 1e-3) / 1e9, "pair_bias_ms": t}
+
+
 def bench_attn_gate(torch, native, dev, stream, steps, warmup):
     """Attention output gate of MSA row attention: o [512,8,256,32], x [512,256,256] ~N(0,1),
     wg [256,256] ~N(0,1/256), bg = 0, bf16 -> [512,256,256]; rotates 3 sets (600 MB)."""
@@ -379,6 +403,9 @@ def main(argv=None):
         print("bench: timing LayerNorm + gated dual projection", file=sys.stderr, flush=True)
         sec.update(bench_ln_gdp(torch, workloads, native, dev, stream, args.steps, args.warmup))
         sec["ln_gdp_frac_hbm"] = sec["ln_gdp_GBps"] / HBM_PEAK
+        print("bench: timing the pair-bias projection", file=sys.stderr, flush=True)
+        sec.update(bench_pair_bias(torch, workloads, native, dev, stream, args.steps, args.warmup))
+        sec["pair_bias_frac_hbm"] = sec["pair_bias_GBps"] / HBM_PEAK
         print("bench: timing the attention output gate", file=sys.stderr, flush=True)
         sec.update(bench_attn_gate(torch, native, dev, stream, args.steps, args.warmup))
         sec["attn_gate_frac_hbm"] = sec["attn_gate_GBps"] / HBM_PEAK

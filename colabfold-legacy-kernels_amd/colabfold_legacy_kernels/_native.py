@@ -45,6 +45,8 @@ PROTOTYPES = {
                                        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_i64,
                                        c_i64, c_i64, c_f32]),
+    "clk_ln_pair_bias": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                                 c_void_p, c_i64, c_i64, c_i64, c_f32]),
     "clk_attention_gate": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                                    c_void_p, c_i64, c_i64, c_i64, c_i64, c_i64]),
     "clk_triangle_einsum": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_i64,

@@ -268,6 +268,26 @@ def ln_gated_dual_proj(z, ln_scale, ln_offset, branch_a, branch_b, mask, eps=1e-
     return a, b
 
 
+def ln_pair_bias(z, scale, offset, w, eps=1e-5):
+    """LN(z).w transposed to the attention bias layout: z [Sq,Sk,C] (or [M,C]), scale/offset
+    float32 [C], w [C,H] -> [H,Sq,Sk] (or [H,M])."""
+    what = "ln_pair_bias"
+    dev = _require([("z", z), ("scale", scale), ("offset", offset), ("w", w)], what)
+    m, c = _ln_dims(z, scale, what)
+    _shape_check(w.dim() == 2 and w.shape[0] == c and w.dtype == z.dtype, what,
+                 "w must be [C,H] of z's dtype")
+    _shape_check(tuple(offset.shape) == (c,) and offset.dtype == torch.float32, what,
+                 "offset must be float32 [C]")
+    h = w.shape[1]
+    code = _dtype_code(z, (_native.F16, _native.BF16), what)
+    out = torch.empty((h,) + tuple(z.shape[:-1]), device=dev, dtype=z.dtype)
+    with torch.cuda.device(dev):
+        _check(_native.lib().clk_ln_pair_bias(_stream(dev), code, _ptr(z), _ptr(scale),
+                                              _ptr(offset), _ptr(w), _ptr(out), m, c, h,
+                                              float(eps)))
+    return out
+
+
 def attention_gate(o, x, wg, bg):
     """o * sigmoid(x.wg + bg), transposed to the output projection's layout: o [N,H,Sq,D] (the
     attention output), x [N,Sq,C], wg [C,H*D], bg [H*D] -> [N,Sq,H*D]."""

@@ -367,6 +367,129 @@ int bwd_blocks(int64_t M, int rows_per_block) {
     return (int)(b < kMaxBwdBlocks ? b : kMaxBwdBlocks);
 }
 
+// ---------------------------------------------------------------------------------------------
+// Pair-bias projection (AlphaFold's triangle-attention / MSA-row-attention bias, the step before
+// the attention kernels): bias[h, m] = sum_c LN(z)[m, c] * w[c, h], i.e. LN(z).w transposed to
+// [H, M] = [H, Sq, Sk], the layout the attention bias argument takes. One pass over z: the row is
+// normalised in registers as in ln_fwd_kernel, LN's affine folds into the projection
+// ((x^ g + b).w = x^.(diag(g) w) + b.w), each lane forms H partial dot products over its
+// channels, and the LPR lanes of a row reduce them with DPP; lane h < H of the row stores head
+// h. HBM-bound on the read of z (M*C*b_in bytes in, M*H*b_out out).
+// ---------------------------------------------------------------------------------------------
+template <typename TR, int LPR, int NV, int H>
+__global__ __launch_bounds__(kThreads) void ln_bias_kernel(const void* __restrict__ xv,
+                                                           const float* __restrict__ scale,
+                                                           const float* __restrict__ offset,
+                                                           const void* __restrict__ wv,
+                                                           void* __restrict__ biasv, int M,
+                                                           float eps) {
+    using E = typename TR::elem;
+    constexpr int VEC = Vec<TR>::N;
+    constexpr int C = LPR * NV * VEC;
+    constexpr int ROWS = kThreads / LPR;
+    static_assert(H <= LPR, "one storing lane per head");
+    const E* x = static_cast<const E*>(xv);
+    const E* w = static_cast<const E*>(wv);
+    E* bias = static_cast<E*>(biasv);
+    const int s = threadIdx.x % LPR;
+    const int slot = threadIdx.x / LPR;
+
+    // diag(scale) w for this lane's channels, and offset . w reduced over the row's lanes.
+    float wl[NV][VEC][H];
+    float hb[H];
+#pragma unroll
+    for (int h = 0; h < H; ++h) hb[h] = 0.f;
+#pragma unroll
+    for (int v = 0; v < NV; ++v)
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) {
+            const int c = (v * LPR + s) * VEC + i;
+#pragma unroll
+            for (int h = 0; h < H; ++h) {
+                const float wch = TR::to_f(w[c * H + h]);
+                wl[v][i][h] = scale[c] * wch;
+                hb[h] = fmaf(offset[c], wch, hb[h]);
+            }
+        }
+#pragma unroll
+    for (int h = 0; h < H; ++h) hb[h] = row_sum<LPR>(hb[h]);
+
+    for (int row = blockIdx.x * ROWS + slot; row < M; row += gridDim.x * ROWS) {
+        const E* xr = x + (size_t)row * C;
+        float xs[NV][VEC];
+#pragma unroll
+        for (int v = 0; v < NV; ++v) unpack<TR>(ld16(xr + (v * LPR + s) * VEC), xs[v]);
+        float sum = 0.f;
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) sum += xs[v][i];
+        float mean = sum * (1.f / (NV * VEC));
+        float m2 = 0.f;
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) {
+                const float d = xs[v][i] - mean;
+                m2 += d * d;
+            }
+        merge_stats<LPR>(mean, m2, (float)(NV * VEC));
+        const float rstd = rsqrtf(m2 * (1.f / C) + eps);
+        float part[H];
+#pragma unroll
+        for (int h = 0; h < H; ++h) part[h] = 0.f;
+#pragma unroll
+        for (int v = 0; v < NV; ++v)
+#pragma unroll
+            for (int i = 0; i < VEC; ++i) {
+                const float d = xs[v][i] - mean;
+#pragma unroll
+                for (int h = 0; h < H; ++h) part[h] = fmaf(d, wl[v][i][h], part[h]);
+            }
+        float mine = 0.f;
+#pragma unroll
+        for (int h = 0; h < H; ++h) {
+            const float val = fmaf(rstd, row_sum<LPR>(part[h]), hb[h]);
+            if (s == h) mine = val;
+        }
+        if (s < H) bias[(size_t)s * M + row] = TR::from_f(mine);
+    }
+}
+
+template <typename TR, int LPR, int NV, int H>
+void launch_bias(hipStream_t st, const void* x, const float* sc, const float* of, const void* w,
+                 void* bias, int M, float eps) {
+    const int grid = fwd_blocks(M, kThreads / LPR);
+    KernelTimer timer("ln_bias", st);
+    ln_bias_kernel<TR, LPR, NV, H><<<grid, kThreads, 0, st>>>(x, sc, of, w, bias, M, eps);
+}
+
+template <typename TR, int H>
+bool dispatch_bias_h(hipStream_t st, const void* x, const float* sc, const float* of,
+                     const void* w, void* bias, int M, int C, float eps) {
+    const RowShape rs = row_shape(C, Vec<TR>::N);
+#define CLK_LNB_CASE(L, V)                                              \
+    if (rs.lpr == (L) && rs.nv == (V)) {                                \
+        launch_bias<TR, L, V, H>(st, x, sc, of, w, bias, M, eps);       \
+        return true;                                                    \
+    }
+    CLK_LNB_CASE(8, 1) CLK_LNB_CASE(16, 1) CLK_LNB_CASE(32, 1)
+#undef CLK_LNB_CASE
+    return false;
+}
+
+template <typename TR>
+bool dispatch_bias(hipStream_t st, const void* x, const float* sc, const float* of, const void* w,
+                   void* bias, int M, int C, int H, float eps) {
+    switch (H) {
+        case 1: return dispatch_bias_h<TR, 1>(st, x, sc, of, w, bias, M, C, eps);
+        case 2: return dispatch_bias_h<TR, 2>(st, x, sc, of, w, bias, M, C, eps);
+        case 4: return dispatch_bias_h<TR, 4>(st, x, sc, of, w, bias, M, C, eps);
+        case 8: return dispatch_bias_h<TR, 8>(st, x, sc, of, w, bias, M, C, eps);
+        default: return false;
+    }
+}
+
 template <typename TR, int LPR, int NV>
 void launch_fwd(hipStream_t st, const void* x, const float* sc, const float* of, void* y, int M,
                 float eps) {
@@ -515,4 +638,29 @@ extern "C" clk_status clk_layer_norm_bwd(hipStream_t stream, clk_dtype dtype, co
     ln_colsum<<<ceil_div(2 * C, 32), 512, 0, stream>>>(part, stride, nblocks, (int)C, dscale,
                                                            doffset);
     return check_launch("layer_norm_bwd");
+}
+
+extern "C" clk_status clk_ln_pair_bias(hipStream_t stream, clk_dtype dtype, const void* z,
+                                       const float* scale, const float* offset, const void* w,
+                                       void* bias, int64_t M, int64_t C, int64_t H, float eps) {
+    const char* who = "ln_pair_bias";
+    if (dtype != CLK_F16 && dtype != CLK_BF16)
+        return fail(CLK_INVALID_ARGUMENT, "%s: dtype %s not supported (f16, bf16)", who,
+                    dtype_name(dtype));
+    if (M < 0 || M > INT32_MAX || (H != 1 && H != 2 && H != 4 && H != 8))
+        return fail(CLK_INVALID_ARGUMENT, "%s: M=%lld, H=%lld (H must be 1, 2, 4 or 8)", who,
+                    (long long)M, (long long)H);
+    if (C != 64 && C != 128 && C != 256)
+        return fail(CLK_INVALID_ARGUMENT, "%s: C=%lld (64, 128 or 256)", who, (long long)C);
+    if (M == 0) return ok();
+    if (!z || !scale || !offset || !w || !bias)
+        return fail(CLK_INVALID_ARGUMENT, "%s: null operand pointer", who);
+    if (!aligned16(z)) return fail(CLK_INVALID_ARGUMENT, "%s: z must be 16-byte aligned", who);
+    const bool done = dtype == CLK_BF16
+                          ? dispatch_bias<BF16>(stream, z, scale, offset, w, bias, (int)M,
+                                                (int)C, (int)H, eps)
+                          : dispatch_bias<F16>(stream, z, scale, offset, w, bias, (int)M,
+                                               (int)C, (int)H, eps);
+    if (!done) return fail(CLK_INVALID_ARGUMENT, "%s: C=%lld not supported", who, (long long)C);
+    return check_launch(who);
 }

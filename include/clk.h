@@ -138,6 +138,17 @@ clk_status clk_ln_gated_dual_proj(hipStream_t stream, clk_dtype dtype, const voi
                                   int64_t C, int64_t N, float eps);
 
 /*
+ * Pair-bias projection (new; the step before the attention kernels in AlphaFold's triangle and
+ * MSA-row attention): bias[h, m] = sum_c LN(z)[m, c] * w[c, h] for z [M, C] (M = Sq*Sk pair
+ * positions), LN with scale/offset float32 [C] and eps, w [C, H] row-major, bias [H, M] --
+ * the [H, Sq, Sk] attention bias -- in one pass over z. z, w and bias of dtype CLK_F16 or
+ * CLK_BF16; C = 64, 128 or 256; H = 1, 2, 4 or 8.
+ */
+clk_status clk_ln_pair_bias(hipStream_t stream, clk_dtype dtype, const void* z, const float* scale,
+                            const float* offset, const void* w, void* bias, int64_t M, int64_t C,
+                            int64_t H, float eps);
+
+/*
  * Gated attention output (new; the reference leaves the gate to the caller's jnp code):
  *   out[n, s, h*D + d] = o[n, h, s, d] * sigmoid(x[n, s, :] . wg[:, h*D + d] + bg[h*D + d])
  * with o [N,H,Sq,D] the attention output, x [N,Sq,C] the attention's query-side input, wg

@@ -9,11 +9,15 @@ uses a Chan/Welford merge, which tracks the two-pass value.
 Backward (no reference code), with xhat = (x - mu) * r and g = scale * dy:
   dx = r * (g - mean_c(g) - xhat * mean_c(g * xhat)),
   dscale = sum_m dy * xhat, doffset = sum_m dy.
+
+ln_pair_bias (no reference code: AlphaFold's attention bias from the pair representation, the
+step before the reference's attention targets): bias[h, ...] = sum_c LN(z)[..., c] * w[c, h],
+the LN(z).w product with the head axis moved first ([H, Sq, Sk], the attention bias layout).
 """
 
 import numpy as np
 
-__all__ = ["layer_norm_fwd", "layer_norm_bwd"]
+__all__ = ["layer_norm_fwd", "layer_norm_bwd", "ln_pair_bias"]
 
 
 def _stats(x, eps):
@@ -41,3 +45,12 @@ def layer_norm_bwd(x, scale, dy, eps=1e-5):
               - xhat * (g * xhat).mean(axis=-1, keepdims=True))
     red = tuple(range(x.ndim - 1))
     return dx, (dy * xhat).sum(axis=red), dy.sum(axis=red)
+
+
+def ln_pair_bias(z, scale, offset, w, eps=1e-5):
+    """[H, ...] float64 for z [..., C] and w [C, H]."""
+    z = np.asarray(z, np.float64)
+    c = z.shape[-1]
+    y, _, _ = layer_norm_fwd(z.reshape(-1, c), scale, offset, eps)
+    b = y @ np.asarray(w, np.float64)
+    return np.moveaxis(b.reshape(z.shape[:-1] + (b.shape[-1],)), -1, 0)

@@ -76,3 +76,21 @@ def test_layer_norm_rejects_bad_operands(cuda):
     with pytest.raises(ops.InvalidArgument):
         ops.layer_norm(x.to(torch.float64), torch.ones(128, device=cuda),
                        torch.zeros(128, device=cuda))
+
+
+# (Sq, Sk, C, H): triangle attention (4 heads on 128 channels), MSA row attention's pair bias
+# (8 heads), the template stack (64 channels), 256 channels, one head, ragged row counts.
+BIAS_SHAPES = [(64, 64, 128, 4), (37, 53, 128, 8), (40, 40, 64, 4), (9, 11, 256, 2), (3, 5, 128, 1)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=dname)
+@pytest.mark.parametrize("sq,sk,c,h", BIAS_SHAPES)
+def test_ln_pair_bias_parity(cuda, sq, sk, c, h, dtype):
+    g = torch.Generator().manual_seed(sq * sk + c + h)
+    z = (torch.randn((sq, sk, c), generator=g) * 2 + 0.5).to(dtype)
+    sc = 1 + 0.1 * torch.randn(c, generator=g)
+    of = 0.1 * torch.randn(c, generator=g)
+    w = (torch.randn((c, h), generator=g) / c ** 0.5).to(dtype)
+    out = ops.ln_pair_bias(z.to(cuda), sc.to(cuda), of.to(cuda), w.to(cuda))
+    r = ref.ln_pair_bias(np64(z), np64(sc), np64(of), np64(w))
+    assert_close("bias", out, r, TOL[dname(dtype)]["ln"])

@@ -396,3 +396,17 @@ def test_triangle_multiply_matches_torch():
         ref = (x @ T(ws[4]) + T(bs[4])) * torch.sigmoid(y @ T(ws[5]) + T(bs[5]))
         out = TM.triangle_multiply(z, mask, ln_in, ws, bs, ln_c, outgoing)
         np.testing.assert_allclose(out, ref.numpy(), rtol=1e-12, atol=1e-13)
+
+
+def test_ln_pair_bias_matches_torch_and_pair_block():
+    """LN(z).w with the head axis first: an independent torch float64 einsum, and the bias that
+    the pair micro-block composes (evoformer.pair_block_fwd)."""
+    r = np.random.default_rng(6)
+    z = r.standard_normal((5, 7, 16))
+    g, b = 1 + 0.1 * r.standard_normal(16), 0.1 * r.standard_normal(16)
+    w = r.standard_normal((16, 4))
+    out = L.ln_pair_bias(z, g, b, w, 1e-5)
+    y = torch.nn.functional.layer_norm(T(z), (16,), T(g), T(b), 1e-5)
+    np.testing.assert_allclose(out, torch.einsum("qkc,ch->hqk", y, T(w)).numpy(), rtol=1e-12,
+                               atol=1e-13)
+    assert out.shape == (4, 5, 7)
