@@ -9,7 +9,8 @@ batch, through the C ABI with preallocated buffers; inputs rotate over 3 sets (~
 256 MB Infinity Cache cannot hold them. Secondary figures: LayerNorm forward/backward and
 LayerNorm + gated dual projection on the 512x512x128 pair representation, and the attention
 output gate of MSA row attention (512 rows x 256 queries, 8 x 32 heads, 256 channels), in HBM
-GB/s; the pair-bias projection LN(z).w -> [4,512,512] in GB/s; the triangle multiplication
+GB/s; the gated dual projection backward on [512*512, 128] per kernel; the pair-bias projection
+LN(z).w -> [4,512,512] in GB/s; the triangle multiplication
 (outgoing, incoming) on z [512,512,128] per kernel.
 
 The roofline block names the kernel with the most time per step, its algorithmic work per launch
@@ -195,6 +196,39 @@ def bench_ln_gdp(torch, workloads, native, dev, stream, steps, warmup):
     return {"ln_gdp_GBps": nbytes / (t * 1e-3) / 1e9, "ln_gdp_ms": t,
             "ln_gdp_kernel_ms": k.get("ln_gdp", {}).get("avg_ms"), "ln_gdp_bytes": nbytes,
             "ln_gdp_TFLOPs": 4 * 2.0 * m * c * n / (t * 1e-3) / 1e12}
+
+
+def bench_gdp_bwd(torch, workloads, native, dev, stream, steps, warmup):
+    """Gated dual projection backward on x [512*512, 128] bf16, 128x128 weights, dout ~N(0,1);
+    2 rotating sets. Reports the call time and each kernel's."""
+    m, k, n = 512 * 512, 128, 128
+    lib = native.lib()
+    wsb = lib.clk_gated_dual_proj_bwd_workspace_size(m, k, n)
+    sets = []
+    for r in range(2):
+        li = workloads.layer_norm_inputs(m, k, torch.bfloat16, seed=30 + r, device=dev)
+        w = workloads.gdp_weights(k, n, torch.bfloat16, seed=50 + r, device=dev)
+        dout = torch.randn((m, n), device=dev).to(torch.bfloat16)
+        f32 = dict(device=dev, dtype=torch.float32)
+        grads = (torch.empty_like(li["x"]), torch.empty((k, n), **f32), torch.empty(n, **f32),
+                 torch.empty((k, n), **f32), torch.empty(n, **f32))
+        sets.append((li, w, dout, grads, torch.empty(wsb, dtype=torch.uint8, device=dev)))
+
+    def run(i):
+        li, w, dout, gr, ws = sets[i % len(sets)]
+        st = lib.clk_gated_dual_proj_bwd(stream, native.BF16, li["x"].data_ptr(),
+                                         *(t.data_ptr() for t in w), li["mask"].data_ptr(),
+                                         dout.data_ptr(), *(t.data_ptr() for t in gr),
+                                         ws.data_ptr(), wsb, m, k, n, 0)
+        if st != 0:
+            raise RuntimeError(native.last_error())
+
+    t = timed(torch, run, steps, warmup, torch.cuda.current_stream(dev))
+    kt = per_kernel(torch, native, run, steps)
+    out = {"gdp_bwd_ms": t}
+    for name, v in kt.items():
+        out["gdp_bwd_%s_ms" % name.replace("gdp_bwd_", "")] = v["avg_ms"]
+    return out
 
 
 def bench_pair_bias(torch, workloads, native, dev, stream, steps, warmup):
@@ -403,6 +437,8 @@ def main(argv=None):
         print("bench: timing LayerNorm + gated dual projection", file=sys.stderr, flush=True)
         sec.update(bench_ln_gdp(torch, workloads, native, dev, stream, args.steps, args.warmup))
         sec["ln_gdp_frac_hbm"] = sec["ln_gdp_GBps"] / HBM_PEAK
+        print("bench: timing the gated dual projection backward", file=sys.stderr, flush=True)
+        sec.update(bench_gdp_bwd(torch, workloads, native, dev, stream, args.steps, args.warmup))
         print("bench: timing the pair-bias projection", file=sys.stderr, flush=True)
         sec.update(bench_pair_bias(torch, workloads, native, dev, stream, args.steps, args.warmup))
         sec["pair_bias_frac_hbm"] = sec["pair_bias_GBps"] / HBM_PEAK

@@ -41,6 +41,11 @@ PROTOTYPES = {
                                    c_void_p, c_void_p, c_void_p, c_size, c_i64, c_i64, c_f32]),
     "clk_gated_dual_proj": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                                     c_void_p, c_void_p, c_void_p, c_i64, c_i64, c_i64]),
+    "clk_gated_dual_proj_bwd_workspace_size": (c_size, [c_i64, c_i64, c_i64]),
+    "clk_gated_dual_proj_bwd": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                                        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                        c_void_p, c_void_p, c_void_p, c_void_p, c_size, c_i64,
+                                        c_i64, c_i64, c_int]),
     "clk_ln_gated_dual_proj": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                                        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_i64,

@@ -240,6 +240,57 @@ def gated_dual_proj(x, wp, bp, wg, bg, mask):
     return out
 
 
+def gated_dual_proj_bwd(x, wp, bp, wg, bg, mask, dout, dx=None):
+    """Gradients of gated_dual_proj: (dx, dwp, dbp, dwg, dbg); dx in x's dtype, the rest
+    float32. If dx is given, the input gradient is added to it in place (two branches that read
+    the same x)."""
+    what = "gated_dual_proj_bwd"
+    dev = _require([("x", x), ("wp", wp), ("bp", bp), ("wg", wg), ("bg", bg), ("mask", mask),
+                    ("dout", dout), ("dx", dx)], what)
+    _shape_check(x.dim() == 2, what, "x must be [M,K]")
+    m, kdim = x.shape
+    _shape_check(wp.dim() == 2 and wp.shape[0] == kdim, what, "wp must be [K,N]")
+    n = wp.shape[1]
+    _shape_check(tuple(wg.shape) == (kdim, n), what, "wg must be [K,N]")
+    _shape_check(tuple(bp.shape) == (n,) and tuple(bg.shape) == (n,), what, "bp, bg must be [N]")
+    _shape_check(tuple(mask.shape) == (m,), what, "mask must be [M]")
+    _shape_check(tuple(dout.shape) == (m, n), what, "dout must be [M,N]")
+    _shape_check(all(t.dtype == x.dtype for t in (wp, bp, wg, bg, mask, dout)), what,
+                 "all operands must share one dtype")
+    code = _dtype_code(x, (_native.F16, _native.BF16), what)
+    acc = dx is not None
+    if acc:
+        _shape_check(tuple(dx.shape) == (m, kdim) and dx.dtype == x.dtype, what,
+                     "dx must be [M,K] of x's dtype")
+    else:
+        dx = torch.empty_like(x)
+    f32 = dict(device=dev, dtype=torch.float32)
+    dwp, dwg = torch.empty((kdim, n), **f32), torch.empty((kdim, n), **f32)
+    dbp, dbg = torch.empty(n, **f32), torch.empty(n, **f32)
+    lib = _native.lib()
+    wsb = lib.clk_gated_dual_proj_bwd_workspace_size(m, kdim, n)
+    ws = torch.empty(max(wsb, 1), device=dev, dtype=torch.uint8)
+    with torch.cuda.device(dev):
+        _check(lib.clk_gated_dual_proj_bwd(_stream(dev), code, _ptr(x), _ptr(wp), _ptr(bp),
+                                           _ptr(wg), _ptr(bg), _ptr(mask), _ptr(dout), _ptr(dx),
+                                           _ptr(dwp), _ptr(dbp), _ptr(dwg), _ptr(dbg), _ptr(ws),
+                                           wsb, m, kdim, n, 1 if acc else 0))
+    return dx, dwp, dbp, dwg, dbg
+
+
+def ln_gated_dual_proj_bwd(z, ln_scale, ln_offset, branch_a, branch_b, mask, da, db, eps=1e-5):
+    """Gradients of ln_gated_dual_proj: (dz, dln_scale, dln_offset, grads_a, grads_b) with
+    grads_x = (dwp, dbp, dwg, dbg). Recomputes y = LN(z), runs the GDP backward of both branches
+    into one dy, then the LayerNorm backward."""
+    y = layer_norm(z, ln_scale, ln_offset, eps)
+    c = z.shape[-1]
+    y2, m2 = y.reshape(-1, c), mask.reshape(-1)
+    dy, *ga = gated_dual_proj_bwd(y2, *branch_a, m2, da.reshape(y2.shape[0], -1))
+    _, *gb = gated_dual_proj_bwd(y2, *branch_b, m2, db.reshape(y2.shape[0], -1), dx=dy)
+    dz, dsc, dof = layer_norm_bwd(z, ln_scale, dy.reshape(z.shape), eps)
+    return dz, dsc, dof, tuple(ga), tuple(gb)
+
+
 def ln_gated_dual_proj(z, ln_scale, ln_offset, branch_a, branch_b, mask, eps=1e-5):
     """(a, b): LayerNorm(z) then both gated projections, in one pass. Each branch is
     (wp, bp, wg, bg); z [M,C] (or [..., C]); mask [M]."""

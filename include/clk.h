@@ -124,6 +124,22 @@ clk_status clk_gated_dual_proj(hipStream_t stream, clk_dtype dtype, const void* 
                                const void* mask, void* out, int64_t M, int64_t K, int64_t N);
 
 /*
+ * Backward of the gated dual projection (new; the reference is forward-only): for out = mask *
+ * (x.wp + bp) * sigmoid(x.wg + bg) and the incoming gradient dout [M,N], writes dx [M,K] (added
+ * to the existing dx when accumulate_dx != 0, for two branches reading the same x), dwp, dwg
+ * [K,N] and dbp, dbg [N] in float32. x, weights, biases, mask, dout, dx of dtype CLK_F16 or
+ * CLK_BF16. K and N in {64, 128}. Deterministic: the weight and bias gradients are summed from
+ * per-block partials in a fixed order. Workspace: clk_gated_dual_proj_bwd_workspace_size bytes.
+ */
+size_t clk_gated_dual_proj_bwd_workspace_size(int64_t M, int64_t K, int64_t N);
+clk_status clk_gated_dual_proj_bwd(hipStream_t stream, clk_dtype dtype, const void* x,
+                                   const void* wp, const void* bp, const void* wg, const void* bg,
+                                   const void* mask, const void* dout, void* dx, float* dwp,
+                                   float* dbp, float* dwg, float* dbg, void* workspace,
+                                   size_t workspace_bytes, int64_t M, int64_t K, int64_t N,
+                                   int accumulate_dx);
+
+/*
  * LayerNorm fused with both gated-projection branches of the triangle multiplication:
  *   y = LN(z); a = mask*(y.wpa+bpa)*sigmoid(y.wga+bga); b = likewise with the b weights.
  * One pass over z instead of VoltaLayerNorm followed by two VoltaGdp calls. z, weights, biases,

@@ -6,6 +6,11 @@ cuda/volta_gdp_wmma.cu:76-96):
 with wp, wg row-major [K,N], biases [N] and a per-row mask [M]. The bias is added before the
 sigmoid, the row mask multiplies last (volta_ops.cu:201-204).
 
+gated_dual_proj_bwd is the derivative of gated_dual_proj (no reference code; the reference is
+forward-only): with p = x.wp + bp, s = sigmoid(x.wg + bg),
+  dp = dout * mask * s, dg = dout * mask * p * s * (1 - s),
+  dx = dp.wp^T + dg.wg^T, dwp = x^T.dp, dwg = x^T.dg, dbp = sum_m dp, dbg = sum_m dg.
+
 ln_gated_dual_proj is the pair-stack use in ColabFold's triangle multiplication: the two GDP
 branches a and b read the same LayerNorm(z). The reference runs it as one VoltaLayerNorm call and
 two VoltaGdp calls (volta_ops.cu:62-95 then :210-265 twice); here it is their composition.
@@ -15,7 +20,7 @@ import numpy as np
 
 from .layer_norm import layer_norm_fwd
 
-__all__ = ["sigmoid", "gated_dual_proj", "ln_gated_dual_proj"]
+__all__ = ["sigmoid", "gated_dual_proj", "ln_gated_dual_proj", "gated_dual_proj_bwd"]
 
 
 def sigmoid(x):
@@ -37,3 +42,16 @@ def ln_gated_dual_proj(z, ln_scale, ln_offset, eps, branch_a, branch_b, mask):
     a = gated_dual_proj(y, *branch_a, mask)
     b = gated_dual_proj(y, *branch_b, mask)
     return a, b
+
+
+def gated_dual_proj_bwd(x, wp, bp, wg, bg, mask, dout):
+    """(dx [M,K], dwp [K,N], dbp [N], dwg [K,N], dbg [N]) float64."""
+    x = np.asarray(x, np.float64)
+    wp = np.asarray(wp, np.float64)
+    wg = np.asarray(wg, np.float64)
+    p = x @ wp + np.asarray(bp, np.float64)
+    s = sigmoid(x @ wg + np.asarray(bg, np.float64))
+    dm = np.asarray(dout, np.float64) * np.asarray(mask, np.float64)[:, None]
+    dp = dm * s
+    dg = dm * p * s * (1.0 - s)
+    return dp @ wp.T + dg @ wg.T, x.T @ dp, dp.sum(0), x.T @ dg, dg.sum(0)

@@ -137,3 +137,11 @@ def test_attention_gate_validation(n, h, sq, d, c, msg):
     lib = _native.lib()
     assert lib.clk_attention_gate(None, BF16, *([FAKE] * 5), n, h, sq, d, c) == INVALID
     assert msg in _native.last_error()
+
+
+@pytest.mark.parametrize("m,k,n,msg", [(4, 96, 128, "64 or 128"), (4, 128, 32, "64 or 128"),
+                                       (-1, 128, 128, "64 or 128")])
+def test_gdp_bwd_validation(m, k, n, msg):
+    lib = _native.lib()
+    assert lib.clk_gated_dual_proj_bwd(None, BF16, *([FAKE] * 13), 1 << 30, m, k, n, 0) == INVALID
+    assert msg in _native.last_error()

@@ -93,3 +93,73 @@ def test_ln_gdp_full_pair_rep(cuda):
     err = (a.float() - a2.float()).abs().max().item()
     assert err <= 2e-2 * a2.float().abs().max().item()
     _ = np
+
+
+# (M, K, N): the pair stack (128 -> 128), the template stack (64), mixed widths, ragged row
+# counts (not multiples of the 64-row tile), one row.
+GDP_BWD_SHAPES = [(1000, 128, 128), (77, 64, 64), (300, 128, 64), (33, 64, 128), (1, 128, 128),
+                  (4096, 128, 128)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=dname)
+@pytest.mark.parametrize("m,k,n", GDP_BWD_SHAPES)
+def test_gdp_bwd_parity(cuda, m, k, n, dtype):
+    li = layer_norm_inputs(m, k, dtype, seed=m + 3 * k + n)
+    w = gdp_weights(k, n, dtype, seed=n + 1, bias_std=0.3)
+    g = torch.Generator().manual_seed(m)
+    dout = torch.randn((m, n), generator=g).to(dtype)
+    x, mask = li["x"], li["mask"]
+    got = ops.gated_dual_proj_bwd(x.to(cuda), *(t.to(cuda) for t in w), mask.to(cuda),
+                                  dout.to(cuda))
+    r = ref.gated_dual_proj_bwd(np64(x), *(np64(t) for t in w), np64(mask), np64(dout))
+    tol = TOL[dname(dtype)]["grad"]
+    for name, a, b in zip(("dx", "dwp", "dbp", "dwg", "dbg"), got, r):
+        assert_close(name, a, b, tol)
+
+
+def test_gdp_bwd_accumulates_and_repeats(cuda):
+    """dx accumulation (two branches reading one x) and bit-identical repeated runs."""
+    dt = torch.bfloat16
+    m, k, n = 2000, 128, 128
+    li = layer_norm_inputs(m, k, dt, seed=5)
+    wa = [t.to(cuda) for t in gdp_weights(k, n, dt, seed=6, bias_std=0.3)]
+    wb = [t.to(cuda) for t in gdp_weights(k, n, dt, seed=7, bias_std=0.3)]
+    g = torch.Generator().manual_seed(8)
+    da, db = (torch.randn((m, n), generator=g).to(dt).to(cuda) for _ in range(2))
+    x, mask = li["x"].to(cuda), li["mask"].to(cuda)
+    dx, *ga = ops.gated_dual_proj_bwd(x, *wa, mask, da)
+    again = ops.gated_dual_proj_bwd(x, *wa, mask, da)
+    for u, v in zip([dx] + ga, again):
+        assert torch.equal(u, v)
+    dx2 = dx.clone()
+    ops.gated_dual_proj_bwd(x, *wb, mask, db, dx=dx2)
+    ra = ref.gated_dual_proj_bwd(np64(x), *(np64(t) for t in wa), np64(mask), np64(da))
+    rb = ref.gated_dual_proj_bwd(np64(x), *(np64(t) for t in wb), np64(mask), np64(db))
+    assert_close("dx_a+dx_b", dx2, ra[0] + rb[0], TOL["bf16"]["grad"])
+
+
+def test_ln_gdp_bwd_composition(cuda):
+    """LayerNorm + both branches backward (recomputed LN, two GDP backwards into one dy, LN
+    backward) against the float64 composition of the oracle functions."""
+    from oracle import layer_norm as L
+    dt = torch.bfloat16
+    m, c, n = 1500, 128, 128
+    li = layer_norm_inputs(m, c, dt, seed=11)
+    wa = [t.to(cuda) for t in gdp_weights(c, n, dt, seed=12, bias_std=0.3)]
+    wb = [t.to(cuda) for t in gdp_weights(c, n, dt, seed=13, bias_std=0.3)]
+    g = torch.Generator().manual_seed(14)
+    da, db = (torch.randn((m, n), generator=g).to(dt).to(cuda) for _ in range(2))
+    z, sc, of, mask = (li[k].to(cuda) for k in ("x", "scale", "offset", "mask"))
+    dz, dsc, dof, ga, gb = ops.ln_gated_dual_proj_bwd(z, sc, of, wa, wb, mask, da, db)
+    y, _, _ = L.layer_norm_fwd(np64(z), np64(sc), np64(of), 1e-5)
+    ra = ref.gated_dual_proj_bwd(y, *(np64(t) for t in wa), np64(mask), np64(da))
+    rb = ref.gated_dual_proj_bwd(y, *(np64(t) for t in wb), np64(mask), np64(db))
+    rdz, rdsc, rdof = L.layer_norm_bwd(np64(z), np64(sc), ra[0] + rb[0], 1e-5)
+    tol = TOL["bf16"]["grad"]
+    assert_close("dz", dz, rdz, tol)
+    assert_close("dscale", dsc, rdsc, tol)
+    assert_close("doffset", dof, rdof, tol)
+    for name, a, b in zip(("dwpa", "dbpa", "dwga", "dbga"), ga, ra[1:]):
+        assert_close(name, a, b, tol)
+    for name, a, b in zip(("dwpb", "dbpb", "dwgb", "dbgb"), gb, rb[1:]):
+        assert_close(name, a, b, tol)

@@ -410,3 +410,15 @@ def test_ln_pair_bias_matches_torch_and_pair_block():
     np.testing.assert_allclose(out, torch.einsum("qkc,ch->hqk", y, T(w)).numpy(), rtol=1e-12,
                                atol=1e-13)
     assert out.shape == (4, 5, 7)
+
+
+def test_gdp_bwd_matches_torch_autograd():
+    x, wp, bp, wg, bg, mask = gdp_case(8, m=9, k=12, n=7)
+    r = np.random.default_rng(9)
+    dout = r.standard_normal((9, 7))
+    tx, twp, tbp, twg, tbg = (T(a).requires_grad_() for a in (x, wp, bp, wg, bg))
+    out = T(mask)[:, None] * (tx @ twp + tbp) * torch.sigmoid(tx @ twg + tbg)
+    out.backward(T(dout))
+    got = G.gated_dual_proj_bwd(x, wp, bp, wg, bg, mask, dout)
+    for a, b in zip(got, (tx.grad, twp.grad, tbp.grad, twg.grad, tbg.grad)):
+        np.testing.assert_allclose(a, b.numpy(), rtol=1e-12, atol=1e-13)
