@@ -460,7 +460,9 @@ __global__ __launch_bounds__(512) void gdp_bwd_dw_kernel(const typename TR::elem
 }
 
 // dwp, dwg [K][N] and dbp, dbg [N] from nb partials [nb][2N*K + 2N] ([2N][K] then [2N]) and the
-// grad kernel's column sums [ng][2N], added in block order.
+// grad kernel's column sums [ng][2N]. A block owns 64 consecutive outputs: thread (c, s) adds the
+// partials s, s + 16, s + 32, ... of four consecutive outputs (16-byte loads, all in flight), and
+// the 16 subtotals are then added in s order -- a fixed order, so the sums are reproducible.
 template <int K, int N>
 __global__ __launch_bounds__(256) void gdp_bwd_sum_kernel(const float* __restrict__ part, int nb,
                                                           const float* __restrict__ dbpart, int ng,
@@ -468,20 +470,34 @@ __global__ __launch_bounds__(256) void gdp_bwd_sum_kernel(const float* __restric
                                                           float* __restrict__ dwg,
                                                           float* __restrict__ dbp,
                                                           float* __restrict__ dbg) {
-    constexpr int W2 = 2 * N, PS = W2 * K + W2;
-    const int i = blockIdx.x * 256 + threadIdx.x;
-    if (i < W2 * K) {
-        float a = 0.f;
-        for (int b = 0; b < nb; ++b) a += part[(size_t)b * PS + i];
-        const int n = i / K, k = i % K;
-        if (n < N) dwp[k * N + n] = a;
-        else dwg[k * N + (n - N)] = a;
-    } else if (i < W2 * K + W2) {
-        const int n = i - W2 * K;
-        float a = 0.f;
-        for (int b = 0; b < ng; ++b) a += dbpart[(size_t)b * W2 + n];
-        if (n < N) dbp[n] = a;
-        else dbg[n - N] = a;
+    constexpr int W2 = 2 * N, PS = W2 * K + W2, NW = W2 * K;
+    static_assert(NW % 64 == 0 && W2 % 64 == 0 && PS % 4 == 0, "whole 64-output blocks");
+    __shared__ f32x4 sub[16][16];
+    const int c = threadIdx.x % 16, s = threadIdx.x / 16;
+    const int e0 = blockIdx.x * 64;  // first output of the block; [0, NW) weights, then biases
+    const bool weights = e0 < NW;
+    const float* src = weights ? part + e0 + 4 * c : dbpart + (e0 - NW) + 4 * c;
+    const int stride = weights ? PS : W2, count = weights ? nb : ng;
+    f32x4 a = {0.f, 0.f, 0.f, 0.f};
+    for (int b = s; b < count; b += 16) a += *reinterpret_cast<const f32x4*>(src + (size_t)b * stride);
+    sub[s][c] = a;
+    __syncthreads();
+    if (s != 0) return;
+    f32x4 t = sub[0][c];
+#pragma unroll
+    for (int q = 1; q < 16; ++q) t += sub[q][c];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        const int e = e0 + 4 * c + q;
+        if (weights) {
+            const int n = e / K, k = e % K;
+            if (n < N) dwp[k * N + n] = t[q];
+            else dwg[k * N + (n - N)] = t[q];
+        } else {
+            const int n = e - NW;
+            if (n < N) dbp[n] = t[q];
+            else dbg[n - N] = t[q];
+        }
     }
 }
 
@@ -537,7 +553,7 @@ clk_status run_gdp_bwd(hipStream_t st, const void* x, const void* wp, const void
     {
         constexpr int count = 2 * N * K + 2 * N;
         KernelTimer timer("gdp_bwd_sum", st);
-        gdp_bwd_sum_kernel<K, N><<<(count + 255) / 256, 256, 0, st>>>(
+        gdp_bwd_sum_kernel<K, N><<<count / 64, 256, 0, st>>>(
             part, gm.dw_blocks, dbpart, gm.grad_blocks, dwp, dwg, dbp, dbg);
     }
     return check_launch("gated_dual_proj_bwd");

@@ -19,6 +19,13 @@
 //   ClkLnGdp          z, ln_scale, ln_offset, wpa, bpa, wga, bga, wpb, bpb, wgb, bgb, mask
 //                     -> a, b; attribute eps
 //   ClkAttentionGate  o [N,H,Sq,D], x [N,Sq,C], wg [C,H*D], bg [H*D] -> out [N,Sq,H*D]
+//   ClkLnPairBias     z [..., C], scale, offset (f32 [C]), w [C,H] -> bias [H, ...]; attribute eps
+//   ClkGdpBwd         x, wp, bp, wg, bg, mask, dout -> dx, dwp, dbp, dwg, dbg (f32), workspace (u8,
+//                     clk_gated_dual_proj_bwd_workspace_size bytes)
+//   ClkTriangleMultiply  z [N,N,C], mask [N,N], ln_in scale, offset, ln_c scale, offset (f32 [C]),
+//                     six weights [C,C], six biases [C] -> out [N,N,C], workspace (u8,
+//                     clk_triangle_multiply_workspace_size bytes); attributes eps (f32), outgoing
+//                     (i64, 1 = 'ikc,jkc->ijc', 0 = 'kjc,kic->ijc')
 #include <hip/hip_runtime.h>
 
 #include <cstring>
@@ -341,6 +348,105 @@ clk_status attention_gate(const Frame& f) {
                               bg->data, out->data, N, H, Sq, D, C);
 }
 
+clk_status ln_pair_bias(const Frame& f) {
+    const char* who = "ClkLnPairBias";
+    if (f.nargs() != 4 || f.nrets() != 1)
+        return bad(who, "expects 4 operands (z, scale, offset, w) and 1 result");
+    const Buffer *z = f.arg(0), *sc = f.arg(1), *of = f.arg(2), *w = f.arg(3), *out = f.ret(0);
+    if (!z || !sc || !of || !w || !out) return bad(who, "operands must be buffers");
+    if (z->rank < 1) return bad(who, "z must be [..., C]");
+    const int64_t C = z->dims[z->rank - 1], M = C ? numel(z) / C : 0;
+    if (!dims_are(sc, {C}) || !dims_are(of, {C}) || sc->dtype != kF32 || of->dtype != kF32)
+        return bad(who, "scale and offset must be f32 [C]");
+    if (w->rank != 2 || w->dims[0] != C) return bad(who, "w must be [C,H]");
+    const int64_t H = w->dims[1];
+    const DataType t = z->dtype;
+    if (!half_type(t) || w->dtype != t || out->dtype != t) return bad(who, "z, w, out f16 or bf16");
+    if (numel(out) != H * M || out->rank != z->rank || out->dims[0] != H)
+        return bad(who, "out must be [H, ...] over z's leading axes");
+    float eps;
+    if (!f.attr_f32("eps", &eps)) return bad(who, "missing f32 attribute 'eps'");
+    return clk_ln_pair_bias(f.stream(), static_cast<clk_dtype>(t), z->data,
+                            static_cast<const float*>(sc->data), static_cast<const float*>(of->data),
+                            w->data, out->data, M, C, H, eps);
+}
+
+clk_status gdp_bwd(const Frame& f) {
+    const char* who = "ClkGdpBwd";
+    if (f.nargs() != 7 || f.nrets() != 6)
+        return bad(who, "expects 7 operands (x, wp, bp, wg, bg, mask, dout) and 6 results "
+                        "(dx, dwp, dbp, dwg, dbg, workspace)");
+    const Buffer* a[7];
+    for (int i = 0; i < 7; ++i)
+        if (!(a[i] = f.arg(i))) return bad(who, "operands must be buffers");
+    const Buffer* r[6];
+    for (int i = 0; i < 6; ++i)
+        if (!(r[i] = f.ret(i))) return bad(who, "results must be buffers");
+    const Buffer* x = a[0];
+    if (x->rank != 2 || a[1]->rank != 2 || a[1]->dims[0] != x->dims[1])
+        return bad(who, "x [M,K] and wp [K,N] expected");
+    const int64_t M = x->dims[0], K = x->dims[1], N = a[1]->dims[1];
+    const DataType t = x->dtype;
+    if (!half_type(t)) return bad(who, "x must be f16 or bf16");
+    if (!dims_are(a[3], {K, N}) || !dims_are(a[2], {N}) || !dims_are(a[4], {N}) ||
+        !dims_are(a[5], {M}) || !dims_are(a[6], {M, N}) || !dims_are(r[0], {M, K}))
+        return bad(who, "wg [K,N], bp, bg [N], mask [M], dout [M,N], dx [M,K] expected");
+    for (int i = 1; i < 7; ++i)
+        if (a[i]->dtype != t) return bad(who, "all operands must share x's dtype");
+    if (r[0]->dtype != t) return bad(who, "dx must have x's dtype");
+    if (!dims_are(r[1], {K, N}) || !dims_are(r[3], {K, N}) || !dims_are(r[2], {N}) ||
+        !dims_are(r[4], {N}) || r[1]->dtype != kF32 || r[2]->dtype != kF32 ||
+        r[3]->dtype != kF32 || r[4]->dtype != kF32)
+        return bad(who, "dwp, dwg f32 [K,N] and dbp, dbg f32 [N] expected");
+    if (r[5]->dtype != kU8) return bad(who, "sixth result must be the u8 workspace");
+    return clk_gated_dual_proj_bwd(
+        f.stream(), static_cast<clk_dtype>(t), x->data, a[1]->data, a[2]->data, a[3]->data,
+        a[4]->data, a[5]->data, a[6]->data, r[0]->data, static_cast<float*>(r[1]->data),
+        static_cast<float*>(r[2]->data), static_cast<float*>(r[3]->data),
+        static_cast<float*>(r[4]->data), r[5]->data, (size_t)numel(r[5]), M, K, N, 0);
+}
+
+clk_status triangle_multiply(const Frame& f) {
+    const char* who = "ClkTriangleMultiply";
+    if (f.nargs() != 18 || f.nrets() != 2)
+        return bad(who, "expects 18 operands (z, mask, 4 LayerNorm vectors, 6 weights, 6 biases) "
+                        "and 2 results (out, workspace)");
+    const Buffer* z = f.arg(0);
+    const Buffer* mask = f.arg(1);
+    const Buffer *out = f.ret(0), *ws = f.ret(1);
+    if (!z || !mask || !out || !ws) return bad(who, "operands must be buffers");
+    if (z->rank != 3 || z->dims[0] != z->dims[1]) return bad(who, "z must be [N,N,C]");
+    const int64_t N = z->dims[0], C = z->dims[2];
+    const DataType t = z->dtype;
+    if (!half_type(t)) return bad(who, "z must be f16 or bf16");
+    if (!dims_are(mask, {N, N}) || mask->dtype != t) return bad(who, "mask must be [N,N]");
+    if (!dims_are(out, {N, N, C}) || out->dtype != t) return bad(who, "out must be [N,N,C]");
+    if (ws->dtype != kU8) return bad(who, "second result must be the u8 workspace");
+    const float* ln[4];
+    for (int i = 0; i < 4; ++i) {
+        const Buffer* b = f.arg(2 + i);
+        if (!b || !dims_are(b, {C}) || b->dtype != kF32)
+            return bad(who, "LayerNorm scales and offsets must be f32 [C]");
+        ln[i] = static_cast<const float*>(b->data);
+    }
+    const void *w[6], *bb[6];
+    for (int i = 0; i < 6; ++i) {
+        const Buffer *wi = f.arg(6 + i), *bi = f.arg(12 + i);
+        if (!wi || !bi || !dims_are(wi, {C, C}) || !dims_are(bi, {C}) || wi->dtype != t ||
+            bi->dtype != t)
+            return bad(who, "weights must be [C,C] and biases [C] of z's dtype");
+        w[i] = wi->data;
+        bb[i] = bi->data;
+    }
+    float eps;
+    int64_t outgoing;
+    if (!f.attr_f32("eps", &eps)) return bad(who, "missing f32 attribute 'eps'");
+    if (!f.attr_i64("outgoing", &outgoing)) return bad(who, "missing i64 attribute 'outgoing'");
+    return clk_triangle_multiply(f.stream(), static_cast<clk_dtype>(t), z->data, mask->data, ln,
+                                 w, bb, out->data, ws->data, (size_t)numel(ws), N, C,
+                                 outgoing != 0, eps);
+}
+
 }  // namespace
 
 #define CLK_FFI_EXPORT extern "C" __attribute__((visibility("default")))
@@ -374,4 +480,13 @@ CLK_FFI_EXPORT Error* ClkLnGdp(CallFrame* frame) {
 }
 CLK_FFI_EXPORT Error* ClkAttentionGate(CallFrame* frame) {
     return run(frame, [](const Frame& f) { return attention_gate(f); });
+}
+CLK_FFI_EXPORT Error* ClkLnPairBias(CallFrame* frame) {
+    return run(frame, [](const Frame& f) { return ln_pair_bias(f); });
+}
+CLK_FFI_EXPORT Error* ClkGdpBwd(CallFrame* frame) {
+    return run(frame, [](const Frame& f) { return gdp_bwd(f); });
+}
+CLK_FFI_EXPORT Error* ClkTriangleMultiply(CallFrame* frame) {
+    return run(frame, [](const Frame& f) { return triangle_multiply(f); });
 }

@@ -12,7 +12,8 @@ from _xla_ffi import BF16, F16, F32, F64, S32, S64, U8, FakeXla, Metadata, Metad
 pytestmark = pytest.mark.skipif(not clk.available("gfx950"), reason="library not built")
 
 TARGETS = ["VoltaMma", "VoltaWmma", "ClkAttentionFwd", "ClkAttentionBwd", "VoltaLayerNorm",
-           "ClkLayerNormBwd", "VoltaGdp", "VoltaGdpWmma", "ClkLnGdp", "ClkAttentionGate"]
+           "ClkLayerNormBwd", "VoltaGdp", "VoltaGdpWmma", "ClkLnGdp", "ClkAttentionGate",
+           "ClkLnPairBias", "ClkGdpBwd", "ClkTriangleMultiply"]
 FAKE = 0x100000
 
 
@@ -129,3 +130,18 @@ def test_attention_gate_decode_errors(lib):
     fr = x.frame([x.buffer(BF16, (2, 8, 16, 32), FAKE)], [x.buffer(BF16, (2, 16, 256), FAKE)], [])
     assert x.call(lib, "ClkAttentionGate", fr) is not None
     assert "4 operands" in x.errors[-1][1]
+
+
+def test_new_targets_decode_errors(lib):
+    x = FakeXla()
+    fr = x.frame([x.buffer(BF16, (8, 8, 128), FAKE)], [x.buffer(BF16, (8, 8, 128), FAKE)], [])
+    assert x.call(lib, "ClkTriangleMultiply", fr) is not None
+    assert "18 operands" in x.errors[-1][1]
+    fr = x.frame([x.buffer(BF16, (64, 128), FAKE)], [x.buffer(BF16, (64, 128), FAKE)], [])
+    assert x.call(lib, "ClkGdpBwd", fr) is not None
+    assert "7 operands" in x.errors[-1][1]
+    fr = x.frame([x.buffer(BF16, (4, 4, 128), FAKE), x.buffer(F32, (128,), FAKE),
+                  x.buffer(F32, (128,), FAKE), x.buffer(BF16, (128, 4), FAKE)],
+                 [x.buffer(BF16, (4, 4, 4), FAKE)], [])
+    assert x.call(lib, "ClkLnPairBias", fr) is not None
+    assert "eps" in x.errors[-1][1]

@@ -94,3 +94,60 @@ def test_layer_norm_and_gdp_targets(cuda):
                                     li["mask"])
     torch.cuda.synchronize()
     assert torch.equal(a, ra) and torch.equal(b, rb)
+
+
+def test_new_targets_match_the_c_abi(cuda):
+    """ClkAttentionGate, ClkLnPairBias, ClkGdpBwd and ClkTriangleMultiply on device buffers."""
+    lib, x = lib_and_runtime(cuda)
+    g = torch.Generator().manual_seed(21)
+    bf = lambda *s, std=1.0: (torch.randn(s, generator=g) * std).to(torch.bfloat16).to(cuda)  # noqa
+    f32 = lambda *s, base=0.0: (base + 0.1 * torch.randn(s, generator=g)).to(cuda)  # noqa
+
+    o, xin, wgt, bgt = bf(2, 8, 40, 32), bf(2, 40, 256), bf(256, 256, std=1 / 16), bf(256, std=0.3)
+    out = torch.empty((2, 40, 256), dtype=torch.bfloat16, device=cuda)
+    fr = x.frame([buf(x, t) for t in (o, xin, wgt, bgt)], [buf(x, out)])
+    assert x.call(lib, "ClkAttentionGate", fr) is None, x.errors
+    torch.cuda.synchronize()
+    assert torch.equal(out, ops.attention_gate(o, xin, wgt, bgt))
+
+    z, sc, of, w = bf(16, 24, 128), f32(128, base=1.0), f32(128), bf(128, 4, std=1 / 11.3)
+    bias = torch.empty((4, 16, 24), dtype=torch.bfloat16, device=cuda)
+    fr = x.frame([buf(x, t) for t in (z, sc, of, w)], [buf(x, bias)], [("eps", F32, 1e-5)])
+    assert x.call(lib, "ClkLnPairBias", fr) is None, x.errors
+    torch.cuda.synchronize()
+    assert torch.equal(bias, ops.ln_pair_bias(z, sc, of, w))
+
+    li = layer_norm_inputs(300, 128, torch.bfloat16, seed=22, device=cuda)
+    wts = gdp_weights(128, 128, torch.bfloat16, seed=23, device=cuda, bias_std=0.2)
+    dout = bf(300, 128)
+    ws_bytes = lib.clk_gated_dual_proj_bwd_workspace_size
+    ws_bytes.restype = ctypes.c_size_t
+    ws_bytes.argtypes = [ctypes.c_int64] * 3
+    ws = torch.empty(ws_bytes(300, 128, 128), dtype=torch.uint8, device=cuda)
+    rets = [torch.empty_like(li["x"])] + [torch.empty(s, device=cuda)
+                                          for s in ((128, 128), (128,), (128, 128), (128,))]
+    fr = x.frame([buf(x, t) for t in (li["x"],) + tuple(wts) + (li["mask"], dout)],
+                 [buf(x, t) for t in rets] + [buf(x, ws)])
+    assert x.call(lib, "ClkGdpBwd", fr) is None, x.errors
+    ref = ops.gated_dual_proj_bwd(li["x"], *wts, li["mask"], dout)
+    torch.cuda.synchronize()
+    for a, b in zip(rets, ref):
+        assert torch.equal(a, b)
+
+    n, c = 24, 128
+    zt, mask = bf(n, n, c), (torch.rand((n, n), generator=g) > 0.1).to(torch.bfloat16).to(cuda)
+    lns = [f32(c, base=1.0), f32(c), f32(c, base=1.0), f32(c)]
+    ws6 = [bf(c, c, std=c ** -0.5) for _ in range(6)]
+    bs6 = [bf(c, std=0.2) for _ in range(6)]
+    tws = lib.clk_triangle_multiply_workspace_size
+    tws.restype = ctypes.c_size_t
+    tws.argtypes = [ctypes.c_int64] * 2
+    ws = torch.empty(tws(n, c), dtype=torch.uint8, device=cuda)
+    for outgoing in (1, 0):
+        out = torch.empty_like(zt)
+        fr = x.frame([buf(x, t) for t in [zt, mask] + lns + ws6 + bs6], [buf(x, out), buf(x, ws)],
+                     [("eps", F32, 1e-5), ("outgoing", S64, outgoing)])
+        assert x.call(lib, "ClkTriangleMultiply", fr) is None, x.errors
+        ref = ops.triangle_multiply(zt, mask, lns[:2], ws6, bs6, lns[2:], bool(outgoing))
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref)
