@@ -155,29 +155,10 @@ __device__ __forceinline__ void vm_wait() {
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-// Explicit LDS reads for loops whose buffers are chosen at run time. The compiler neither sees
-// these reads nor tracks their completion: the caller waits with lds_wait<N>(dst...), which
-// waits until at most N of the wave's LDS operations are outstanding (LDS reads complete in
-// issue order) and then hands the named registers on, so that their uses stay behind the wait.
+// The LDS address (byte offset in the workgroup's LDS) of a __shared__ pointer, for explicit LDS
+// instructions.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
-}
-template <typename V, int OFF>
-__device__ __forceinline__ V lds_read16(uint32_t addr) {
-    static_assert(sizeof(V) == 16 && OFF >= 0 && OFF < 65536, "16-byte read, 16-bit offset");
-    V v;
-    asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "n"(OFF));
-    return v;
-}
-template <typename T>
-__device__ __forceinline__ void after_wait(T& r) {
-    asm volatile("" : "+v"(r));
-}
-template <int N, typename... T>
-__device__ __forceinline__ void lds_wait(T&... regs) {
-    static_assert(N >= 0 && N < 16, "lgkmcnt holds 4 bits");
-    asm volatile("s_waitcnt lgkmcnt(%0)" ::"n"(N));
-    (after_wait(regs), ...);
 }
 
 // 16-byte buffer store; a store whose offset falls past the resource's range is dropped.

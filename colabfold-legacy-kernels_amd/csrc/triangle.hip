@@ -20,6 +20,33 @@ namespace {
 constexpr int kTriTile = 256;  // output tile edge
 constexpr int kTriK = 32;      // contraction slice per stage
 
+// The twelve 16-byte fragments of one slice (four B rows, eight A rows, 1 KB apart) read from
+// LDS and waited for in one asm statement: the loop picks its stage at run time, and a read the
+// compiler can see would have to wait for every direct-to-LDS load in flight. All outputs are
+// complete when the statement ends, so no register is read before its data has arrived; the
+// "memory" clobber keeps the statement behind the barrier that publishes the stage.
+template <typename V8>
+__device__ __forceinline__ void read_fragments(uint32_t ba, uint32_t bb, V8 (&fb)[4], V8 (&fa)[8]) {
+    asm volatile(
+        "ds_read_b128 %0, %13\n\t"
+        "ds_read_b128 %1, %13 offset:1024\n\t"
+        "ds_read_b128 %2, %13 offset:2048\n\t"
+        "ds_read_b128 %3, %13 offset:3072\n\t"
+        "ds_read_b128 %4, %12\n\t"
+        "ds_read_b128 %5, %12 offset:1024\n\t"
+        "ds_read_b128 %6, %12 offset:2048\n\t"
+        "ds_read_b128 %7, %12 offset:3072\n\t"
+        "ds_read_b128 %8, %12 offset:4096\n\t"
+        "ds_read_b128 %9, %12 offset:5120\n\t"
+        "ds_read_b128 %10, %12 offset:6144\n\t"
+        "ds_read_b128 %11, %12 offset:7168\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(fb[0]), "=&v"(fb[1]), "=&v"(fb[2]), "=&v"(fb[3]), "=&v"(fa[0]), "=&v"(fa[1]),
+          "=&v"(fa[2]), "=&v"(fa[3]), "=&v"(fa[4]), "=&v"(fa[5]), "=&v"(fa[6]), "=&v"(fa[7])
+        : "v"(ba), "v"(bb)
+        : "memory");
+}
+
 // X[c] = A[c] . B[c]^T for A, B, X [C][N][N] row-major. N must be a multiple of 8.
 template <typename TR>
 __global__ __launch_bounds__(512) void tri_einsum_kernel(const typename TR::elem* __restrict__ A,
@@ -91,8 +118,7 @@ __global__ __launch_bounds__(512) void tri_einsum_kernel(const typename TR::elem
     // X^T tile products: the A operand is B (rows j), the B operand is A (rows i), so a lane's
     // accumulator holds four consecutive j of one i. The loop body is not unrolled (copies of it
     // cost the register allocator more than the 256 VGPRs a lane has), so the stage buffers are
-    // picked at run time and the fragment reads are explicit LDS instructions with explicit
-    // waits: the compiler cannot then tie them to the direct-to-LDS loads in flight.
+    // picked at run time and the fragments are read by read_fragments.
     for (int kk = 0; kk < nk; ++kk) {
         const int cur = kk % 3, nxt = (kk + 2) % 3;
         vm_wait<DPW>();
@@ -100,40 +126,12 @@ __global__ __launch_bounds__(512) void tri_einsum_kernel(const typename TR::elem
         stage(kk + 2, smem + nxt * STAGE);
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         const uint32_t ba = lds0 + cur * STAGE + rda, bb = lds0 + cur * STAGE + rdb;
-        V8 fb0 = lds_read16<V8, 0>(bb), fb1 = lds_read16<V8, 1024>(bb);
-        V8 fb2 = lds_read16<V8, 2048>(bb), fb3 = lds_read16<V8, 3072>(bb);
-        V8 fa[8];
-        fa[0] = lds_read16<V8, 0>(ba);
-        fa[1] = lds_read16<V8, 1024>(ba);
-        fa[2] = lds_read16<V8, 2048>(ba);
-        fa[3] = lds_read16<V8, 3072>(ba);
-        fa[4] = lds_read16<V8, 4096>(ba);
-        fa[5] = lds_read16<V8, 5120>(ba);
-        fa[6] = lds_read16<V8, 6144>(ba);
-        fa[7] = lds_read16<V8, 7168>(ba);
-        // LDS reads complete in order: fragment fa[it] is in once at most 7 - it remain.
-        lds_wait<7>(fb0, fb1, fb2, fb3, fa[0]);
-        auto step = [&](int it, const V8& x) {
-            acc[0][it] = TR::mfma(fb0, x, acc[0][it]);
-            acc[1][it] = TR::mfma(fb1, x, acc[1][it]);
-            acc[2][it] = TR::mfma(fb2, x, acc[2][it]);
-            acc[3][it] = TR::mfma(fb3, x, acc[3][it]);
-        };
-        step(0, fa[0]);
-        lds_wait<6>(fa[1]);
-        step(1, fa[1]);
-        lds_wait<5>(fa[2]);
-        step(2, fa[2]);
-        lds_wait<4>(fa[3]);
-        step(3, fa[3]);
-        lds_wait<3>(fa[4]);
-        step(4, fa[4]);
-        lds_wait<2>(fa[5]);
-        step(5, fa[5]);
-        lds_wait<1>(fa[6]);
-        step(6, fa[6]);
-        lds_wait<0>(fa[7]);
-        step(7, fa[7]);
+        V8 fb[4], fa[8];
+        read_fragments(ba, bb, fb, fa);
+#pragma unroll
+        for (int it = 0; it < 8; ++it)
+#pragma unroll
+            for (int jt = 0; jt < 4; ++jt) acc[jt][it] = TR::mfma(fb[jt], fa[it], acc[jt][it]);
     }
 
     // Lane (r16, g) of accumulator (jt, it) holds X[i][j..j+3] for i = i0 + 128wi + 16it + r16,
