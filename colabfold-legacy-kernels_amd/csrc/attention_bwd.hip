@@ -399,13 +399,6 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv(
 // launch whose operands all arrive by direct global->LDS loads into static double buffers.
 // ---------------------------------------------------------------------------------------------
 
-// True when some byte of the eight is zero (an absent key).
-__device__ __forceinline__ bool has_zero_byte(u32x2 w) {
-    const unsigned a = (w[0] - 0x01010101u) & ~w[0] & 0x80808080u;
-    const unsigned b = (w[1] - 0x01010101u) & ~w[1] & 0x80808080u;
-    return (a | b) != 0u;
-}
-
 // Bit j set when byte j of the eight is nonzero.
 __device__ __forceinline__ unsigned nonzero_bits8(u32x2 w) {
     unsigned bits = 0;

@@ -23,6 +23,13 @@ struct AttnGeom {
 // Row of the 16-row operand tile t (0..3) of a 64-row tile that lane row r16 supplies. Inside
 // each 32-row chunk c = t/2 the rows are permuted so that the C tile of the product holds rows
 // 32c + 8*(l/16) + 0..7 in lane l: half t%2 covers +0..3, the other +4..7.
+// True when some byte of the eight is zero (an absent key).
+__device__ __forceinline__ bool has_zero_byte(u32x2 w) {
+    const unsigned a = (w[0] - 0x01010101u) & ~w[0] & 0x80808080u;
+    const unsigned b = (w[1] - 0x01010101u) & ~w[1] & 0x80808080u;
+    return (a | b) != 0u;
+}
+
 __device__ __forceinline__ int perm_key(int t, int r16) {
     return 32 * (t >> 1) + 8 * (r16 >> 2) + 4 * (t & 1) + (r16 & 3);
 }

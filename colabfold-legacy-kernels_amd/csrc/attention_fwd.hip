@@ -28,25 +28,47 @@
 namespace clk {
 namespace {
 
-// Per-tile "some key absent or past Sk" flags of one mask row, for up to kMaxFlagTiles tiles of
-// 64 keys (beyond that every tile takes the checked path). Also returns the row's masked logit.
-constexpr int kMaxFlagTiles = 128;
-
-__device__ __forceinline__ float tile_flags(const uint8_t* mrow, int Sk, int* flags) {
+// Per-tile "some key absent or past Sk" flags of one mask row, as bits of a 64-bit word (tiles of
+// 64 keys; tiles past the 64th always take the checked path), worked out by each wave on its
+// own with ballots -- no LDS and no block barrier. Also returns the row's masked logit.
+struct RowFlags {
+    uint64_t bits;
+    float masked_logit;
+};
+template <bool VEC>
+__device__ __forceinline__ RowFlags row_flags(const uint8_t* mrow, int Sk) {
+    const int lane = threadIdx.x & 63;
     const int ntiles = (Sk + 63) / 64;
-    for (int t = threadIdx.x; t < kMaxFlagTiles; t += blockDim.x)
-        flags[t] = (t >= ntiles || 64 * (t + 1) > Sk) ? 1 : 0;
-    __syncthreads();
-    int any = 0;
+    uint64_t bits = Sk % 64 ? 1ull << (ntiles - 1) : 0ull;  // the ragged last tile
+    bool any_present = false;
     if (mrow) {
-        for (int i = threadIdx.x; i < Sk; i += blockDim.x) {
-            const bool present = mrow[i] != 0;
-            any |= present;
-            if (!present && i / 64 < kMaxFlagTiles) flags[i / 64] = 1;
+        for (int base = 0; base < Sk; base += 512) {
+            const int k = base + 8 * lane;
+            bool absent = false, present = false;
+            if constexpr (VEC) {
+                // Sk % 8 == 0 and 8-byte aligned rows: whole 8-key groups.
+                if (k < Sk) {
+                    const u32x2 m = *reinterpret_cast<const u32x2*>(mrow + k);
+                    present = (m[0] | m[1]) != 0u;
+                    absent = has_zero_byte(m);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+                    if (k + j < Sk) {
+                        const bool p = mrow[k + j] != 0;
+                        present |= p;
+                        absent |= !p;
+                    }
+            }
+            const uint64_t ab = __ballot(absent);
+            any_present |= __ballot(present) != 0ull;
+#pragma unroll
+            for (int t = 0; t < 8; ++t)
+                if (base / 64 + t < 64 && ((ab >> (8 * t)) & 0xffull)) bits |= 1ull << (base / 64 + t);
         }
     }
-    any = __syncthreads_or(any);
-    return (mrow && !any) ? 0.f : kMaskedLogit;
+    return {bits, (mrow && !any_present) ? 0.f : kMaskedLogit};
 }
 
 // Per-lane prefetch state of one key tile: the mask bytes of keys k0 + 32c + 8g + 0..7 (c = 0, 1)
@@ -114,7 +136,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
     // wait for the direct-to-LDS loads into the other.
     __shared__ __attribute__((aligned(16))) char kv0[2 * TILE + BTILE];  // K rows, V rows, bias
     __shared__ __attribute__((aligned(16))) char kv1[2 * TILE + BTILE];
-    __shared__ int flags[kMaxFlagTiles];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r16 = lane & 15, g = lane >> 4;
@@ -153,7 +174,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
         }
     };
     if (ntiles > 0) stage(0, kv0);
-    const float masked_logit = tile_flags(mp, Sk, flags);
 
     // B operand Q^T: lane (query r16, group g) holds head dims 32*ks + 8*g + 0..7.
     V8 qf[QT][G::KS];
@@ -175,6 +195,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
     for (int qt = 0; qt < QT; ++qt) brow[qt] = bp + (size_t)min(qbase + qt * 16 + r16, Sq - 1) * Sk;
     PF ca, cb;
     if (ntiles > 0) ca.load(brow, mp, 0, g, Sk);
+    // The mask row's tile flags, with the Q and first-tile loads already in flight.
+    const RowFlags rf = row_flags<VEC>(mp, Sk);
+    const float masked_logit = rf.masked_logit;
 
     // Running max, and O^T plus one extra accumulator per sub-tile: the MFMA of an all-ones
     // A operand with P^T, i.e. the row sum of the (rounded) P that the P.V product uses.
@@ -195,7 +218,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
         const int k0 = kt * BK;
         async_wait();
         __syncthreads();  // tile kt visible; every wave is done with the other buffer
-        const bool need_mask = kt >= kMaxFlagTiles || flags[kt] != 0;
+        const bool need_mask = kt >= 64 || ((rf.bits >> kt) & 1ull) != 0ull;
         if (kt + 1 < ntiles) {
             stage(k0 + BK, kvn);
             nxt.load(brow, mp, k0 + BK, g, Sk);
