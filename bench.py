@@ -22,7 +22,8 @@ rocprofv3 FETCH_SIZE/WRITE_SIZE summaries in profiles/*hbm_traffic*.md (lines
 scale each counter by what it reads for a plain device copy of known size, which
 "--copy-calibration MIB" performs (and nothing else).
 cpu_baseline times the same math in torch float32 on the host cores (oracle/cpu_baseline.py) on
-a bounded sample of rows, scaled to the same unit.
+all 384 rows by default (--cpu-rows for fewer), repeated for about --cpu-seconds (10 s) and
+reported as the median run in the same unit.
 """
 
 import argparse
@@ -373,7 +374,7 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-rows", type=int, default=64)
+    ap.add_argument("--cpu-rows", type=int, default=N_ROWS)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
