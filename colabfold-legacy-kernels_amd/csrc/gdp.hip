@@ -144,18 +144,25 @@ __global__ __launch_bounds__(256) void gdp_kernel(const typename TR::elem* __res
 }
 
 // ---------------------------------------------------------------------------------------------
-// LayerNorm + both gated branches (the two inputs of the triangle multiplication). Wave w of the
-// N/16 waves owns the 32 output columns 32*cb + 0..31 (cb = w % (N/32)) of branch w / (N/32) and
-// holds the matching columns of that branch's projection and gate weights as MFMA A operands in
-// registers for the whole kernel, with the LN affine folded in:
+// LayerNorm + both gated branches (the two inputs of the triangle multiplication). A block has
+// two kinds of waves. MFMA wave w of the N/16 owns the 32 output columns 32*cb + 0..31
+// (cb = w % (N/32)) of branch w / (N/32) and holds the matching columns of that branch's
+// projection and gate weights as MFMA A operands in registers for the whole kernel, with the LN
+// affine folded in:
 //   (xhat*gamma + beta).W + b = xhat.(diag(gamma) W) + (beta.W + b),
-// the folded biases being the accumulators' starting values. The block walks 64-row tiles of z:
-// the rows arrive by direct buffer->LDS loads two tiles ahead, one LayerNorm pass writes xhat (in
-// the input type) into a swizzled LDS tile, and every wave reads it as the B operand of
-// out^T = W^T . xhat^T. A-tile row r of column half h stands for output column
-// 32cb + 8*(r/4) + 4h + r%4, so a lane's accumulators hold 8 consecutive output columns of one
-// row and the epilogue (bias, sigmoid gate, row mask) ends in one 16-byte store per lane and
-// 16-row sub-tile. HBM traffic is one read of z and the mask and one write of a and b.
+// the folded biases being the accumulators' starting values. Four LayerNorm waves stage 64-row
+// tiles of z by direct buffer->LDS loads two tiles ahead and write xhat (in the input type) into
+// a swizzled LDS tile. In step j the LayerNorm waves normalise tile j while the MFMA waves read
+// tile j-1 as the B operand of out^T = W^T . xhat^T; one barrier per step. A-tile row r of column
+// half h stands for output column 32cb + 8*(r/4) + 4h + r%4, so a lane's accumulators hold 8
+// consecutive output columns of one row and the epilogue (bias, sigmoid gate, row mask) ends in
+// one 16-byte store per lane and 16-row sub-tile. HBM traffic is one read of z and the mask and
+// one write of a and b.
+//
+// The row statistics follow volta_ops.cu:40-52: one pass of sum and sum of squares in fp32,
+// var = max(sum_sq/C - mean^2, 0). With bf16/f16 inputs the pair products are exact in fp32, so
+// this loses accuracy only for rows whose mean is large against their spread (|mean|/std beyond
+// about 10^3).
 // ---------------------------------------------------------------------------------------------
 
 // Weights and biases of the two branches, passed by value: w = {wpa, wga, wpb, wgb}, same for b.
@@ -175,121 +182,191 @@ struct LnGdpGeom {
     static constexpr int LPR = PL <= 4 ? 4 : PL <= 8 ? 8 : 16;
 };
 
+// N 16-byte LDS reads at addr + i * STRIDE and the wait for them, as one asm statement.
+template <int N, int STRIDE>
+__device__ __forceinline__ void lds_rows(uint32_t addr, u32x4 (&r)[N]) {
+    static_assert((N == 1 || N == 2 || N == 4) && (N - 1) * STRIDE < 65536, "ds offset field");
+    if constexpr (N == 1) {
+        asm volatile("ds_read_b128 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(r[0]) : "v"(addr)
+                     : "memory");
+    } else if constexpr (N == 2) {
+        asm volatile(
+            "ds_read_b128 %0, %2\n\tds_read_b128 %1, %2 offset:%3\n\ts_waitcnt lgkmcnt(0)"
+            : "=&v"(r[0]), "=&v"(r[1])
+            : "v"(addr), "i"(STRIDE)
+            : "memory");
+    } else {
+        asm volatile(
+            "ds_read_b128 %0, %4\n\tds_read_b128 %1, %4 offset:%5\n\t"
+            "ds_read_b128 %2, %4 offset:%6\n\tds_read_b128 %3, %4 offset:%7\n\t"
+            "s_waitcnt lgkmcnt(0)"
+            : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3])
+            : "v"(addr), "i"(STRIDE), "i"(2 * STRIDE), "i"(3 * STRIDE)
+            : "memory");
+    }
+}
+
+// a.x * b.x + a.y * b.y + c for two packed 16-bit pairs, in fp32.
+template <typename TR>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    if constexpr (std::is_same_v<typename TR::elem, __bf16>) {
+        typedef __bf16 p2 __attribute__((ext_vector_type(2)));
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(p2, a), __builtin_bit_cast(p2, b),
+                                               c, false);
+    } else {
+        typedef _Float16 p2 __attribute__((ext_vector_type(2)));
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(p2, a), __builtin_bit_cast(p2, b), c,
+                                      false);
+    }
+}
+
 // CM = false: a and b are [M, N] row-major (the pair layout). CM = true: a and b are channel-
 // major [N, M] (a[n][m]), the operand layout of the triangle-multiplication contraction; the MFMA
 // operands swap roles (out = xhat . W') so that a lane's accumulators hold four consecutive rows
 // of one output column, stored as one 8-byte piece of that column's plane. CM needs M % 64 == 0.
+// Block: N/16 MFMA waves, then 4 LayerNorm waves.
 template <typename TR, int C, int N, bool CM>
-__global__ __launch_bounds__(4 * N) void ln_gdp_kernel(
+__global__ __launch_bounds__(4 * N + 256) void ln_gdp_kernel(
     const typename TR::elem* __restrict__ z, const float* __restrict__ gamma,
     const float* __restrict__ beta, LnGdpWeights<typename TR::elem> wb,
     const typename TR::elem* __restrict__ mask, typename TR::elem* __restrict__ outa,
     typename TR::elem* __restrict__ outb, int M, float eps) {
     using E = typename TR::elem;
     using V8 = typename TR::vec8;
-    constexpr int NW = N / 16, NT = 64 * NW;
+    constexpr int NWM = N / 16;          // MFMA waves
+    constexpr int NTL = 256;             // LayerNorm threads (4 waves)
     constexpr int KS = C / 32;
     constexpr int R = kLnGdpRows, SUB = R / 16;
     constexpr int PL = C / 8;
     using GM = LnGdpGeom<PL>;
-    constexpr int LPR = GM::LPR, RPP = NT / LPR, PASSES = (R + RPP - 1) / RPP;
+    constexpr int LPR = GM::LPR, RPP = NTL / LPR, PASSES = (R + RPP - 1) / RPP;
     constexpr int ZB = R * C * 2;
-    constexpr int DPW = (R * PL + NT - 1) / NT;  // 16-byte loads per lane and tile
-    constexpr int ZBP = DPW * NT * 16;
+    constexpr int DPW = (R * PL + NTL - 1) / NTL;  // 16-byte loads per LayerNorm lane and tile
+    constexpr int ZBP = DPW * NTL * 16;
 
-    // Three z tiles (the one being normalised and the next two in flight), each padded to whole
-    // rounds of the block's 16-byte loads, and the normalised tile.
+    // Three z tiles (normalised, landing, in flight), two normalised tiles and their row masks.
     __shared__ __attribute__((aligned(16))) char z0[ZBP];
     __shared__ __attribute__((aligned(16))) char z1[ZBP];
     __shared__ __attribute__((aligned(16))) char z2[ZBP];
-    __shared__ __attribute__((aligned(16))) char xh[ZB];
-    __shared__ float mk[R];
+    __shared__ __attribute__((aligned(16))) char xh0[ZB];
+    __shared__ __attribute__((aligned(16))) char xh1[ZB];
+    __shared__ float mk0[R];
+    __shared__ float mk1[R];
 
     const int tid = threadIdx.x, lane = tid & 63;
-    // Wave-uniform by construction; readfirstlane lets the compiler keep it (and the output
-    // resources derived from it) in scalar registers.
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r16 = lane & 15, g = lane >> 4;
+    const bool mfma_wave = wave < NWM;
     const int br = wave / (N / 32), cb = wave % (N / 32);
     E* const out = br == 0 ? outa : outb;
 
-    // Resident A operands W'^T and the folded biases.
+    // MFMA waves: resident A operands W'^T and the folded biases.
     V8 wa[2][2][KS];
     f32x4 binit[2][2];
+    if (mfma_wave) {
 #pragma unroll
-    for (int mat = 0; mat < 2; ++mat) {
-        const E* W = wb.w[2 * br + mat];
-        // The gate is carried as -log2(e) * (its pre-activation), the argument of exp2 in the
-        // sigmoid: the scale rides on the folded weights and bias instead of one multiply per
-        // output.
-        const float fold = mat == 1 ? -kLog2e : 1.f;
+        for (int mat = 0; mat < 2; ++mat) {
+            const E* W = wb.w[2 * br + mat];
+            const float fold = mat == 1 ? -kLog2e : 1.f;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const int col = 32 * cb + 8 * (r16 >> 2) + 4 * h + (r16 & 3);
-            float part = 0.f;
+            for (int h = 0; h < 2; ++h) {
+                const int col = 32 * cb + 8 * (r16 >> 2) + 4 * h + (r16 & 3);
+                float part = 0.f;
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks)
+                for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int k = 32 * ks + 8 * g + j;
-                    const float v = TR::to_f(W[(size_t)k * N + col]);
-                    wa[mat][h][ks][j] = TR::from_f(gamma[k] * v * fold);
-                    part = fmaf(beta[k], v, part);
+                    for (int j = 0; j < 8; ++j) {
+                        const int k = 32 * ks + 8 * g + j;
+                        const float v = TR::to_f(W[(size_t)k * N + col]);
+                        wa[mat][h][ks][j] = TR::from_f(gamma[k] * v * fold);
+                        part = fmaf(beta[k], v, part);
+                    }
+                const float bcol = (xgroup_sum(part) + TR::to_f(wb.b[2 * br + mat][col])) * fold;
+                if constexpr (CM) {
+                    binit[mat][h] = f32x4{bcol, bcol, bcol, bcol};
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) binit[mat][h][i] = __shfl(bcol, 4 * g + i);
                 }
-            // The four lane groups hold disjoint k-slots of the same column.
-            const float bcol = (xgroup_sum(part) + TR::to_f(wb.b[2 * br + mat][col])) * fold;
-            if constexpr (CM) {
-                // The column is the lane's own (B operand column r16); all four rows share it.
-                binit[mat][h] = f32x4{bcol, bcol, bcol, bcol};
-            } else {
-                // C lane (r16, g) needs the columns 32cb + 8g + 4h + i, held by lanes
-                // r16' = 4g + i.
-#pragma unroll
-                for (int i = 0; i < 4; ++i) binit[mat][h][i] = __shfl(bcol, 4 * g + i);
             }
         }
     }
 
+    const int G = gridDim.x;
     const int ntiles = (M + R - 1) / R;
-    // Every tile issues the same vector memory operations in every wave, whatever its position:
-    // DPW direct-to-LDS loads (pieces past the tile read zeros into the padding of the buffer),
-    // PASSES mask loads (rows clamped into [0, M)) and SUB stores (rows past M fall outside the
-    // store resource and are dropped); tiles past the end load from an empty resource. The wait
-    // for a tile's rows can then count the operations issued after them.
-    auto stage = [&](int t, char* zb) {
-        const int rows = t < ntiles ? min(R, M - t * R) : 0;
+    const int mine = (ntiles - (int)blockIdx.x + G - 1) / G;  // tiles of this block, in turn
+    auto tile_of = [&](int j) { return (int)blockIdx.x + j * G; };
+
+    // ---- LayerNorm waves: stage z, normalise into xh, row mask into mk ----
+    const int lt = tid - NWM * 64, lw = wave - NWM;
+    const int lr = lt % LPR;
+    auto stage = [&](int j, char* zb) {
+        const int t = tile_of(j);
+        const int rows = j < mine ? min(R, M - t * R) : 0;
         const Rsrc rz = buffer_rsrc(rows > 0 ? z + (size_t)t * R * C : z, (uint32_t)rows * C * 2);
 #pragma unroll
         for (int k = 0; k < DPW; ++k) {
-            const int b = wave * 64 + k * NT;
+            const int b = lw * 64 + k * NTL;
             buf_dma16(rz, (b + lane) * 16, 0, zb + b * 16);
         }
     };
-    const int lr = tid % LPR;
-    // Raw mask values of the rows this thread normalises. Converted when used: converting here
-    // would wait for the tile's direct-to-LDS loads as well.
-    auto load_mask = [&](int t, uint32_t (&mv)[PASSES]) {
+    auto load_mask = [&](int j, uint32_t (&mv)[PASSES]) {
         const uint16_t* m16 = reinterpret_cast<const uint16_t*>(mask);
+        const int t = tile_of(j);
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
-            const int64_t r = (int64_t)t * R + p * RPP + tid / LPR;
+            const int64_t r = (int64_t)t * R + p * RPP + lt / LPR;
             mv[p] = m16[r < M ? r : M - 1];
         }
     };
-    auto out_rsrc = [&](int t) {
-        const int rows = t < ntiles ? min(R, M - t * R) : 0;
-        return buffer_rsrc(rows > 0 ? out + (size_t)t * R * N : out, (uint32_t)rows * N * 2);
+    auto normalise = [&](const char* zc, char* xh, float* mrow, const uint32_t (&mc)[PASSES]) {
+        // The whole tile slice in one asm statement with its wait: the compiler sees no LDS load
+        // here, so it adds no wait for the direct-to-LDS loads still in flight into other buffers.
+        u32x4 raw[PASSES];
+        lds_rows<PASSES, RPP * C * 2>(lds_addr(zc + (lt / LPR) * C * 2 + (lr < PL ? lr : 0) * 16),
+                                      raw);
+#pragma unroll
+        for (int p = 0; p < PASSES; ++p) {
+            const int row = p * RPP + lt / LPR;
+            // Sum and sum of squares in one pass, as pair dot products on the packed inputs.
+            constexpr uint32_t kOnes =
+                std::is_same_v<E, __bf16> ? 0x3F803F80u : 0x3C003C00u;  // (1, 1)
+            float sum = 0.f, sq = 0.f;
+            if (lr < PL) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    sum = dot2<TR>(raw[p][q], kOnes, sum);
+                    sq = dot2<TR>(raw[p][q], raw[p][q], sq);
+                }
+            }
+            sum = group_sum<LPR>(sum);
+            sq = group_sum<LPR>(sq);
+            const float mean = sum * (1.f / C);
+            const float var = fmaxf(fmaf(sq, 1.f / C, -mean * mean), 0.f);
+            const float rstd = __builtin_amdgcn_rsqf(var + eps);
+            const float shift = -mean * rstd;
+            if (lr < PL) {
+                float v[8], x[8];
+                unpack8<TR>(raw[p], v);
+#pragma unroll
+                for (int q = 0; q < 8; ++q) x[q] = fmaf(v[q], rstd, shift);
+                *reinterpret_cast<u32x4*>(xh + row * PL * 16 + 16 * (lr ^ (row & GM::SWZ))) =
+                    pack8<TR>(x);
+            }
+            if (lr == 0) mrow[row] = TR::to_f(__builtin_bit_cast(E, (uint16_t)mc[p]));
+        }
     };
 
-    // Outputs of the previous tile, stored after the next barrier: the barrier then never waits
-    // for fresh stores. Row-major: one 16-byte piece per sub-tile (8 columns of one row).
-    // Channel-major: one 8-byte piece per sub-tile and column half (4 rows of one column).
-    constexpr int NST = CM ? 2 * SUB : SUB;  // stores per lane and tile
+    // ---- MFMA waves: the gated projections of a normalised tile, stores one step later ----
     u32x4 pend[SUB] = {};
     u32x2 pendc[SUB][2] = {};
-    Rsrc pend_out = out_rsrc(ntiles);  // empty: the first flush stores nothing
+    Rsrc pend_out = buffer_rsrc(out, 0);
     int pend_row = 0;
     const Rsrc plane_out = buffer_rsrc(out, CM ? (uint32_t)((size_t)M * N * 2) : 0u);
+    auto out_rsrc = [&](int t) {
+        const int rows = min(R, M - t * R);
+        return buffer_rsrc(out + (size_t)t * R * N, (uint32_t)rows * N * 2);
+    };
     auto flush = [&]() {
         if constexpr (CM) {
 #pragma unroll
@@ -307,61 +384,7 @@ __global__ __launch_bounds__(4 * N) void ln_gdp_kernel(
                 buf_st16(pend_out, ((16 * sub + r16) * N + 32 * cb + 8 * g) * 2, 0, pend[sub]);
         }
     };
-
-    // Tile t is read from zc; tile t + 2*gridDim.x goes into zn, which held tile t - gridDim.x.
-    // Issued after zc's loads: at least the SUB stores and the DPW loads of the tile before.
-    auto tile = [&](int t, const char* zc, char* zn, const uint32_t (&mc)[PASSES],
-                    uint32_t (&mn)[PASSES]) {
-        vm_wait<NST + DPW>();
-        lds_barrier();  // z tile t in zc; every wave is done with xh and mk of the last tile
-        flush();
-        // LayerNorm: LPR lanes per row, 8 channels each; xhat into the swizzled tile.
-#pragma unroll
-        for (int p = 0; p < PASSES; ++p) {
-            const int row = p * RPP + tid / LPR;
-            if (row >= R) break;  // whole LPR groups: the lane exchanges stay within active lanes
-            float v[8];
-            float sum = 0.f;
-            if (lr < PL) {
-                unpack8<TR>(*reinterpret_cast<const u32x4*>(zc + row * C * 2 + lr * 16), v);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) sum += v[j];
-            }
-            sum = group_sum<LPR>(sum);
-            const float mean = sum * (1.f / C);
-            float m2 = 0.f;
-            if (lr < PL) {
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float d = v[j] - mean;
-                    m2 = fmaf(d, d, m2);
-                }
-            }
-            m2 = group_sum<LPR>(m2);
-            const float rstd = rsqrtf(m2 * (1.f / C) + eps);
-            if (lr < PL) {
-                float x[8];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) x[j] = (v[j] - mean) * rstd;
-                *reinterpret_cast<u32x4*>(xh + row * PL * 16 + 16 * (lr ^ (row & GM::SWZ))) =
-                    pack8<TR>(x);
-            }
-            if (lr == 0) mk[row] = TR::to_f(__builtin_bit_cast(E, (uint16_t)mc[p]));
-        }
-        lds_barrier();  // xhat and the row mask of tile t ready; zn is free (read before it)
-        // Tile loads go out after the barrier (an LDS read behind a barrier would otherwise wait
-        // for them), the mask loads first so that they never sit between a tile's loads and the
-        // wait that counts them.
-        const int tn = t + 2 * gridDim.x;
-        load_mask(tn, mn);
-        stage(tn, zn);
-        if constexpr (CM) {
-            pend_out = plane_out;
-            pend_row = t * R;
-        } else {
-            pend_out = out_rsrc(t);
-        }
-
+    auto project = [&](int t, const char* xh, const float* mrow) {
 #pragma unroll
         for (int sub = 0; sub < SUB; ++sub) {
             const int xrow = 16 * sub + r16;
@@ -382,52 +405,79 @@ __global__ __launch_bounds__(4 * N) void ln_gdp_kernel(
                                          : TR::mfma(wa[mat][h][ks], xb, acc[mat][h]);
             }
             if constexpr (CM) {
-                // Lane (r16, g) holds rows 16sub + 4g + i of its column in each half h.
 #pragma unroll
                 for (int h = 0; h < 2; ++h) {
                     E e[4];
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
-                        e[i] = TR::from_f(mk[16 * sub + 4 * g + i] * acc[0][h][i] *
+                        e[i] = TR::from_f(mrow[16 * sub + 4 * g + i] * acc[0][h][i] *
                                           fast_rcp(1.f + fast_exp2(acc[1][h][i])));
                     __builtin_memcpy(&pendc[sub][h], e, 8);
                 }
             } else {
-                const float m = mk[xrow];
+                const float m = mrow[xrow];
                 float o[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const int h = j >> 2, i = j & 3;
-                    o[j] = m * acc[0][h][i] * fast_rcp(1.f + fast_exp2(acc[1][h][i]));
+                for (int q = 0; q < 8; ++q) {
+                    const int h = q >> 2, i = q & 3;
+                    o[q] = m * acc[0][h][i] * fast_rcp(1.f + fast_exp2(acc[1][h][i]));
                 }
                 pend[sub] = pack8<TR>(o);
             }
         }
+        if constexpr (CM) {
+            pend_out = plane_out;
+            pend_row = t * R;
+        } else {
+            pend_out = out_rsrc(t);
+        }
     };
 
-    uint32_t ma[PASSES], mb[PASSES], mc[PASSES];
-    const int G = gridDim.x;
-    int t = blockIdx.x;
-    // Prologue: two tiles in flight, with a store batch (of nothing) between them so that the
-    // first wait counts as every later one does.
-    load_mask(t, ma);
-    stage(t, z0);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    flush();
-    load_mask(t + G, mb);
-    stage(t + G, z1);
-    // The first two tiles' mask values are in registers before the loop starts (the compiler may
-    // sink their loads below the tile loads; the loop must not inherit a wait on those).
-#pragma unroll
-    for (int p = 0; p < PASSES; ++p) asm volatile("" ::"v"(ma[p]), "v"(mb[p]));
-    for (; t < ntiles; t += 3 * G) {
-        tile(t, z0, z2, ma, mc);
-        if (t + G >= ntiles) break;
-        tile(t + G, z1, z0, mb, ma);
-        if (t + 2 * G >= ntiles) break;
-        tile(t + 2 * G, z2, z1, mc, mb);
+    // Step j: the LayerNorm waves normalise tile j (and start loading tile j + 2) while the MFMA
+    // waves project tile j - 1; one barrier per step. The two roles run separate loops with the
+    // same number of barriers, so neither holds the other's registers.
+    if (mfma_wave) {
+        auto mstep = [&](int j, const char* xr, const float* mr) {
+            lds_barrier();
+            flush();
+            if (j >= 1) project(tile_of(j - 1), xr, mr);
+        };
+        for (int j = 0; j <= mine; j += 2) {
+            mstep(j, xh1, mk1);
+            if (j + 1 > mine) break;
+            mstep(j + 1, xh0, mk0);
+        }
+        flush();
+    } else {
+        uint32_t ma[PASSES], mb[PASSES];
+        load_mask(0, ma);
+        stage(0, z0);
+        __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        stage(1, z1);
+        auto lstep = [&](int j, const char* zc, char* zn, char* xw, float* mw,
+                         uint32_t (&mc)[PASSES], uint32_t (&mn)[PASSES]) {
+            vm_wait<DPW>();  // this wave's part of tile j, loaded two steps ago
+            lds_barrier();
+            if (j < mine) {
+                load_mask(j + 1, mn);  // before the tile loads: waiting for it never waits for them
+                stage(j + 2, zn);
+                normalise(zc, xw, mw, mc);
+            }
+        };
+        for (int j = 0; j <= mine; j += 6) {
+            lstep(j, z0, z2, xh0, mk0, ma, mb);
+            if (j + 1 > mine) break;
+            lstep(j + 1, z1, z0, xh1, mk1, mb, ma);
+            if (j + 2 > mine) break;
+            lstep(j + 2, z2, z1, xh0, mk0, ma, mb);
+            if (j + 3 > mine) break;
+            lstep(j + 3, z0, z2, xh1, mk1, mb, ma);
+            if (j + 4 > mine) break;
+            lstep(j + 4, z1, z0, xh0, mk0, ma, mb);
+            if (j + 5 > mine) break;
+            lstep(j + 5, z2, z1, xh1, mk1, mb, ma);
+        }
     }
-    flush();
     async_wait();  // no direct-to-LDS load may still be in flight when the workgroup ends
 }
 
@@ -480,13 +530,13 @@ clk_status launch_ln_gdp(hipStream_t st, const void* z, const float* gamma, cons
                          const LnGdpWeights<typename TR::elem>& wb, const void* mask, void* a,
                          void* b, int M, float eps) {
     using E = typename TR::elem;
-    // One 8-wave block per CU at N = 128 (registers allow two waves per SIMD); narrower N runs
-    // more, smaller blocks per CU.
+    // One 12-wave block per CU at N = C = 128 (its five 16 KB LDS tiles take half the CU's LDS,
+    // its registers three waves per SIMD); narrower N runs more, smaller blocks per CU.
     const int ntiles = (M + kLnGdpRows - 1) / kLnGdpRows;
     const int per_cu = 128 / N;
     const int grid = ntiles < 256 * per_cu ? ntiles : 256 * per_cu;
     KernelTimer timer("ln_gdp", st);
-    ln_gdp_kernel<TR, C, N, CM><<<grid, 4 * N, 0, st>>>((const E*)z, gamma, beta, wb,
+    ln_gdp_kernel<TR, C, N, CM><<<grid, 4 * N + 256, 0, st>>>((const E*)z, gamma, beta, wb,
                                                      (const E*)mask, (E*)a, (E*)b, M, eps);
     return check_launch("ln_gated_dual_proj");
 }

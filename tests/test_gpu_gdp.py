@@ -72,6 +72,33 @@ def test_ln_gdp_parity(cuda, m, c, n, dtype):
     assert_close("b", b, rb, tol)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=dname)
+def test_ln_gdp_offset_and_constant_rows(cuda, dtype):
+    """Rows whose mean is large against their spread (|mean|/std up to 50) and constant rows
+    (variance 0, so LN(z) = beta): the one-pass sum / sum-of-squares statistics stay within the
+    same tolerance as the two-pass oracle."""
+    m, c = 192, 128
+    li = layer_norm_inputs(m, c, dtype, seed=5)
+    g = torch.Generator().manual_seed(6)
+    z = li["x"].float()
+    mean = torch.empty(m).uniform_(-100.0, 100.0, generator=g)
+    std = torch.empty(m).uniform_(2.0, 4.0, generator=g)
+    z = mean[:, None] + std[:, None] * z
+    z[::7] = mean[::7, None]  # constant rows
+    z = z.to(dtype)
+    wa = gdp_weights(c, c, dtype, seed=13, bias_std=0.2)
+    wb = gdp_weights(c, c, dtype, seed=14, bias_std=0.2)
+    dev = lambda ts: tuple(t.to(cuda) for t in ts)  # noqa: E731
+    a, b = ops.ln_gated_dual_proj(z.to(cuda), li["scale"].to(cuda), li["offset"].to(cuda),
+                                  dev(wa), dev(wb), li["mask"].to(cuda), 1e-5)
+    ra, rb = ref.ln_gated_dual_proj(np64(z), np64(li["scale"]), np64(li["offset"]), 1e-5,
+                                    tuple(np64(t) for t in wa), tuple(np64(t) for t in wb),
+                                    np64(li["mask"]))
+    tol = TOL[dname(dtype)]["gdp"]
+    assert_close("a", a, ra, tol)
+    assert_close("b", b, rb, tol)
+
+
 def test_ln_gdp_full_pair_rep(cuda):
     """The 512x512x128 pair representation with a 5% padding mask: sampled rows against the
     oracle, masked rows exactly zero, and agreement with LayerNorm followed by two GDP calls."""
