@@ -252,7 +252,9 @@ def bench_pair_bias(torch, workloads, native, dev, stream, steps, warmup):
 
     t = timed(torch, run, steps, warmup, torch.cuda.current_stream(dev))
     nbytes = m * c * 2.0 + h * m * 2.0
-    return {"pair_bias_GBps": nbytes / (t * 1e-3) / 1e9, "pair_bias_ms": t}
+    k = per_kernel(torch, native, run, steps)
+    return {"pair_bias_GBps": nbytes / (t * 1e-3) / 1e9, "pair_bias_ms": t,
+            "pair_bias_kernel_ms": k.get("ln_bias", {}).get("avg_ms")}
 
 
 def bench_attn_gate(torch, native, dev, stream, steps, warmup):

@@ -119,6 +119,24 @@ __device__ __forceinline__ u32x4 pack8(const float* v) {
     return raw;
 }
 
+// a.x * b.x + a.y * b.y + c for two packed 16-bit pairs, in fp32.
+template <typename TR>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+    if constexpr (std::is_same_v<typename TR::elem, __bf16>) {
+        typedef __bf16 p2 __attribute__((ext_vector_type(2)));
+        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(p2, a), __builtin_bit_cast(p2, b),
+                                               c, false);
+    } else {
+        typedef _Float16 p2 __attribute__((ext_vector_type(2)));
+        return __builtin_amdgcn_fdot2(__builtin_bit_cast(p2, a), __builtin_bit_cast(p2, b), c,
+                                      false);
+    }
+}
+
+// The pair (1, 1) in the 2-byte element type: dot2 with it sums a packed pair.
+template <typename TR>
+constexpr uint32_t kOnePair = std::is_same_v<typename TR::elem, __bf16> ? 0x3F803F80u : 0x3C003C00u;
+
 // Raw buffer resource over `bytes` bytes at `base` (stride 0). Buffer loads check the whole
 // offset (VGPR offset + SGPR offset) against `bytes` and return zeros past it, so tiles that run
 // off the end of a slice need no per-lane selects, and the per-lane offsets stay the same from

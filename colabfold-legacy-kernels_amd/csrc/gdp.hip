@@ -206,20 +206,6 @@ __device__ __forceinline__ void lds_rows(uint32_t addr, u32x4 (&r)[N]) {
     }
 }
 
-// a.x * b.x + a.y * b.y + c for two packed 16-bit pairs, in fp32.
-template <typename TR>
-__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
-    if constexpr (std::is_same_v<typename TR::elem, __bf16>) {
-        typedef __bf16 p2 __attribute__((ext_vector_type(2)));
-        return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(p2, a), __builtin_bit_cast(p2, b),
-                                               c, false);
-    } else {
-        typedef _Float16 p2 __attribute__((ext_vector_type(2)));
-        return __builtin_amdgcn_fdot2(__builtin_bit_cast(p2, a), __builtin_bit_cast(p2, b), c,
-                                      false);
-    }
-}
-
 // CM = false: a and b are [M, N] row-major (the pair layout). CM = true: a and b are channel-
 // major [N, M] (a[n][m]), the operand layout of the triangle-multiplication contraction; the MFMA
 // operands swap roles (out = xhat . W') so that a lane's accumulators hold four consecutive rows
@@ -329,13 +315,11 @@ __global__ __launch_bounds__(4 * N + 256) void ln_gdp_kernel(
         for (int p = 0; p < PASSES; ++p) {
             const int row = p * RPP + lt / LPR;
             // Sum and sum of squares in one pass, as pair dot products on the packed inputs.
-            constexpr uint32_t kOnes =
-                std::is_same_v<E, __bf16> ? 0x3F803F80u : 0x3C003C00u;  // (1, 1)
             float sum = 0.f, sq = 0.f;
             if (lr < PL) {
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    sum = dot2<TR>(raw[p][q], kOnes, sum);
+                    sum = dot2<TR>(raw[p][q], kOnePair<TR>, sum);
                     sq = dot2<TR>(raw[p][q], raw[p][q], sq);
                 }
             }

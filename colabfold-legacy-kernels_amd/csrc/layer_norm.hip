@@ -370,11 +370,14 @@ int bwd_blocks(int64_t M, int rows_per_block) {
 // ---------------------------------------------------------------------------------------------
 // Pair-bias projection (AlphaFold's triangle-attention / MSA-row-attention bias, the step before
 // the attention kernels): bias[h, m] = sum_c LN(z)[m, c] * w[c, h], i.e. LN(z).w transposed to
-// [H, M] = [H, Sq, Sk], the layout the attention bias argument takes. One pass over z: the row is
-// normalised in registers as in ln_fwd_kernel, LN's affine folds into the projection
-// ((x^ g + b).w = x^.(diag(g) w) + b.w), each lane forms H partial dot products over its
-// channels, and the LPR lanes of a row reduce them with DPP; lane h < H of the row stores head
-// h. HBM-bound on the read of z (M*C*b_in bytes in, M*H*b_out out).
+// [H, M] = [H, Sq, Sk], the layout the attention bias argument takes. One pass over z, with LN
+// folded into the projection:
+//   LN(z).w = rstd * (z.w' - mean * sum_c w'[c]) + offset.w,   w' = diag(scale) w,
+// so a row needs only its raw values: the sum and sum of squares (one pass, as the reference's
+// LayerNorm, volta_ops.cu:40-52) and the H dot products z.w' are pair dot products (v_dot2) on
+// the packed 16-bit inputs, with w' rounded to the input type like the MFMA operands of the fused
+// LN + GDP. The LPR lanes of a row reduce them with DPP; lane h < H of the row stores head h.
+// HBM-bound on the read of z (M*C*b_in bytes in, M*H*b_out out).
 // ---------------------------------------------------------------------------------------------
 template <typename TR, int LPR, int NV, int H>
 __global__ __launch_bounds__(kThreads) void ln_bias_kernel(const void* __restrict__ xv,
@@ -385,6 +388,7 @@ __global__ __launch_bounds__(kThreads) void ln_bias_kernel(const void* __restric
                                                            float eps) {
     using E = typename TR::elem;
     constexpr int VEC = Vec<TR>::N;
+    static_assert(VEC == 8, "16-bit inputs: four pairs per 16-byte vector");
     constexpr int C = LPR * NV * VEC;
     constexpr int ROWS = kThreads / LPR;
     static_assert(H <= LPR, "one storing lane per head");
@@ -394,72 +398,94 @@ __global__ __launch_bounds__(kThreads) void ln_bias_kernel(const void* __restric
     const int s = threadIdx.x % LPR;
     const int slot = threadIdx.x / LPR;
 
-    // diag(scale) w for this lane's channels, and offset . w reduced over the row's lanes.
-    float wl[NV][VEC][H];
-    float hb[H];
+    // w' for this lane's channels as packed pairs, its column sums and offset . w, both reduced
+    // over the row's lanes (the column sums from the rounded w' the dot products use).
+    uint32_t wp[NV][4][H];
+    float csum[H], hb[H];
 #pragma unroll
-    for (int h = 0; h < H; ++h) hb[h] = 0.f;
+    for (int h = 0; h < H; ++h) csum[h] = hb[h] = 0.f;
 #pragma unroll
     for (int v = 0; v < NV; ++v)
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) {
-            const int c = (v * LPR + s) * VEC + i;
+        for (int q = 0; q < 4; ++q)
 #pragma unroll
             for (int h = 0; h < H; ++h) {
-                const float wch = TR::to_f(w[c * H + h]);
-                wl[v][i][h] = scale[c] * wch;
-                hb[h] = fmaf(offset[c], wch, hb[h]);
-            }
-        }
+                E pr[2];
 #pragma unroll
-    for (int h = 0; h < H; ++h) hb[h] = row_sum<LPR>(hb[h]);
+                for (int e = 0; e < 2; ++e) {
+                    const int c = (v * LPR + s) * VEC + 2 * q + e;
+                    const float wch = TR::to_f(w[c * H + h]);
+                    pr[e] = TR::from_f(scale[c] * wch);
+                    csum[h] += TR::to_f(pr[e]);
+                    hb[h] = fmaf(offset[c], wch, hb[h]);
+                }
+                __builtin_memcpy(&wp[v][q][h], pr, 4);
+            }
+#pragma unroll
+    for (int h = 0; h < H; ++h) {
+        csum[h] = row_sum<LPR>(csum[h]);
+        hb[h] = row_sum<LPR>(hb[h]);
+    }
 
-    for (int row = blockIdx.x * ROWS + slot; row < M; row += gridDim.x * ROWS) {
-        const E* xr = x + (size_t)row * C;
-        float xs[NV][VEC];
+    // A row group takes RPI consecutive rows per iteration: RPI loads in flight per lane, and
+    // lane h stores head h of those rows as one RPI*2-byte piece.
+    constexpr int RPI = 4;
+    const int64_t stride = (int64_t)gridDim.x * ROWS * RPI;
+    for (int64_t r0 = ((int64_t)blockIdx.x * ROWS + slot) * RPI; r0 < M; r0 += stride) {
+        u32x4 raw[RPI][NV];
 #pragma unroll
-        for (int v = 0; v < NV; ++v) unpack<TR>(ld16(xr + (v * LPR + s) * VEC), xs[v]);
-        float sum = 0.f;
+        for (int r = 0; r < RPI; ++r)
 #pragma unroll
-        for (int v = 0; v < NV; ++v)
+            for (int v = 0; v < NV; ++v)
+                raw[r][v] = r0 + r < M ? ld16(x + (r0 + r) * C + (v * LPR + s) * VEC) : u32x4{};
+        E out[RPI];
 #pragma unroll
-            for (int i = 0; i < VEC; ++i) sum += xs[v][i];
-        float mean = sum * (1.f / (NV * VEC));
-        float m2 = 0.f;
+        for (int r = 0; r < RPI; ++r) {
+            float sum = 0.f, sq = 0.f, d[H];
 #pragma unroll
-        for (int v = 0; v < NV; ++v)
+            for (int h = 0; h < H; ++h) d[h] = 0.f;
 #pragma unroll
-            for (int i = 0; i < VEC; ++i) {
-                const float d = xs[v][i] - mean;
-                m2 += d * d;
+            for (int v = 0; v < NV; ++v)
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    sum = dot2<TR>(raw[r][v][q], kOnePair<TR>, sum);
+                    sq = dot2<TR>(raw[r][v][q], raw[r][v][q], sq);
+#pragma unroll
+                    for (int h = 0; h < H; ++h) d[h] = dot2<TR>(raw[r][v][q], wp[v][q][h], d[h]);
+                }
+            const float mean = row_sum<LPR>(sum) * (1.f / C);
+            const float var = fmaxf(fmaf(row_sum<LPR>(sq), 1.f / C, -mean * mean), 0.f);
+            const float rstd = __builtin_amdgcn_rsqf(var + eps);
+            float mine = 0.f;
+#pragma unroll
+            for (int h = 0; h < H; ++h) {
+                const float val = fmaf(rstd, fmaf(-mean, csum[h], row_sum<LPR>(d[h])), hb[h]);
+                if (s == h) mine = val;
             }
-        merge_stats<LPR>(mean, m2, (float)(NV * VEC));
-        const float rstd = rsqrtf(m2 * (1.f / C) + eps);
-        float part[H];
-#pragma unroll
-        for (int h = 0; h < H; ++h) part[h] = 0.f;
-#pragma unroll
-        for (int v = 0; v < NV; ++v)
-#pragma unroll
-            for (int i = 0; i < VEC; ++i) {
-                const float d = xs[v][i] - mean;
-#pragma unroll
-                for (int h = 0; h < H; ++h) part[h] = fmaf(d, wl[v][i][h], part[h]);
-            }
-        float mine = 0.f;
-#pragma unroll
-        for (int h = 0; h < H; ++h) {
-            const float val = fmaf(rstd, row_sum<LPR>(part[h]), hb[h]);
-            if (s == h) mine = val;
+            out[r] = TR::from_f(mine);
         }
-        if (s < H) bias[(size_t)s * M + row] = TR::from_f(mine);
+        if (s < H) {
+            E* dst = bias + (size_t)s * M + r0;
+            if (r0 + RPI <= M && (M % RPI) == 0 && (reinterpret_cast<uintptr_t>(bias) & 7) == 0) {
+                uint64_t piece;
+                __builtin_memcpy(&piece, out, 8);
+                *reinterpret_cast<uint64_t*>(dst) = piece;
+            } else {
+#pragma unroll
+                for (int r = 0; r < RPI; ++r)
+                    if (r0 + r < M) dst[r] = out[r];
+            }
+        }
     }
 }
 
 template <typename TR, int LPR, int NV, int H>
 void launch_bias(hipStream_t st, const void* x, const float* sc, const float* of, const void* w,
                  void* bias, int M, float eps) {
-    const int grid = fwd_blocks(M, kThreads / LPR);
+    // Four rows per row group and iteration; 1024 blocks (four per CU) measured faster than
+    // one block per row group (each wave then prepares w' for only four rows).
+    const int64_t groups = ((int64_t)M + 3) / 4, per = kThreads / LPR;
+    const int grid = (int)std::min<int64_t>((groups + per - 1) / per, 1024);
     KernelTimer timer("ln_bias", st);
     ln_bias_kernel<TR, LPR, NV, H><<<grid, kThreads, 0, st>>>(x, sc, of, w, bias, M, eps);
 }
