@@ -306,13 +306,14 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_generic(const void* __restric
 }
 
 // out[which][c] = sum over the partial rows b of part[b*stride + which*C + c], in a fixed order:
-// 16 row groups (b = sp, sp+16, ...) each summed with eight interleaved accumulators so eight
-// loads are in flight, then the groups are added in order. Columns are spread over many blocks
-// (32 columns per block).
-__global__ __launch_bounds__(512) void ln_colsum(const float* __restrict__ part, size_t stride,
-                                                 int nblocks, int C, float* __restrict__ dscale,
-                                                 float* __restrict__ doffset) {
-    constexpr int kCols = 32, kSplit = 16, kAcc = 8;
+// 64 row groups (b = sp, sp+64, ...) each summed with sixteen interleaved accumulators, so that a
+// thousand partial rows are one round of loads in flight per thread, then the groups are added
+// in order. 16 columns per 1024-thread block.
+constexpr int kColsumCols = 16;
+__global__ __launch_bounds__(1024) void ln_colsum(const float* __restrict__ part, size_t stride,
+                                                  int nblocks, int C, float* __restrict__ dscale,
+                                                  float* __restrict__ doffset) {
+    constexpr int kCols = kColsumCols, kSplit = 64, kAcc = 16;
     __shared__ float red[kSplit][kCols];
     const int cl = threadIdx.x % kCols, sp = threadIdx.x / kCols;
     const int t = blockIdx.x * kCols + cl;  // over 2*C outputs
@@ -639,8 +640,8 @@ extern "C" clk_status clk_layer_norm_bwd(hipStream_t stream, clk_dtype dtype, co
     if (M == 0) {
         if (!dscale || !doffset) return fail(CLK_INVALID_ARGUMENT, "layer_norm_bwd: null pointer");
         // No rows: the column sums are zero (a fill kernel, so the call stays graph-capturable).
-        ln_colsum<<<ceil_div(2 * C, 32), 512, 0, stream>>>(nullptr, 0, 0, (int)C, dscale,
-                                                               doffset);
+        ln_colsum<<<ceil_div(2 * C, kColsumCols), 1024, 0, stream>>>(nullptr, 0, 0, (int)C,
+                                                                     dscale, doffset);
         return check_launch("layer_norm_bwd");
     }
     float* part = static_cast<float*>(workspace);
@@ -661,8 +662,8 @@ extern "C" clk_status clk_layer_norm_bwd(hipStream_t stream, clk_dtype dtype, co
             break;
     }
     KernelTimer timer("ln_bwd_colsum", stream);
-    ln_colsum<<<ceil_div(2 * C, 32), 512, 0, stream>>>(part, stride, nblocks, (int)C, dscale,
-                                                           doffset);
+    ln_colsum<<<ceil_div(2 * C, kColsumCols), 1024, 0, stream>>>(part, stride, nblocks, (int)C,
+                                                                 dscale, doffset);
     return check_launch("layer_norm_bwd");
 }
 
