@@ -16,8 +16,10 @@
 //
 // Numerics (volta_mma_attn.cu:137,174-272): logit = scale*(q.k) + bias in float32; a key with
 // kmask == 0 gets the logit -1e9 (the float32 value of the caller's additive 1e9*(mask-1)), a
-// key past Sk gets -inf; online softmax in the exp2 domain; P rounded to the input type for the
-// P.V product (as the reference rounds it to f16, :221); O = acc / max(l, 1e-30) (:265).
+// key past Sk gets -inf; online softmax in the exp2 domain, whose running max moves only when a
+// tile's max exceeds it by more than 2^8 in P (so P <= 256, and O and l are rescaled on few
+// tiles); P rounded to the input type for the P.V product (as the reference rounds it to f16,
+// :221: the relative rounding is the same at any magnitude); O = acc / max(l, 1e-30) (:265).
 // A row whose keys are all masked gets the logit 0 for them instead: its softmax is the same
 // (uniform over the Sk keys), but float32 cannot subtract a running max of -1e9 exactly (its
 // rounding unit there is 128), which would scale P by up to 2^64.
@@ -27,6 +29,8 @@
 
 namespace clk {
 namespace {
+
+constexpr float kRescaleSlack = 8.f;  // log2 of the largest P before the running max moves
 
 // Per-tile "some key absent or past Sk" flags of one mask row, as bits of a 64-bit word (tiles of
 // 64 keys; tiles past the 64th always take the checked path), worked out by each wave on its
@@ -292,24 +296,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
 #pragma unroll
                 for (int j = 0; j < 8; ++j) mt = fmaxf(mt, x[qt][c][j]);
             mt = xgroup_max(mt);
-            const float m_new = fmaxf(m_run[qt], mt);
-            const float alpha = fast_exp2((m_run[qt] - m_new) * kLog2e);
-            const float neg = -m_new * kLog2e;
+            // Lazy rescaling: the running max moves only when the tile's max exceeds it by more
+            // than kRescaleSlack (in log2 units), so P stays below 2^kRescaleSlack and most tiles
+            // skip the rescale of O and l (a wave-uniform branch).
+            const bool move = mt * kLog2e > m_run[qt] * kLog2e + kRescaleSlack;
+            if (__any(move)) {
+                const float m_new = move ? mt : m_run[qt];
+                const float alpha = fast_exp2((m_run[qt] - m_new) * kLog2e);
+                m_run[qt] = m_new;
+                lsum[qt][0] *= alpha;  // only component 0 is read
+#pragma unroll
+                for (int dt = 0; dt < G::DT; ++dt) acc[qt][dt] *= alpha;
+            }
+            const float neg = -m_run[qt] * kLog2e;
             V8 pf[2];
 #pragma unroll
             for (int c = 0; c < 2; ++c)
 #pragma unroll
                 for (int j = 0; j < 8; ++j) pf[c][j] = TR::from_f(fast_exp2(fmaf(x[qt][c][j], kLog2e, neg)));
-            m_run[qt] = m_new;
-            lsum[qt][0] *= alpha;  // only component 0 is read
 #pragma unroll
             for (int c = 0; c < 2; ++c) lsum[qt] = TR::mfma(ones, pf[c], lsum[qt]);
 #pragma unroll
-            for (int dt = 0; dt < G::DT; ++dt) {
-                acc[qt][dt] *= alpha;
+            for (int dt = 0; dt < G::DT; ++dt)
 #pragma unroll
                 for (int c = 0; c < 2; ++c) acc[qt][dt] = TR::mfma(vf[dt][c], pf[c], acc[qt][dt]);
-            }
         }
     };
     for (int kt = 0; kt < ntiles; kt += 2) {

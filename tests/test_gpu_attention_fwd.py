@@ -70,6 +70,25 @@ def test_attention_fwd_fully_masked_row_is_mean_v(cuda):
     assert_close("O[masked]", out[1], mean_v, TOL["bf16"]["o"])
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=dname)
+@pytest.mark.parametrize("slope", [0.02, 0.06, 0.3, -0.3])
+def test_attention_fwd_rising_and_falling_logits(cuda, slope, dtype):
+    """Bias ramps along the keys, so a row's running max rises tile after tile by less than,
+    about, or more than the forward's rescale slack (2^8 in P: 5.5 logit units; a 64-key tile
+    rises by 64*slope), or falls (slope < 0: the first tile holds the max). O and the
+    logsumexp against the oracle."""
+    n, h, sq, sk, d = 2, 2, 70, 320, 32
+    inp = attention_inputs(n, h, sq, sk, d, dtype, seed=13, bias_var=0.25, masked_tail=0.05,
+                           with_dout=False)
+    ramp = slope * torch.arange(sk, dtype=torch.float32)
+    inp["bias"] = (inp["bias"].float() + ramp).to(dtype)
+    g = {k: (v.to(cuda) if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    out, lse = ops.attention_fwd(g["q"], g["k"], g["v"], g["bias"], g["kmask"], g["scale"])
+    o_ref, lse_ref = _oracle(inp)
+    assert_close("O", out, o_ref, TOL[dname(dtype)]["o"])
+    assert np.abs(np64(lse) - lse_ref).max() < 5e-2
+
+
 @pytest.mark.parametrize("block", [(64, 64), (64, 32), (32, 32), (128, 64), (32, 64), (16, 64),
                                    (128, 32), (7, 5)])
 def test_attention_fwd_accepts_reference_block_hints(cuda, block):
