@@ -1027,18 +1027,16 @@ BwdPlan plan_bwd(int64_t N, int64_t H, int64_t Sq, int64_t Sk, int64_t D) {
         const int64_t kcw = (chunks32 + 3) / 4;
         p.KCW = (int)(kcw < 1 ? 1 : kcw > 3 ? 3 : kcw);
         range_keys = 128 * (int64_t)p.KCW;
-        // dK/dV blocks: 16*KSUB keys per wave, KNW waves (128, 256 or 384 keys per block).
-        // 32 keys x 12 waves fits 168 VGPRs, i.e. three waves per SIMD; measured faster at
-        // Sk = 384 than 48 keys x 8 waves (two waves per SIMD).
+        // dK/dV blocks: 16*KSUB keys per wave, KNW waves, 128 keys per block. At 32 keys per
+        // wave (168 VGPRs, three waves per SIMD) three 4-wave blocks share a CU, so one block's
+        // first loads overlap the others' work: measured 14-19% faster than one 8- or 12-wave
+        // block of 256 or 384 keys per CU (Sk = 256, 384).
         if (Sk <= 128) {
             p.KSUB = 1;
             p.KNW = 8;
-        } else if (Sk <= 256) {
-            p.KSUB = 2;
-            p.KNW = 8;
         } else {
             p.KSUB = 2;
-            p.KNW = 12;
+            p.KNW = 4;
         }
         p.SqP = (int)((Sq + 63) / 64 * 64);
         qtiles = (Sq + 63) / 64;
@@ -1218,7 +1216,7 @@ void run_bwd_v2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, 
         launch_dkv2<TR, D, V, W, VEC>(st, p, q, k, v, bias_t, kmask, dout, lse2, ndi, rowl, dk,  \
                                       dv, N, H, Sq, Sk, scale);                                  \
         break;
-        CLK_KSUB(1, 8) CLK_KSUB(2, 8) CLK_KSUB(2, 12)
+        CLK_KSUB(1, 8) CLK_KSUB(2, 4)
 #undef CLK_KSUB
     }
     finish_partials<TR>(st, p, dbias_part, dq_part, dbias, dq, (size_t)H * Sq * Sk,
