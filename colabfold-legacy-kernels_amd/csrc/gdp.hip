@@ -286,6 +286,12 @@ __global__ __launch_bounds__(4 * N + 256) void ln_gdp_kernel(
     // ---- LayerNorm waves: stage z, normalise into xh, row mask into mk ----
     const int lt = tid - NWM * 64, lw = wave - NWM;
     const int lr = lt % LPR;
+    // XOR swizzle of a row's 16-byte pieces. The MFMA waves' 16-lane reads touch rows
+    // 16*sub + 0..15 (row-major outputs) or 16*a + 4*sub + b, a, b < 4 (channel-major): the
+    // swizzle takes distinct values on either set.
+    auto swz = [](int row) {
+        return (CM ? (((row >> 4) & 3) << 2) | (row & 3) : row) & GM::SWZ;
+    };
     auto stage = [&](int j, char* zb) {
         const int t = tile_of(j);
         const int rows = j < mine ? min(R, M - t * R) : 0;
@@ -334,7 +340,7 @@ __global__ __launch_bounds__(4 * N + 256) void ln_gdp_kernel(
                 unpack8<TR>(raw[p], v);
 #pragma unroll
                 for (int q = 0; q < 8; ++q) x[q] = fmaf(v[q], rstd, shift);
-                *reinterpret_cast<u32x4*>(xh + row * PL * 16 + 16 * (lr ^ (row & GM::SWZ))) =
+                *reinterpret_cast<u32x4*>(xh + row * PL * 16 + 16 * (lr ^ swz(row))) =
                     pack8<TR>(x);
             }
             if (lr == 0) mrow[row] = TR::to_f(__builtin_bit_cast(E, (uint16_t)mc[p]));
@@ -353,15 +359,18 @@ __global__ __launch_bounds__(4 * N + 256) void ln_gdp_kernel(
     };
     auto flush = [&]() {
         if constexpr (CM) {
+            // Rows 16g .. 16g+15 of one column: two 16-byte pieces per lane, which with the
+            // other three lane groups fill the column's 128-byte line of the tile.
 #pragma unroll
-            for (int sub = 0; sub < SUB; ++sub)
+            for (int h = 0; h < 2; ++h) {
+                const int col = 32 * cb + 8 * (r16 >> 2) + 4 * h + (r16 & 3);
 #pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    const int col = 32 * cb + 8 * (r16 >> 2) + 4 * h + (r16 & 3);
-                    __builtin_amdgcn_raw_buffer_store_b64(
-                        pendc[sub][h], pend_out, (col * M + pend_row + 16 * sub + 4 * g) * 2, 0,
-                        0);
+                for (int half = 0; half < 2; ++half) {
+                    const u32x2 a = pendc[2 * half][h], b = pendc[2 * half + 1][h];
+                    buf_st16(pend_out, (col * M + pend_row + 16 * g + 8 * half) * 2, 0,
+                             u32x4{a[0], a[1], b[0], b[1]});
                 }
+            }
         } else {
 #pragma unroll
             for (int sub = 0; sub < SUB; ++sub)
@@ -371,7 +380,9 @@ __global__ __launch_bounds__(4 * N + 256) void ln_gdp_kernel(
     auto project = [&](int t, const char* xh, const float* mrow) {
 #pragma unroll
         for (int sub = 0; sub < SUB; ++sub) {
-            const int xrow = 16 * sub + r16;
+            // CM: A row r16 of sub-tile sub is tile row 16*(r16/4) + 4*sub + r16%4, so the C rows
+            // 4g+i of the four sub-tiles are the 16 consecutive rows 16g .. 16g+15.
+            const int xrow = CM ? 16 * (r16 >> 2) + 4 * sub + (r16 & 3) : 16 * sub + r16;
             f32x4 acc[2][2];
 #pragma unroll
             for (int mat = 0; mat < 2; ++mat)
@@ -380,7 +391,7 @@ __global__ __launch_bounds__(4 * N + 256) void ln_gdp_kernel(
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) {
                 const V8 xb = *reinterpret_cast<const V8*>(
-                    xh + xrow * PL * 16 + 16 * ((4 * ks + g) ^ (xrow & GM::SWZ)));
+                    xh + xrow * PL * 16 + 16 * ((4 * ks + g) ^ swz(xrow)));
 #pragma unroll
                 for (int mat = 0; mat < 2; ++mat)
 #pragma unroll
@@ -394,7 +405,7 @@ __global__ __launch_bounds__(4 * N + 256) void ln_gdp_kernel(
                     E e[4];
 #pragma unroll
                     for (int i = 0; i < 4; ++i)
-                        e[i] = TR::from_f(mrow[16 * sub + 4 * g + i] * acc[0][h][i] *
+                        e[i] = TR::from_f(mrow[16 * g + 4 * sub + i] * acc[0][h][i] *
                                           fast_rcp(1.f + fast_exp2(acc[1][h][i])));
                     __builtin_memcpy(&pendc[sub][h], e, 8);
                 }
