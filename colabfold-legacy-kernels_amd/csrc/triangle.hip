@@ -2,16 +2,19 @@
 // AlphaFold's TriangleMultiplication (the step that consumes the a and b the gated dual
 // projection writes; the reference library stops at the projection, cuda/volta_ops.cu:97):
 //   outgoing  x[i,j,c] = sum_k a[i,k,c] b[j,k,c]        incoming  x[i,j,c] = sum_k a[k,i,c] b[k,j,c]
-// Per channel both are a plain N x N x N product X_c = A_c . B_c^T once a and b are stored
-// channel-major with the contraction index last (A_c[i][k] = a[i,k,c] outgoing, a[k,i,c]
-// incoming) -- the layout the fused LayerNorm + gated projection writes for this consumer.
+// Per channel both are a plain N x N x N product once a and b are stored channel-major (the
+// layout the fused LayerNorm + gated projection writes for this consumer, plane c row-major
+// over the pair index): outgoing X_c = A_c . B_c^T with the contraction index last in both
+// (A_c[i][k] = a[i,k,c]); incoming X_c = A_c^T . B_c with it first (A_c[k][i] = a[k,i,c]).
 //
 // tri_einsum_kernel: one 256 x 256 output tile of one channel per block of 8 waves (2 x 4 wave
-// tiles of 128 i x 64 j, 32 MFMA 16x16x32 accumulators each). Rows of A_c and B_c reach LDS in
-// 32-wide k slices by direct buffer->LDS loads, three slices in flight; each 16-byte piece of a
-// row is XOR-swizzled by (row / 4) % 4 so the sixteen rows an operand read touches fall in
-// distinct banks. Per slice a block moves 32 KB from L2 for 4.2 MFLOP (128 flop/B). Tiles of
-// one channel run on one XCD, whose L2 then serves A_c and B_c to all of them.
+// tiles of 128 i x 64 j, 32 MFMA 16x16x32 accumulators each). The operands reach LDS in
+// 32-wide k slices by direct buffer->LDS loads, three slices in flight. Contraction index last:
+// 256 rows of 64 bytes per operand, each 16-byte piece XOR-swizzled by (row / 4) % 4 so the
+// sixteen rows an operand read touches fall in distinct banks. Contraction index first: 32 rows
+// of 512 bytes, read with ds_read_b64_tr_b16 (a transposed 4 x 16 block per 16-lane group),
+// pieces swizzled by 2 * (row % 4). Per slice a block moves 32 KB from L2 for 4.2 MFLOP
+// (128 flop/B). Tiles of one channel run on one XCD, whose L2 then serves both operands.
 #include "common.hpp"
 
 namespace clk {
@@ -47,8 +50,38 @@ __device__ __forceinline__ void read_fragments(uint32_t ba, uint32_t bb, V8 (&fb
         : "memory");
 }
 
-// X[c] = A[c] . B[c]^T for A, B, X [C][N][N] row-major. N must be a multiple of 8.
-template <typename TR>
+// The 24 transposed fragment reads of one TN slice (A: 8 fragments, B: 4, each two
+// ds_read_b64_tr_b16 of rows 8g+j and 8g+4+j, 2 KB apart) and their wait, as one asm statement.
+__device__ __forceinline__ void read_tr_fragments(const uint32_t (&ad)[12], i16x4 (&r)[24]) {
+    asm volatile(
+        "ds_read_b64_tr_b16 %0, %24\n\tds_read_b64_tr_b16 %1, %24 offset:2048\n\t"
+        "ds_read_b64_tr_b16 %2, %25\n\tds_read_b64_tr_b16 %3, %25 offset:2048\n\t"
+        "ds_read_b64_tr_b16 %4, %26\n\tds_read_b64_tr_b16 %5, %26 offset:2048\n\t"
+        "ds_read_b64_tr_b16 %6, %27\n\tds_read_b64_tr_b16 %7, %27 offset:2048\n\t"
+        "ds_read_b64_tr_b16 %8, %28\n\tds_read_b64_tr_b16 %9, %28 offset:2048\n\t"
+        "ds_read_b64_tr_b16 %10, %29\n\tds_read_b64_tr_b16 %11, %29 offset:2048\n\t"
+        "ds_read_b64_tr_b16 %12, %30\n\tds_read_b64_tr_b16 %13, %30 offset:2048\n\t"
+        "ds_read_b64_tr_b16 %14, %31\n\tds_read_b64_tr_b16 %15, %31 offset:2048\n\t"
+        "ds_read_b64_tr_b16 %16, %32\n\tds_read_b64_tr_b16 %17, %32 offset:2048\n\t"
+        "ds_read_b64_tr_b16 %18, %33\n\tds_read_b64_tr_b16 %19, %33 offset:2048\n\t"
+        "ds_read_b64_tr_b16 %20, %34\n\tds_read_b64_tr_b16 %21, %34 offset:2048\n\t"
+        "ds_read_b64_tr_b16 %22, %35\n\tds_read_b64_tr_b16 %23, %35 offset:2048\n\t"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]),
+          "=&v"(r[6]), "=&v"(r[7]), "=&v"(r[8]), "=&v"(r[9]), "=&v"(r[10]), "=&v"(r[11]),
+          "=&v"(r[12]), "=&v"(r[13]), "=&v"(r[14]), "=&v"(r[15]), "=&v"(r[16]), "=&v"(r[17]),
+          "=&v"(r[18]), "=&v"(r[19]), "=&v"(r[20]), "=&v"(r[21]), "=&v"(r[22]), "=&v"(r[23])
+        : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3]), "v"(ad[4]), "v"(ad[5]), "v"(ad[6]),
+          "v"(ad[7]), "v"(ad[8]), "v"(ad[9]), "v"(ad[10]), "v"(ad[11])
+        : "memory");
+}
+
+// TN = false: X[c] = A[c] . B[c]^T for A, B, X [C][N][N] row-major (the contraction index
+// last). TN = true: X[c] = A[c]^T . B[c] (the contraction index first, A[c][k][i], B[c][k][j]):
+// a slice is 32 rows k of A (B) x the tile's 256 columns i (j), and the fragments are read
+// transposed with ds_read_b64_tr_b16, so the incoming direction needs no plane transposes.
+// N must be a multiple of 8.
+template <typename TR, bool TN>
 __global__ __launch_bounds__(512) void tri_einsum_kernel(const typename TR::elem* __restrict__ A,
                                                          const typename TR::elem* __restrict__ B,
                                                          typename TR::elem* __restrict__ X, int N,
@@ -76,24 +109,38 @@ __global__ __launch_bounds__(512) void tri_einsum_kernel(const typename TR::elem
     const size_t plane = (size_t)N * N;
     const E* Ac = A + c * plane;
     const E* Bc = B + c * plane;
-    // Rows of the tile past N read zeros (the resource ends with the channel's plane).
-    const Rsrc ra = buffer_rsrc(Ac + (size_t)i0 * N, (uint32_t)((size_t)min(BT, N - i0) * N * 2));
-    const Rsrc rb = buffer_rsrc(Bc + (size_t)j0 * N, (uint32_t)((size_t)min(BT, N - j0) * N * 2));
+    // NT: rows of the tile past N read zeros (the resource ends with the channel's plane).
+    // TN: the resources cover the whole plane; rows k past N read zeros, columns past N are
+    // given an out-of-range offset.
+    const Rsrc ra = TN ? buffer_rsrc(Ac, (uint32_t)(plane * 2))
+                       : buffer_rsrc(Ac + (size_t)i0 * N, (uint32_t)((size_t)min(BT, N - i0) * N * 2));
+    const Rsrc rb = TN ? buffer_rsrc(Bc, (uint32_t)(plane * 2))
+                       : buffer_rsrc(Bc + (size_t)j0 * N, (uint32_t)((size_t)min(BT, N - j0) * N * 2));
     const Rsrc none = buffer_rsrc(A, 0);
     const int nk = (N + KC - 1) / KC;
 
     // Slice kk of both operands into buffer st: A rows at st, B rows at st + SLICE. Piece q of
     // LDS row r holds the row's 16-byte piece q ^ ((r >> 2) & 3); pieces past N read zeros.
+    // TN: LDS row r (k = kk*32 + r) holds the tile's 256 columns as 32 pieces; slot q holds
+    // piece q ^ 2*(r % 4), so that the four rows of a transposed read fall in distinct banks.
     auto stage = [&](int kk, char* st) {
         const bool live = kk < nk;
 #pragma unroll
         for (int k = 0; k < DPW; ++k) {
             const int op = k / (DPW / 2);  // 0: A, 1: B
             const int b = (k % (DPW / 2)) * NT + wave * 64;
-            const int slot = b + lane, row = slot / PR;
-            const int piece = (slot % PR) ^ ((row >> 2) & (PR - 1));
-            const int kcol = kk * KC + piece * 8;
-            const int voff = kcol < N ? (row * N + kcol) * 2 : kPastEnd;
+            const int slot = b + lane;
+            int voff;
+            if constexpr (TN) {
+                const int row = slot / (BT / 8), piece = (slot % (BT / 8)) ^ (2 * (row & 3));
+                const int col = (op ? j0 : i0) + piece * 8;
+                voff = col < N ? ((kk * KC + row) * N + col) * 2 : kPastEnd;
+            } else {
+                const int row = slot / PR;
+                const int piece = (slot % PR) ^ ((row >> 2) & (PR - 1));
+                const int kcol = kk * KC + piece * 8;
+                voff = kcol < N ? (row * N + kcol) * 2 : kPastEnd;
+            }
             buf_dma16(live ? (op ? rb : ra) : none, voff, 0, st + op * SLICE + b * 16);
         }
     };
@@ -110,6 +157,18 @@ __global__ __launch_bounds__(512) void tri_einsum_kernel(const typename TR::elem
     const uint32_t lds0 = lds_addr(smem);
     const uint32_t rd = (uint32_t)(r16 * PR + (g ^ ((r16 >> 2) & (PR - 1)))) * 16;
     const uint32_t rda = rd + 128 * wi * PR * 16, rdb = rd + SLICE + 64 * wj * PR * 16;
+    // TN: fragment f (it = 0..7 of A, then jt = 0..3 of B) is column block m0 = 128wi + 16it
+    // (64wj + 16jt); lane 4j + t reads row 8g + j (and + 4), columns m0 + 4t .. + 3.
+    uint32_t trd[12];
+    if constexpr (TN) {
+        const int j = r16 >> 2, t = r16 & 3, row = 8 * g + j;
+#pragma unroll
+        for (int f = 0; f < 12; ++f) {
+            const int m0 = f < 8 ? 128 * wi + 16 * f : 64 * wj + 16 * (f - 8);
+            const int piece = ((m0 + 4 * t) >> 3) ^ (2 * j);
+            trd[f] = (f < 8 ? 0 : SLICE) + row * (BT * 2) + piece * 16 + 8 * (t & 1);
+        }
+    }
 
     stage(0, smem);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
@@ -125,9 +184,25 @@ __global__ __launch_bounds__(512) void tri_einsum_kernel(const typename TR::elem
         lds_barrier();  // slice kk in stage cur; every wave is done reading stage nxt
         stage(kk + 2, smem + nxt * STAGE);
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        const uint32_t ba = lds0 + cur * STAGE + rda, bb = lds0 + cur * STAGE + rdb;
         V8 fb[4], fa[8];
-        read_fragments(ba, bb, fb, fa);
+        if constexpr (TN) {
+            uint32_t ad[12];
+#pragma unroll
+            for (int f = 0; f < 12; ++f) ad[f] = lds0 + cur * STAGE + trd[f];
+            i16x4 r[24];
+            read_tr_fragments(ad, r);
+#pragma unroll
+            for (int f = 0; f < 12; ++f) {
+                const i16x4 lo = r[2 * f], hi = r[2 * f + 1];
+                typedef short i16x8 __attribute__((ext_vector_type(8)));
+                const i16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                if (f < 8) fa[f] = __builtin_bit_cast(V8, v);
+                else fb[f - 8] = __builtin_bit_cast(V8, v);
+            }
+        } else {
+            const uint32_t ba = lds0 + cur * STAGE + rda, bb = lds0 + cur * STAGE + rdb;
+            read_fragments(ba, bb, fb, fa);
+        }
 #pragma unroll
         for (int it = 0; it < 8; ++it)
 #pragma unroll
@@ -402,55 +477,15 @@ __global__ __launch_bounds__(512) void tri_out_kernel(TriOutParams<typename TR::
     async_wait();  // no direct-to-LDS load may still be in flight when the workgroup ends
 }
 
-template <typename TR>
+template <typename TR, bool TN = false>
 clk_status launch_einsum(hipStream_t st, const void* a, const void* b, void* x, int C, int N) {
     using E = typename TR::elem;
     const int T = (N + kTriTile - 1) / kTriTile;
     const int ntiles = C * T * T;
     KernelTimer timer("tri_einsum", st);
-    tri_einsum_kernel<TR><<<ntiles, 512, 0, st>>>((const E*)a, (const E*)b, (E*)x, N, T, ntiles);
+    tri_einsum_kernel<TR, TN><<<ntiles, 512, 0, st>>>((const E*)a, (const E*)b, (E*)x, N, T,
+                                                       ntiles);
     return check_launch("triangle_einsum");
-}
-
-// Transposes each [N][N] plane of a [P][N][N] tensor (N % 8 == 0) through a 64 x 64 LDS tile:
-// 16-byte reads of rows, 2-byte LDS scatter, 16-byte writes of the transposed rows.
-template <typename E>
-__global__ __launch_bounds__(256) void plane_transpose_kernel(const E* __restrict__ in,
-                                                              E* __restrict__ out, int N, int T) {
-    __shared__ E tile[64][64 + 8];
-    const int tid = threadIdx.x;
-    const int w = blockIdx.x, plane = w / (T * T), ti = (w / T) % T, tj = w % T;
-    const size_t base = (size_t)plane * N * N;
-    const int r0 = ti * 64, c0 = tj * 64;
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-        const int idx = tid + it * 256, r = idx / 8, c8 = (idx % 8) * 8;
-        if (r0 + r < N && c0 + c8 < N) {
-            const u32x4 v = ld16(in + base + (size_t)(r0 + r) * N + c0 + c8);
-            E e[8];
-            __builtin_memcpy(e, &v, 16);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) tile[c8 + j][r] = e[j];
-        }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int it = 0; it < 2; ++it) {
-        const int idx = tid + it * 256, r = idx / 8, c8 = (idx % 8) * 8;
-        // Output row c0 + r holds input column c0 + r, input rows r0 + c8 .. r0 + c8 + 7.
-        if (c0 + r < N && r0 + c8 < N)
-            st16(out + base + (size_t)(c0 + r) * N + r0 + c8,
-                 *reinterpret_cast<const u32x4*>(&tile[r][c8]));
-    }
-}
-
-template <typename TR>
-clk_status launch_transpose(hipStream_t st, const void* in, void* out, int P, int N) {
-    using E = typename TR::elem;
-    const int T = (N + 63) / 64;
-    KernelTimer timer("tri_transpose", st);
-    plane_transpose_kernel<E><<<P * T * T, 256, 0, st>>>((const E*)in, (E*)out, N, T);
-    return check_launch("triangle_multiply (transpose)");
 }
 
 template <typename TR, int C>
@@ -537,22 +572,14 @@ extern "C" clk_status clk_triangle_multiply(hipStream_t stream, clk_dtype dtype,
     clk_status s = ln_gdp_channel_major(stream, dtype, z, ln[0], ln[1], proj_w, proj_b, mask, wa,
                                         wb, M, c, c, eps);
     if (s != CLK_OK) return s;
-    // 2. The contraction x[c] = A[c] . B[c]^T: outgoing A = left, B = right; incoming
-    //    A = right^T, B = left^T (x[i,j] = sum_k left[k,j] right[k,i]).
-    const void *A = wa, *B = wb;
+    // 2. The contraction: outgoing x[c] = left[c] . right[c]^T; incoming x[c] = right[c]^T .
+    //    left[c] (x[i,j] = sum_k left[k,j] right[k,i]), the contraction index first, read
+    //    transposed from LDS.
     void* X = wx;
-    auto transpose = [&](const void* in, void* o) {
-        return dtype == CLK_BF16 ? launch_transpose<BF16>(stream, in, o, c, n)
-                                 : launch_transpose<F16>(stream, in, o, c, n);
-    };
-    if (!outgoing) {
-        if ((s = transpose(wb, wx)) != CLK_OK) return s;  // right^T
-        if ((s = transpose(wa, wb)) != CLK_OK) return s;  // left^T
-        A = wx;
-        B = wb;
-        X = wa;
-    }
-    if ((s = clk_triangle_einsum(stream, dtype, A, B, X, C, N)) != CLK_OK) return s;
+    s = outgoing ? clk_triangle_einsum(stream, dtype, wa, wb, X, C, N)
+                 : (dtype == CLK_BF16 ? launch_einsum<BF16, true>(stream, wb, wa, X, c, n)
+                                      : launch_einsum<F16, true>(stream, wb, wa, X, c, n));
+    if (s != CLK_OK) return s;
     // 3. LN_c(x), output projection, output gate from LN_in(z).
     auto finish = [&](auto tr) -> clk_status {
         using TR = decltype(tr);

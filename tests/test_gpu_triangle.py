@@ -68,8 +68,9 @@ def module_case(n, c, dtype, seed, dev):
 
 
 # (N, C): the pair stack's 128 channels and the template stack's 64, one 64-position tile,
-# several tiles, N not a multiple of 64 (ragged contraction tiles).
-MODULE_SHAPES = [(8, 128), (64, 128), (72, 128), (40, 64), (136, 64)]
+# several tiles, N not a multiple of 64 (ragged contraction tiles), more than one 256-wide
+# contraction tile per channel (N = 264).
+MODULE_SHAPES = [(8, 128), (64, 128), (72, 128), (40, 64), (136, 64), (264, 64)]
 
 
 @pytest.mark.parametrize("outgoing", [True, False], ids=["outgoing", "incoming"])
@@ -80,6 +81,14 @@ def test_triangle_multiply_parity(cuda, n, c, outgoing):
     r = ref.triangle_multiply(np64(z), np64(mask), tuple(map(np64, ln_in)), [np64(w) for w in ws],
                               [np64(b) for b in bs], tuple(map(np64, ln_c)), outgoing)
     assert_close("out", out, r, 2e-2)
+
+
+def test_triangle_multiply_incoming_f16(cuda):
+    z, mask, ln_in, ws, bs, ln_c = module_case(72, 64, torch.float16, 5, cuda)
+    out = ops.triangle_multiply(z, mask, ln_in, ws, bs, ln_c, False)
+    r = ref.triangle_multiply(np64(z), np64(mask), tuple(map(np64, ln_in)), [np64(w) for w in ws],
+                              [np64(b) for b in bs], tuple(map(np64, ln_c)), False)
+    assert_close("out", out, r, 1e-2)
 
 
 def test_triangle_multiply_f16_and_repeatable(cuda):
