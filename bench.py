@@ -373,8 +373,8 @@ def cpu_baseline(torch, workloads, rows, min_seconds):
 def main(argv=None):
     ap = argparse.ArgumentParser(description="Evoformer hot-path benchmark (one MI355X)")
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=N_ROWS)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)

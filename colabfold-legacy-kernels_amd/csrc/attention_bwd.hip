@@ -427,38 +427,24 @@ __device__ __forceinline__ u32x2 mask_bytes8(const uint8_t* mrow, int kk, int Sk
     }
 }
 
-// Prep: bias [H][Sq][Sk] -> bias_t [H][Sk][SqP] (SqP = Sq rounded up to 64, padding zero) in
-// 64x64 tiles through LDS, and per mask row the logit its absent keys take (-1e9, or 0 when the
-// row has no present key). Blocks [0, ntiles) transpose, blocks [ntiles, ntiles + N) do rows.
+// Tile t (of H * tiles_q * tiles_k) of bias [H][Sq][Sk] -> bias_t [H][Sk][SqP] (SqP = Sq rounded
+// up to 64, padding zero), through the 64 x 64 LDS tile `tile`, by threads tid, tid + nthreads,
+// ... of the block. Returns after the stores are issued; the caller synchronises before `tile`
+// is used again.
 template <typename TR>
-__global__ __launch_bounds__(256) void attn_bwd_prep(const typename TR::elem* __restrict__ bias,
-                                                     typename TR::elem* __restrict__ bias_t,
-                                                     const uint8_t* __restrict__ kmask,
-                                                     float* __restrict__ row_logit, int Sq,
-                                                     int Sk, int SqP, int tiles_q, int tiles_k,
-                                                     int ntiles) {
+__device__ void transpose_bias_tile(const typename TR::elem* __restrict__ bias,
+                                    typename TR::elem* __restrict__ bias_t,
+                                    typename TR::elem (*tile)[72], int t, int Sq, int Sk,
+                                    int SqP, int tiles_q, int tiles_k, int tid, int nthreads) {
     using E = typename TR::elem;
-    __shared__ __attribute__((aligned(16))) E tile[64][72];  // rows 144 B: 16-byte reads
-    if ((int)blockIdx.x >= ntiles) {
-        const int n = blockIdx.x - ntiles;
-        const uint8_t* m = kmask + (size_t)n * Sk;
-        int any = 0;
-        for (int i = threadIdx.x; i < Sk; i += 256) any |= m[i] != 0;
-        any = __syncthreads_or(any);
-        if (threadIdx.x == 0) row_logit[n] = any ? kMaskedLogit : 0.f;
-        return;
-    }
-    int t = blockIdx.x;
     const int tk = t % tiles_k;
     t /= tiles_k;
     const int tq = t % tiles_q, h = t / tiles_q;
     const int q0 = tq * 64, k0 = tk * 64;
-    // Loads: 16-byte pieces of 8 keys of one query row (two per thread) when the piece lies
-    // inside the row and the rows are 16-byte aligned; element loads otherwise.
+    // Loads: 16-byte pieces of 8 keys of one query row when the piece lies inside the row and
+    // the rows are 16-byte aligned; element loads otherwise.
     const bool vec = Sk % 8 == 0;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int ch = threadIdx.x + 256 * i;
+    for (int ch = tid; ch < 512; ch += nthreads) {
         const int r = ch >> 3, c8 = (ch & 7) * 8;  // r: query, c8: first key
         const int qq = q0 + r, kk = k0 + c8;
         E e[8];
@@ -476,9 +462,7 @@ __global__ __launch_bounds__(256) void attn_bwd_prep(const typename TR::elem* __
     }
     __syncthreads();
     // Stores: 16-byte pieces of 8 queries of one key row (SqP % 8 == 0 keeps them aligned).
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-        const int ch = threadIdx.x + 256 * i;
+    for (int ch = tid; ch < 512; ch += nthreads) {
         const int r = ch >> 3, c8 = (ch & 7) * 8;  // r: key, c8: first query
         const int kk = k0 + r, qq = q0 + c8;
         if (kk < Sk && qq < SqP)
@@ -503,10 +487,11 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
     const typename TR::elem* __restrict__ v, const typename TR::elem* __restrict__ bias,
     const uint8_t* __restrict__ kmask, const typename TR::elem* __restrict__ out,
     const typename TR::elem* __restrict__ dout, const float* __restrict__ lse,
-    const float* __restrict__ row_logit, float* __restrict__ lse2_out,
+    float* __restrict__ row_logit, float* __restrict__ lse2_out,
     float* __restrict__ ndi_out, typename TR::elem* __restrict__ dq,
     float* __restrict__ dq_part, float* __restrict__ dbias_dst, int N, int H, int Sq, int Sk,
-    int NB, int nranges, float scale) {
+    int NB, int nranges, float scale, typename TR::elem* __restrict__ bias_t, int SqP,
+    int tiles_q, int tiles_k) {
     using E = typename TR::elem;
     using V8 = typename TR::vec8;
     using T = SwzTile<D>;
@@ -736,6 +721,38 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
             pend_n = n;
         }
     };
+
+    // Work of the column-owner pass that would otherwise take a kernel of its own: the
+    // transposed bias (one 64 x 64 tile per block, through the dQ exchange buffer, which is
+    // idle until the first row ends) and the logit of the absent keys of this block's rows
+    // (-1e9, or 0 when a row has no present key; every block covering the rows writes the same
+    // values).
+    {
+        const int ttiles = H * tiles_q * tiles_k;
+        for (int t = blockIdx.x; t < ttiles; t += gridDim.x) {
+            static_assert(sizeof(xch_raw) >= 64 * 72 * sizeof(E), "transpose tile fits");
+            transpose_bias_tile<TR>(bias, bias_t, reinterpret_cast<E(*)[72]>(xch_raw), t, Sq, Sk,
+                                    SqP, tiles_q, tiles_k, threadIdx.x, 512);
+            __syncthreads();
+        }
+        if (kmask) {
+            for (int nr = n0 + wave; nr < n1; nr += 8) {
+                const uint8_t* m = kmask + (size_t)nr * Sk;
+                bool any = false;
+                if constexpr (VEC) {
+                    for (int i = 8 * lane; i < Sk; i += 512) {
+                        const u32x2 b8 = *reinterpret_cast<const u32x2*>(m + i);
+                        any |= (b8[0] | b8[1]) != 0u;
+                    }
+                } else {
+                    for (int i = lane; i < Sk; i += 64) any |= m[i] != 0;
+                }
+                any = __any(any);
+                if (lane == 0) row_logit[nr] = any ? kMaskedLogit : 0.f;
+            }
+            __syncthreads();  // this block's prefetches read them
+        }
+    }
 
     if (n0 < n1) {
         stage(n0, kv0, qd0);
@@ -1157,15 +1174,16 @@ void run_bwd_v1(hipStream_t st, const BwdPlan& p, const void* q, const void* k, 
 template <typename TR, int D, int KCW, bool VEC>
 void launch_dq2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, const void* v,
                 const void* bias, const uint8_t* kmask, const void* out, const void* dout,
-                const float* lse, const float* rowl, float* lse2, float* ndi, void* dq,
-                float* dq_part, float* dbias_dst, int N, int H, int Sq, int Sk, float scale) {
+                const float* lse, float* rowl, float* lse2, float* ndi, void* dq,
+                float* dq_part, float* dbias_dst, void* bias_t, int N, int H, int Sq, int Sk,
+                float scale) {
     using E = typename TR::elem;
     const dim3 grid(ceil_div(Sq, 64) * H * p.nchunks * p.nranges);
     KernelTimer timer("attn_bwd_dq", st);
     attn_bwd_dq2<TR, D, KCW, VEC><<<grid, 512, 0, st>>>(
         (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (const E*)out,
         (const E*)dout, lse, rowl, lse2, ndi, (E*)dq, dq_part, dbias_dst, N, H, Sq, Sk, p.NB,
-        p.nranges, scale);
+        p.nranges, scale, (E*)bias_t, p.SqP, ceil_div(p.SqP, 64), ceil_div(Sk, 64));
 }
 
 template <typename TR, int D, int KSUB, int NW, bool VEC>
@@ -1193,19 +1211,12 @@ void run_bwd_v2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, 
     float* ndi = reinterpret_cast<float*>(ws + p.off_ndi);
     float* dbias_part = reinterpret_cast<float*>(ws + p.off_dbias);
     float* dq_part = reinterpret_cast<float*>(ws + p.off_dq);
-    {
-        const int tiles_q = ceil_div(p.SqP, 64), tiles_k = ceil_div(Sk, 64);
-        const int ntiles = H * tiles_q * tiles_k;
-        KernelTimer timer("attn_bwd_prep", st);
-        attn_bwd_prep<TR><<<ntiles + (kmask ? N : 0), 256, 0, st>>>(
-            (const E*)bias, bias_t, kmask, rowl, Sq, Sk, p.SqP, tiles_q, tiles_k, ntiles);
-    }
     float* dbias_dst = p.nchunks > 1 ? dbias_part : dbias;
     switch (p.KCW) {
 #define CLK_KCW(V)                                                                               \
     case V:                                                                                      \
         launch_dq2<TR, D, V, VEC>(st, p, q, k, v, bias, kmask, out, dout, lse, rowl, lse2, ndi,  \
-                                  dq, dq_part, dbias_dst, N, H, Sq, Sk, scale);                  \
+                                  dq, dq_part, dbias_dst, bias_t, N, H, Sq, Sk, scale);          \
         break;
         CLK_KCW(1) CLK_KCW(2) CLK_KCW(3)
 #undef CLK_KCW
