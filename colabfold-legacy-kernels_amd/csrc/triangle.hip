@@ -488,6 +488,36 @@ clk_status launch_einsum(hipStream_t st, const void* a, const void* b, void* x, 
     return check_launch("triangle_einsum");
 }
 
+// Positions of an [N, N] grid of U-units (u units per position) copied to or from an [NP, NP]
+// grid (NP >= N): TO_PADDED fills the positions past N with zeros; otherwise only the N x N
+// positions are written back.
+template <typename U, bool TO_PADDED>
+__global__ __launch_bounds__(256) void pad_pairs(const U* __restrict__ src, U* __restrict__ dst,
+                                                 int N, int NP, int u) {
+    const int S = TO_PADDED ? NP : N;  // grid edge of the destination
+    const size_t total = (size_t)S * S * u;
+    for (size_t idx = (size_t)blockIdx.x * 256 + threadIdx.x; idx < total;
+         idx += (size_t)gridDim.x * 256) {
+        const size_t pos = idx / u;
+        const int e = (int)(idx % u), i = (int)(pos / S), j = (int)(pos % S);
+        if constexpr (TO_PADDED) {
+            dst[idx] = (i < N && j < N) ? src[((size_t)i * N + j) * u + e] : U{};
+        } else {
+            dst[idx] = src[((size_t)i * NP + j) * u + e];
+        }
+    }
+}
+
+template <typename U, bool TO_PADDED>
+clk_status launch_pad(hipStream_t st, const void* src, void* dst, int N, int NP, int u) {
+    const int S = TO_PADDED ? NP : N;
+    const size_t total = (size_t)S * S * u;
+    const size_t blocks = (total + 255) / 256;
+    pad_pairs<U, TO_PADDED><<<(int)(blocks < 4096 ? blocks : 4096), 256, 0, st>>>(
+        static_cast<const U*>(src), static_cast<U*>(dst), N, NP, u);
+    return check_launch("triangle_multiply (padding)");
+}
+
 template <typename TR, int C>
 clk_status launch_tri_out(hipStream_t st, const TriOutParams<typename TR::elem>& pr) {
     const int ntiles = pr.M / 64;
@@ -528,9 +558,31 @@ extern "C" clk_status clk_triangle_einsum(hipStream_t stream, clk_dtype dtype, c
     return launch_einsum<F16>(stream, a, b, x, (int)C, (int)N);
 }
 
+namespace {
+// N rounded up to a multiple of 8: a ragged N runs the module on a zero-padded grid.
+int64_t padded_n(int64_t N) { return (N + 7) / 8 * 8; }
+size_t round256(size_t v) { return (v + 255) / 256 * 256; }
+// Workspace layout: left, right, x channel-major [C][NP][NP]; for a ragged N also the padded z,
+// mask and output.
+struct TriWorkspace {
+    size_t planes, zp, mp, outp, total;
+};
+TriWorkspace tri_workspace(int64_t N, int64_t C) {
+    const int64_t NP = padded_n(N);
+    const size_t plane_set = (size_t)C * NP * NP * 2;
+    TriWorkspace w;
+    w.planes = 0;
+    w.zp = round256(3 * plane_set);
+    w.mp = w.zp + (N % 8 ? round256(plane_set) : 0);
+    w.outp = w.mp + (N % 8 ? round256((size_t)NP * NP * 2) : 0);
+    w.total = w.outp + (N % 8 ? plane_set : 0);
+    return w;
+}
+}  // namespace
+
 extern "C" size_t clk_triangle_multiply_workspace_size(int64_t N, int64_t C) {
     if (N <= 0 || C <= 0) return 0;
-    return (size_t)3 * (size_t)C * (size_t)N * (size_t)N * 2;
+    return tri_workspace(N, C).total;
 }
 
 extern "C" clk_status clk_triangle_multiply(hipStream_t stream, clk_dtype dtype, const void* z,
@@ -544,9 +596,7 @@ extern "C" clk_status clk_triangle_multiply(hipStream_t stream, clk_dtype dtype,
                     dtype_name(dtype));
     if (N < 0 || (C != 64 && C != 128))
         return fail(CLK_INVALID_ARGUMENT, "%s: C must be 64 or 128 (C=%lld)", who, (long long)C);
-    if (N % 8) return fail(CLK_INVALID_ARGUMENT, "%s: N=%lld is not a multiple of 8", who,
-                           (long long)N);
-    if (N * N * C * 2 >= ((int64_t)1 << 31))
+    if (padded_n(N) * padded_n(N) * C * 2 >= ((int64_t)1 << 31))
         return fail(CLK_INVALID_ARGUMENT, "%s: N=%lld too large", who, (long long)N);
     if (N == 0) return ok();
     if (!z || !mask || !ln || !w || !b || !out || !workspace)
@@ -561,9 +611,28 @@ extern "C" clk_status clk_triangle_multiply(hipStream_t stream, clk_dtype dtype,
     if (workspace_bytes < need)
         return fail(CLK_INVALID_ARGUMENT, "%s: workspace of %zu bytes, %zu needed", who,
                     workspace_bytes, need);
+    // A ragged N runs on a zero-padded NP x NP grid (mask 0 there, so the padded positions
+    // contribute nothing to the contraction) and copies the N x N outputs back.
+    const TriWorkspace lay = tri_workspace(N, C);
+    char* const ws = static_cast<char*>(workspace);
+    const bool ragged = N % 8 != 0;
+    const int64_t NP = padded_n(N);
+    if (ragged) {
+        clk_status ps = launch_pad<u32x4, true>(stream, z, ws + lay.zp, (int)N, (int)NP,
+                                                (int)C * 2 / 16);
+        if (ps == CLK_OK)
+            ps = launch_pad<uint16_t, true>(stream, mask, ws + lay.mp, (int)N, (int)NP, 1);
+        if (ps != CLK_OK) return ps;
+        z = ws + lay.zp;
+        mask = ws + lay.mp;
+    }
+    void* const out_final = out;
+    if (ragged) out = ws + lay.outp;
+    const int64_t N0 = N;  // the caller's grid edge
+    N = NP;
     const int M = (int)(N * N), n = (int)N, c = (int)C;
     const size_t plane_set = (size_t)C * M * 2;
-    char* wa = static_cast<char*>(workspace);
+    char* wa = ws + lay.planes;
     char* wb = wa + plane_set;
     char* wx = wb + plane_set;
     // 1. LN_in(z) and the four projections -> left (wa), right (wb), channel-major [C][N][N].
@@ -600,5 +669,7 @@ extern "C" clk_status clk_triangle_multiply(hipStream_t stream, clk_dtype dtype,
         pr.eps = eps;
         return c == 128 ? launch_tri_out<TR, 128>(stream, pr) : launch_tri_out<TR, 64>(stream, pr);
     };
-    return dtype == CLK_BF16 ? finish(BF16{}) : finish(F16{});
+    s = dtype == CLK_BF16 ? finish(BF16{}) : finish(F16{});
+    if (s != CLK_OK || !ragged) return s;
+    return launch_pad<u32x4, false>(stream, out, out_final, (int)N0, (int)NP, (int)C * 2 / 16);
 }

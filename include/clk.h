@@ -195,8 +195,10 @@ clk_status clk_triangle_einsum(hipStream_t stream, clk_dtype dtype, const void* 
  * w[0..5] = left projection, right projection, left gate, right gate, output projection, output
  * gate, each [C,C] row-major (input channel first); b[0..5] their [C] biases; ln[0..3] = LN_in
  * scale, offset, LN_c scale, offset (float32 [C]). z, mask, weights, biases and out of dtype
- * CLK_F16 or CLK_BF16. C = 64 or 128; N a multiple of 8. The workspace holds left, right and x
- * channel-major (clk_triangle_multiply_workspace_size bytes).
+ * CLK_F16 or CLK_BF16. C = 64 or 128; any N (a ragged N runs on a zero-padded grid of
+ * N rounded up to 8, the padded positions masked). The workspace holds left, right and x
+ * channel-major, and for a ragged N the padded z, mask and output
+ * (clk_triangle_multiply_workspace_size bytes).
  */
 size_t clk_triangle_multiply_workspace_size(int64_t N, int64_t C);
 clk_status clk_triangle_multiply(hipStream_t stream, clk_dtype dtype, const void* z,

@@ -71,12 +71,24 @@ def module_case(n, c, dtype, seed, dev):
 # several tiles, N not a multiple of 64 (ragged contraction tiles), more than one 256-wide
 # contraction tile per channel (N = 264).
 MODULE_SHAPES = [(8, 128), (64, 128), (72, 128), (40, 64), (136, 64), (264, 64)]
+# Ragged N (not a multiple of 8): run on a zero-padded grid internally.
+RAGGED_SHAPES = [(1, 64), (13, 128), (50, 64), (261, 64)]
 
 
 @pytest.mark.parametrize("outgoing", [True, False], ids=["outgoing", "incoming"])
 @pytest.mark.parametrize("n,c", MODULE_SHAPES)
 def test_triangle_multiply_parity(cuda, n, c, outgoing):
     z, mask, ln_in, ws, bs, ln_c = module_case(n, c, torch.bfloat16, n + c, cuda)
+    out = ops.triangle_multiply(z, mask, ln_in, ws, bs, ln_c, outgoing)
+    r = ref.triangle_multiply(np64(z), np64(mask), tuple(map(np64, ln_in)), [np64(w) for w in ws],
+                              [np64(b) for b in bs], tuple(map(np64, ln_c)), outgoing)
+    assert_close("out", out, r, 2e-2)
+
+
+@pytest.mark.parametrize("outgoing", [True, False], ids=["outgoing", "incoming"])
+@pytest.mark.parametrize("n,c", RAGGED_SHAPES)
+def test_triangle_multiply_ragged_n(cuda, n, c, outgoing):
+    z, mask, ln_in, ws, bs, ln_c = module_case(n, c, torch.bfloat16, 2 * n + c, cuda)
     out = ops.triangle_multiply(z, mask, ln_in, ws, bs, ln_c, outgoing)
     r = ref.triangle_multiply(np64(z), np64(mask), tuple(map(np64, ln_in)), [np64(w) for w in ws],
                               [np64(b) for b in bs], tuple(map(np64, ln_c)), outgoing)
