@@ -620,9 +620,13 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
             qf[qt] = swz_row_operand<V8, D>(qdc, row, 0, g);
             dof[qt] = swz_row_operand<V8, D>(qdc + QB, row, 0, g);
             const V8 of = swz_row_operand<V8, D>(qdc + 2 * QB, row, 0, g);
+            // Packed pair dot products: the element products are exact in float32.
+            u32x4 dw, ow;
+            __builtin_memcpy(&dw, &dof[qt], 16);
+            __builtin_memcpy(&ow, &of, 16);
             float part = 0.f;
 #pragma unroll
-            for (int j = 0; j < 8; ++j) part = fmaf(TR::to_f(dof[qt][j]), TR::to_f(of[j]), part);
+            for (int j = 0; j < 4; ++j) part = dot2<TR>(dw[j], ow[j], part);
             di[qt] = xgroup_sum(part);
         }
         if (range == 0 && kq == 0 && g == 0) {
@@ -682,12 +686,29 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
                 // (or merged across sub-tiles onto) the unmasked path.
                 asm volatile("");
                 const unsigned valid = nonzero_bits8(maskc[i]);
-                const int lim = Sk - (kbeg + c0 + 8 * g);  // keys j >= lim are past Sk
+                if (kbeg + c0 + 32 > Sk) {  // wave-uniform: the chunk runs past the last key
+                    int lim = Sk - (kbeg + c0 + 8 * g);  // keys j >= lim are past Sk
+                    // Opaque, so the eight compares are not hoisted out of the row loop (their
+                    // lane masks would take 48 scalar registers over the chunks and spill).
+                    asm volatile("" : "+v"(lim));
 #pragma unroll
-                for (int qt = 0; qt < 2; ++qt)
+                    for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
-                    for (int j = 0; j < 8; ++j)
-                        x[qt][j] = j >= lim ? -INFINITY : (((valid >> j) & 1u) ? x[qt][j] : mlc);
+                        for (int j = 0; j < 8; ++j)
+                            x[qt][j] = j >= lim ? -INFINITY
+                                                : (((valid >> j) & 1u) ? x[qt][j] : mlc);
+                } else {
+                    // Bit j of `valid` spread over a word (0 or ~0) selects x or the absent
+                    // key's logit bitwise.
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        const int sel = __builtin_amdgcn_sbfe((int)valid, j, 1);
+#pragma unroll
+                        for (int qt = 0; qt < 2; ++qt)
+                            x[qt][j] = __int_as_float((sel & __float_as_int(x[qt][j])) |
+                                                      (~sel & __float_as_int(mlc)));
+                    }
+                }
             }
             V8 dsf[2];
 #pragma unroll
