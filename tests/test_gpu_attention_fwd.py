@@ -89,14 +89,27 @@ def test_attention_fwd_rising_and_falling_logits(cuda, slope, dtype):
     assert np.abs(np64(lse) - lse_ref).max() < 5e-2
 
 
-@pytest.mark.parametrize("block", [(64, 64), (64, 32), (32, 32), (128, 64), (32, 64), (16, 64),
-                                   (128, 32), (7, 5)])
-def test_attention_fwd_accepts_reference_block_hints(cuda, block):
-    inp = attention_inputs(1, 2, 64, 64, 32, torch.float16, seed=3, with_dout=False)
+# Every (D, block_q, block_k) that VoltaMma (cuda/volta_mma_attn.cu:323-331) or VoltaWmma
+# (cuda/volta_wmma_attn.cu:286-292) dispatches, plus one neither knows: block sizes are hints.
+REFERENCE_BLOCKS = {
+    8: [(64, 64), (64, 32), (32, 32), (128, 64), (32, 64), (7, 5)],
+    16: [(64, 64), (32, 32), (64, 32)],
+    32: [(64, 64), (64, 32), (32, 64), (32, 32), (128, 64), (16, 64), (128, 32), (7, 5)],
+    64: [(64, 64), (32, 32), (64, 32)],
+}
+
+
+@pytest.mark.parametrize("d,block", [(d, b) for d, bs in REFERENCE_BLOCKS.items() for b in bs],
+                         ids=lambda v: str(v))
+def test_attention_fwd_accepts_reference_block_hints(cuda, d, block):
+    inp = attention_inputs(1, 2, 70, 90, d, torch.float16, seed=3, masked_tail=0.1,
+                           with_dout=False)
     g = {k: (v.to(cuda) if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
     base = ops.attention(g["q"], g["k"], g["v"], g["bias"], g["kmask"], g["scale"])
     out = ops.attention(g["q"], g["k"], g["v"], g["bias"], g["kmask"], g["scale"], *block)
     assert torch.equal(base, out)
+    o_ref, _ = _oracle(inp)
+    assert_close("O", out, o_ref, TOL["f16"]["o"])
 
 
 @pytest.mark.parametrize("name", ["triangle_attn_256", "triangle_attn_384", "msa_row_attn",

@@ -8,11 +8,11 @@ import torch
 import colabfold_legacy_kernels as clk
 from colabfold_legacy_kernels import ops
 from colabfold_legacy_kernels.workloads import attention_inputs, gdp_weights, layer_norm_inputs
-from _xla_ffi import BF16, F32, S64, U8, FakeXla
+from _xla_ffi import BF16, F16, F32, S64, U8, FakeXla
 
 pytestmark = pytest.mark.gpu
 
-DT = {torch.bfloat16: BF16, torch.float32: F32, torch.uint8: U8}
+DT = {torch.bfloat16: BF16, torch.float16: F16, torch.float32: F32, torch.uint8: U8}
 
 
 def buf(x, t):
@@ -58,6 +58,38 @@ def test_volta_mma_and_attention_bwd_targets(cuda):
     torch.cuda.synchronize()
     for a, b in zip(grads, ref):
         assert torch.equal(a, b)
+
+
+# The (D, block_q, block_k) sets each reference target dispatches (cuda/volta_mma_attn.cu:323-331,
+# cuda/volta_wmma_attn.cu:286-292), called with f16 buffers as the reference's callers do.
+VOLTA_SETS = {
+    "VoltaMma": [(8, 64, 64), (8, 64, 32), (8, 32, 32), (8, 128, 64), (8, 32, 64), (32, 64, 64),
+                 (32, 64, 32), (32, 32, 64), (32, 32, 32), (32, 128, 64), (32, 16, 64),
+                 (16, 64, 64), (16, 32, 32), (16, 64, 32), (64, 64, 64), (64, 32, 32)],
+    "VoltaWmma": [(32, 64, 64), (32, 64, 32), (32, 32, 64), (32, 32, 32), (32, 128, 64),
+                  (32, 128, 32), (16, 64, 64), (16, 32, 32), (16, 64, 32), (64, 64, 64),
+                  (64, 32, 32), (64, 64, 32), (8, 64, 64), (8, 64, 32), (8, 32, 32)],
+}
+
+
+@pytest.mark.parametrize("target", sorted(VOLTA_SETS))
+def test_volta_targets_take_every_reference_block_config(cuda, target):
+    lib, x = lib_and_runtime(cuda)
+    for d in sorted({c[0] for c in VOLTA_SETS[target]}):
+        inp = attention_inputs(2, 2, 70, 90, d, torch.float16, seed=d, device=cuda,
+                               masked_tail=0.1, with_dout=False)
+        q, k, v, bias, km = (inp[n] for n in ("q", "k", "v", "bias", "kmask"))
+        ref = ops.attention(q, k, v, bias, km, inp["scale"])
+        for dd, bq, bk in VOLTA_SETS[target]:
+            if dd != d:
+                continue
+            out = torch.empty_like(q)
+            fr = x.frame([buf(x, q), buf(x, k), buf(x, v), buf(x, bias), buf(x, km)],
+                         [buf(x, out)], [("scale", F32, inp["scale"]), ("block_q", S64, bq),
+                                         ("block_k", S64, bk)])
+            assert x.call(lib, target, fr) is None, (d, bq, bk, x.errors)
+            torch.cuda.synchronize()
+            assert torch.equal(out, ref), (d, bq, bk)
 
 
 def test_layer_norm_and_gdp_targets(cuda):
