@@ -49,9 +49,13 @@ __device__ void stage_weight(E* lds, int ld, const E* w, int K, int N, int KP, i
 }
 
 // ---------------------------------------------------------------------------------------------
-// GDP: a block owns BN output columns and walks row tiles of 4 waves x 16*RT rows.
+// GDP: a block owns BN output columns and walks row tiles of 4 waves x 16*RT rows. The weights of
+// its columns sit in LDS, KP contraction rows at a time: all of K when K <= KP (staged once), else
+// restaged per KP-row chunk inside each row tile (any K, as the reference's bounds-checked K loop,
+// cuda/volta_ops.cu:143-183). XVEC: K % 8 == 0, so x rows are read as 16-byte chunks; otherwise
+// element by element.
 // ---------------------------------------------------------------------------------------------
-template <typename TR, int BN>
+template <typename TR, int BN, bool XVEC>
 __global__ __launch_bounds__(256) void gdp_kernel(const typename TR::elem* __restrict__ x,
                                                   const typename TR::elem* __restrict__ wp,
                                                   const typename TR::elem* __restrict__ bp,
@@ -73,8 +77,11 @@ __global__ __launch_bounds__(256) void gdp_kernel(const typename TR::elem* __res
     const int r16 = lane & 15, g = lane >> 4;
     const int n0 = blockIdx.y * BN;
 
-    stage_weight(wp_lds, LD, wp, K, N, KP, n0, BN, threadIdx.x, 256);
-    stage_weight(wg_lds, LD, wg, K, N, KP, n0, BN, threadIdx.x, 256);
+    const bool chunked = K > KP;  // block-uniform
+    if (!chunked) {
+        stage_weight(wp_lds, LD, wp, K, N, KP, n0, BN, threadIdx.x, 256);
+        stage_weight(wg_lds, LD, wg, K, N, KP, n0, BN, threadIdx.x, 256);
+    }
 
     // Biases of the lane's output columns n0 + 32c + 8g + j.
     float bpv[NT / 2][8], bgv[NT / 2][8];
@@ -99,15 +106,31 @@ __global__ __launch_bounds__(256) void gdp_kernel(const typename TR::elem* __res
                 ap[rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
                 ag[rt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
             }
-        for (int kb = 0; kb < KP; kb += 32) {
+        for (int kc = 0; kc < K; kc += KP) {
+          if (chunked) {
+            __syncthreads();  // every wave is done with the previous chunk
+            stage_weight(wp_lds, LD, wp + (size_t)kc * N, K - kc, N, KP, n0, BN, threadIdx.x, 256);
+            stage_weight(wg_lds, LD, wg + (size_t)kc * N, K - kc, N, KP, n0, BN, threadIdx.x, 256);
+            __syncthreads();
+          }
+          for (int kb = 0; kb < KP; kb += 32) {
             V8 xf[RT];
 #pragma unroll
             for (int rt = 0; rt < RT; ++rt) {
                 const int row = rbase + 16 * rt + r16;
-                const int k = kb + 8 * g;
-                u32x4 raw = {0u, 0u, 0u, 0u};
-                if (row < M && k < K) raw = ld16(x + (size_t)row * K + k);
-                xf[rt] = bits_as<V8>(raw);
+                const int k = kc + kb + 8 * g;
+                if constexpr (XVEC) {
+                    u32x4 raw = {0u, 0u, 0u, 0u};
+                    if (row < M && k < K) raw = ld16(x + (size_t)row * K + k);
+                    xf[rt] = bits_as<V8>(raw);
+                } else {
+                    typename TR::elem e[8];
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        e[j] = (row < M && k + j < K) ? x[(size_t)row * K + k + j]
+                                                      : typename TR::elem(0.f);
+                    __builtin_memcpy(&xf[rt], e, 16);
+                }
             }
 #pragma unroll
             for (int t = 0; t < NT; ++t) {
@@ -119,6 +142,7 @@ __global__ __launch_bounds__(256) void gdp_kernel(const typename TR::elem* __res
                     ag[rt][t] = TR::mfma(ga, xf[rt], ag[rt][t]);
                 }
             }
+          }
         }
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) {
@@ -493,20 +517,23 @@ int row_blocks(int64_t M, int rows_per_block, int cap) {
     return (int)(b < cap ? (b > 0 ? b : 1) : cap);
 }
 
-template <typename TR, int BN>
+constexpr int kGdpMaxKP = 512;  // contraction rows of the weights staged at a time
+
+template <typename TR, int BN, bool XVEC>
 clk_status launch_gdp(hipStream_t st, const void* x, const void* wp, const void* bp,
                       const void* wg, const void* bg, const void* mask, void* out, int M, int K,
                       int N) {
     using E = typename TR::elem;
-    const int KP = (K + 31) / 32 * 32;
+    const int KP = min((K + 31) / 32 * 32, kGdpMaxKP);
     const size_t lds = (size_t)2 * KP * (BN + 8) * sizeof(E);
-    if (lds > kMaxLds) return fail(CLK_INVALID_ARGUMENT, "gated_dual_proj: K=%d too large", K);
-    allow_lds(gdp_kernel<TR, BN>, kMaxLds);
+    static_assert((size_t)2 * kGdpMaxKP * (64 + 8) * 2 <= kMaxLds, "64-column weight slab fits");
+    if (lds > kMaxLds) return fail(CLK_INTERNAL, "gated_dual_proj: K=%d weight slab too large", K);
+    allow_lds(gdp_kernel<TR, BN, XVEC>, kMaxLds);
     dim3 grid(row_blocks(M, 256, 2048), (N + BN - 1) / BN);
     KernelTimer timer("gdp", st);
-    gdp_kernel<TR, BN><<<grid, 256, lds, st>>>((const E*)x, (const E*)wp, (const E*)bp,
-                                                (const E*)wg, (const E*)bg, (const E*)mask,
-                                                (E*)out, M, K, N, KP);
+    gdp_kernel<TR, BN, XVEC><<<grid, 256, lds, st>>>((const E*)x, (const E*)wp, (const E*)bp,
+                                                      (const E*)wg, (const E*)bg, (const E*)mask,
+                                                      (E*)out, M, K, N, KP);
     return check_launch("gated_dual_proj");
 }
 
@@ -515,9 +542,11 @@ clk_status dispatch_gdp(hipStream_t st, const void* x, const void* wp, const voi
                         const void* wg, const void* bg, const void* mask, void* out, int M, int K,
                         int N) {
     const int KP = (K + 31) / 32 * 32;
+    if (K % 8)
+        return launch_gdp<TR, 64, false>(st, x, wp, bp, wg, bg, mask, out, M, K, N);
     if (N >= 128 && KP <= 256)
-        return launch_gdp<TR, 128>(st, x, wp, bp, wg, bg, mask, out, M, K, N);
-    return launch_gdp<TR, 64>(st, x, wp, bp, wg, bg, mask, out, M, K, N);
+        return launch_gdp<TR, 128, true>(st, x, wp, bp, wg, bg, mask, out, M, K, N);
+    return launch_gdp<TR, 64, true>(st, x, wp, bp, wg, bg, mask, out, M, K, N);
 }
 
 template <typename TR, int C, int N, bool CM = false>
@@ -595,12 +624,10 @@ extern "C" clk_status clk_gated_dual_proj(hipStream_t stream, clk_dtype dtype, c
         return fail(CLK_INVALID_ARGUMENT, "%s: dtype %s not supported (f16, bf16)", who,
                     dtype_name(dtype));
     if (M < 0 || K <= 0 || N <= 0) return fail(CLK_INVALID_ARGUMENT, "%s: bad dims", who);
-    // Same divisibility rule as the reference for N (cuda/volta_ops.cu:234-236); K for 16-byte
-    // row chunks; the weights of one 64/128-column slab must fit in LDS.
+    // Same divisibility rule as the reference for N (cuda/volta_ops.cu:234-236); any K, as the
+    // reference's bounds-checked K loop.
     if (N % 8) return fail(CLK_INVALID_ARGUMENT, "%s: N must be a multiple of 8", who);
-    if (K % 8) return fail(CLK_INVALID_ARGUMENT, "%s: K must be a multiple of 8", who);
-    if (K > 512) return fail(CLK_INVALID_ARGUMENT, "%s: K=%lld above 512", who, (long long)K);
-    if (M > INT32_MAX || N > (1 << 20))
+    if (M > INT32_MAX || K > INT32_MAX || N > (1 << 20))
         return fail(CLK_INVALID_ARGUMENT, "%s: dims too large", who);
     if (M == 0) return ok();
     if (!x || !wp || !bp || !wg || !bg || !mask || !out)

@@ -117,7 +117,7 @@ clk_status clk_layer_norm_bwd(hipStream_t stream, clk_dtype dtype, const void* x
  * Gated dual projection: out = mask[m] * (x.wp + bp) * sigmoid(x.wg + bg).
  * Replaces VoltaGdp (cuda/volta_ops.cu:210-265) and VoltaGdpWmma (cuda/volta_gdp_wmma.cu:
  * 99-140): the same six operands and result, all of dtype CLK_F16 or CLK_BF16. N must be a
- * multiple of 8 (volta_ops.cu:234-236); K a multiple of 8, at most 512.
+ * multiple of 8 (volta_ops.cu:234-236); any K (the weights are staged 512 rows at a time).
  */
 clk_status clk_gated_dual_proj(hipStream_t stream, clk_dtype dtype, const void* x,
                                const void* wp, const void* bp, const void* wg, const void* bg,

@@ -10,9 +10,12 @@ from oracle import gdp as ref
 
 pytestmark = pytest.mark.gpu
 
-# (M, K, N): reference shapes (128x128), the MSA width, ragged rows, K/N not multiples of 32/64.
+# (M, K, N): reference shapes (128x128), the MSA width, ragged rows, K/N not multiples of 32/64,
+# K not a multiple of 8 and K above the 512 weight rows staged at a time (both taken by the
+# reference's bounds-checked K loop, cuda/volta_ops.cu:143-183).
 GDP_SHAPES = [(1000, 128, 128), (77, 256, 256), (300, 128, 64), (33, 64, 200), (5, 40, 8),
-              (129, 512, 72), (1, 8, 8)]
+              (129, 512, 72), (1, 8, 8), (70, 100, 64), (41, 3, 16), (90, 1100, 128),
+              (65, 777, 40)]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=dname)
