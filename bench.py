@@ -199,6 +199,32 @@ def bench_ln_gdp(torch, workloads, native, dev, stream, steps, warmup):
             "ln_gdp_TFLOPs": 4 * 2.0 * m * c * n / (t * 1e-3) / 1e12}
 
 
+def bench_gdp(torch, workloads, native, dev, stream, steps, warmup):
+    """The reference's gated dual projection (VoltaGdp) on x [512*512, 128] bf16, 128x128
+    weights, one branch per call; 4 rotating sets."""
+    m, k, n = 512 * 512, 128, 128
+    lib = native.lib()
+    sets = []
+    for r in range(4):
+        li = workloads.layer_norm_inputs(m, k, torch.bfloat16, seed=60 + r, device=dev)
+        w = workloads.gdp_weights(k, n, torch.bfloat16, seed=70 + r, device=dev)
+        sets.append((li, w, torch.empty((m, n), device=dev, dtype=torch.bfloat16)))
+
+    def run(i):
+        li, w, out = sets[i % len(sets)]
+        st = lib.clk_gated_dual_proj(stream, native.BF16, li["x"].data_ptr(),
+                                     *(t.data_ptr() for t in w), li["mask"].data_ptr(),
+                                     out.data_ptr(), m, k, n)
+        if st != 0:
+            raise RuntimeError(native.last_error())
+
+    t = timed(torch, run, steps, warmup, torch.cuda.current_stream(dev))
+    nbytes = m * k * 2.0 + m * 2.0 + m * n * 2.0 + 2.0 * k * n * 2.0
+    kt = per_kernel(torch, native, run, steps)
+    return {"gdp_GBps": nbytes / (t * 1e-3) / 1e9, "gdp_ms": t,
+            "gdp_kernel_ms": kt.get("gdp", {}).get("avg_ms"), "gdp_bytes": nbytes}
+
+
 def bench_gdp_bwd(torch, workloads, native, dev, stream, steps, warmup):
     """Gated dual projection backward on x [512*512, 128] bf16, 128x128 weights, dout ~N(0,1);
     2 rotating sets. Reports the call time and each kernel's."""
@@ -440,6 +466,9 @@ def main(argv=None):
         print("bench: timing LayerNorm + gated dual projection", file=sys.stderr, flush=True)
         sec.update(bench_ln_gdp(torch, workloads, native, dev, stream, args.steps, args.warmup))
         sec["ln_gdp_frac_hbm"] = sec["ln_gdp_GBps"] / HBM_PEAK
+        print("bench: timing the gated dual projection", file=sys.stderr, flush=True)
+        sec.update(bench_gdp(torch, workloads, native, dev, stream, args.steps, args.warmup))
+        sec["gdp_frac_hbm"] = sec["gdp_GBps"] / HBM_PEAK
         print("bench: timing the gated dual projection backward", file=sys.stderr, flush=True)
         sec.update(bench_gdp_bwd(torch, workloads, native, dev, stream, args.steps, args.warmup))
         print("bench: timing the pair-bias projection", file=sys.stderr, flush=True)

@@ -168,6 +168,112 @@ __global__ __launch_bounds__(256) void gdp_kernel(const typename TR::elem* __res
 }
 
 // ---------------------------------------------------------------------------------------------
+// GDP for K <= 32*KS with K % 8 == 0 (the pair and MSA widths), 128 output columns per block:
+// the operand layout of gdp_kernel, but a block stays resident over many 64-row tiles (the
+// weight slab is staged once per block, not once per tile), each wave's x fragments of its next
+// tile are in flight while the current tile is computed (two register sets, the row loop
+// unrolled by two so that neither is ever copied), and the biases enter as the accumulators'
+// starting values, read from LDS.
+// ---------------------------------------------------------------------------------------------
+template <typename TR, int KS>
+__global__ __launch_bounds__(256) void gdp_stream_kernel(
+    const typename TR::elem* __restrict__ x, const typename TR::elem* __restrict__ wp,
+    const typename TR::elem* __restrict__ bp, const typename TR::elem* __restrict__ wg,
+    const typename TR::elem* __restrict__ bg, const typename TR::elem* __restrict__ mask,
+    typename TR::elem* __restrict__ out, int M, int K, int N) {
+    using E = typename TR::elem;
+    using V8 = typename TR::vec8;
+    constexpr int BN = 128, NT = BN / 16, RT = 1, LD = BN + 8, KP = 32 * KS;
+    constexpr int ROWS = 4 * 16 * RT;  // rows per block and tile
+    __shared__ __attribute__((aligned(16))) E wp_lds[KP * LD];
+    __shared__ __attribute__((aligned(16))) E wg_lds[KP * LD];
+    __shared__ __attribute__((aligned(16))) float b_lds[2][BN];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int r16 = lane & 15, g = lane >> 4;
+    const int n0 = blockIdx.y * BN;
+    stage_weight(wp_lds, LD, wp, K, N, KP, n0, BN, tid, 256);
+    stage_weight(wg_lds, LD, wg, K, N, KP, n0, BN, tid, 256);
+    for (int i = tid; i < BN; i += 256) {
+        const int n = n0 + i;
+        b_lds[0][i] = n < N ? TR::to_f(bp[n]) : 0.f;
+        b_lds[1][i] = n < N ? TR::to_f(bg[n]) : 0.f;
+    }
+    __syncthreads();
+
+    using XF = V8[KS][RT];
+    auto load = [&](int r0, XF& xf) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                const int row = r0 + wave * 16 * RT + 16 * rt + r16;
+                const int k = 32 * ks + 8 * g;
+                u32x4 raw = {0u, 0u, 0u, 0u};
+                if (row < M && k < K) raw = ld16(x + (size_t)row * K + k);
+                xf[ks][rt] = bits_as<V8>(raw);
+            }
+    };
+    auto tile = [&](int r0, const XF& xf) {
+        f32x4 ap[RT][NT], ag[RT][NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            // Accumulator row 4g+i of A tile t is output column 32(t/2) + 8g + 4(t%2) + i.
+            const int col = 32 * (t >> 1) + 8 * g + 4 * (t & 1);
+            const f32x4 bpi = *reinterpret_cast<const f32x4*>(&b_lds[0][col]);
+            const f32x4 bgi = *reinterpret_cast<const f32x4*>(&b_lds[1][col]);
+#pragma unroll
+            for (int rt = 0; rt < RT; ++rt) {
+                ap[rt][t] = bpi;
+                ag[rt][t] = bgi;
+            }
+        }
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const V8 pa = w_operand<V8>(wp_lds, LD, 32 * ks, t >> 1, t & 1, r16, g);
+                const V8 ga = w_operand<V8>(wg_lds, LD, 32 * ks, t >> 1, t & 1, r16, g);
+#pragma unroll
+                for (int rt = 0; rt < RT; ++rt) {
+                    ap[rt][t] = TR::mfma(pa, xf[ks][rt], ap[rt][t]);
+                    ag[rt][t] = TR::mfma(ga, xf[ks][rt], ag[rt][t]);
+                }
+            }
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) {
+            const int row = r0 + wave * 16 * RT + 16 * rt + r16;
+            if (row >= M) continue;
+            const float mv = TR::to_f(mask[row]);
+#pragma unroll
+            for (int c = 0; c < NT / 2; ++c) {
+                const int n = n0 + 32 * c + 8 * g;
+                if (n >= N) continue;
+                float o[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int t = 2 * c + (j >> 2), i = j & 3;
+                    o[j] = mv * ap[rt][t][i] * sigmoid(ag[rt][t][i]);
+                }
+                st16(out + (size_t)row * N + n, pack8<TR>(o));
+            }
+        }
+    };
+
+    const int stride = gridDim.x * ROWS;
+    XF xa, xb;
+    int r0 = blockIdx.x * ROWS;
+    if (r0 < M) load(r0, xa);
+    for (; r0 < M; r0 += 2 * stride) {
+        if (r0 + stride < M) load(r0 + stride, xb);
+        tile(r0, xa);
+        if (r0 + stride >= M) break;
+        if (r0 + 2 * stride < M) load(r0 + 2 * stride, xa);
+        tile(r0 + stride, xb);
+    }
+}
+
+// ---------------------------------------------------------------------------------------------
 // LayerNorm + both gated branches (the two inputs of the triangle multiplication). A block has
 // two kinds of waves. MFMA wave w of the N/16 owns the 32 output columns 32*cb + 0..31
 // (cb = w % (N/32)) of branch w / (N/32) and holds the matching columns of that branch's
@@ -234,16 +340,18 @@ __device__ __forceinline__ void lds_rows(uint32_t addr, u32x4 (&r)[N]) {
 // major [N, M] (a[n][m]), the operand layout of the triangle-multiplication contraction; the MFMA
 // operands swap roles (out = xhat . W') so that a lane's accumulators hold four consecutive rows
 // of one output column, stored as one 8-byte piece of that column's plane. CM needs M % 64 == 0.
-// Block: N/16 MFMA waves, then 4 LayerNorm waves.
-template <typename TR, int C, int N, bool CM>
-__global__ __launch_bounds__(4 * N + 256) void ln_gdp_kernel(
+// LN = false, NB = 1: the plain gated dual projection of one branch (x = z as it is; the four
+// staging waves only move z into the swizzled tile, and gamma, beta are not read).
+// Block: NB*N/32 MFMA waves, then 4 LayerNorm (staging) waves.
+template <typename TR, int C, int N, bool CM, bool LN = true, int NB = 2>
+__global__ __launch_bounds__(64 * NB * N / 32 + 256) void ln_gdp_kernel(
     const typename TR::elem* __restrict__ z, const float* __restrict__ gamma,
     const float* __restrict__ beta, LnGdpWeights<typename TR::elem> wb,
     const typename TR::elem* __restrict__ mask, typename TR::elem* __restrict__ outa,
     typename TR::elem* __restrict__ outb, int M, float eps) {
     using E = typename TR::elem;
     using V8 = typename TR::vec8;
-    constexpr int NWM = N / 16;          // MFMA waves
+    constexpr int NWM = NB * N / 32;     // MFMA waves
     constexpr int NTL = 256;             // LayerNorm threads (4 waves)
     constexpr int KS = C / 32;
     constexpr int R = kLnGdpRows, SUB = R / 16;
@@ -288,8 +396,8 @@ __global__ __launch_bounds__(4 * N + 256) void ln_gdp_kernel(
                     for (int j = 0; j < 8; ++j) {
                         const int k = 32 * ks + 8 * g + j;
                         const float v = TR::to_f(W[(size_t)k * N + col]);
-                        wa[mat][h][ks][j] = TR::from_f(gamma[k] * v * fold);
-                        part = fmaf(beta[k], v, part);
+                        wa[mat][h][ks][j] = TR::from_f((LN ? gamma[k] : 1.f) * v * fold);
+                        if constexpr (LN) part = fmaf(beta[k], v, part);
                     }
                 const float bcol = (xgroup_sum(part) + TR::to_f(wb.b[2 * br + mat][col])) * fold;
                 if constexpr (CM) {
@@ -341,6 +449,16 @@ __global__ __launch_bounds__(4 * N + 256) void ln_gdp_kernel(
         u32x4 raw[PASSES];
         lds_rows<PASSES, RPP * C * 2>(lds_addr(zc + (lt / LPR) * C * 2 + (lr < PL ? lr : 0) * 16),
                                       raw);
+        if constexpr (!LN) {
+#pragma unroll
+            for (int p = 0; p < PASSES; ++p) {
+                const int row = p * RPP + lt / LPR;
+                if (lr < PL)
+                    *reinterpret_cast<u32x4*>(xh + row * PL * 16 + 16 * (lr ^ swz(row))) = raw[p];
+                if (lr == 0) mrow[row] = TR::to_f(__builtin_bit_cast(E, (uint16_t)mc[p]));
+            }
+            return;
+        }
 #pragma unroll
         for (int p = 0; p < PASSES; ++p) {
             const int row = p * RPP + lt / LPR;
@@ -537,11 +655,60 @@ clk_status launch_gdp(hipStream_t st, const void* x, const void* wp, const void*
     return check_launch("gated_dual_proj");
 }
 
+// The plain gated dual projection through the LN + GDP kernel without its LayerNorm: one branch,
+// each wave's 32 output columns of both weights resident in registers, x shared through LDS.
+template <typename TR, int K, int N>
+clk_status launch_gdp_resident(hipStream_t st, const void* x, const void* wp, const void* bp,
+                               const void* wg, const void* bg, const void* mask, void* out,
+                               int M) {
+    using E = typename TR::elem;
+    LnGdpWeights<E> wb;
+    wb.w[0] = (const E*)wp;
+    wb.w[1] = (const E*)wg;
+    wb.b[0] = (const E*)bp;
+    wb.b[1] = (const E*)bg;
+    wb.w[2] = wb.w[3] = nullptr;  // one branch: the second pair is never read
+    wb.b[2] = wb.b[3] = nullptr;
+    // Resident blocks per CU: the five 64-row LDS tiles take 80 KB at K = 128 (one block), 40 KB
+    // at K = 64 (two).
+    const int ntiles = (M + kLnGdpRows - 1) / kLnGdpRows;
+    const int per_cu = K == 128 ? 1 : 2;
+    const int grid = ntiles < 256 * per_cu ? ntiles : 256 * per_cu;
+    KernelTimer timer("gdp", st);
+    ln_gdp_kernel<TR, K, N, false, false, 1><<<grid, 2 * N + 256, 0, st>>>(
+        (const E*)x, nullptr, nullptr, wb, (const E*)mask, (E*)out, nullptr, M, 0.f);
+    return check_launch("gated_dual_proj");
+}
+
+template <typename TR, int KS>
+clk_status launch_gdp_stream(hipStream_t st, const void* x, const void* wp, const void* bp,
+                             const void* wg, const void* bg, const void* mask, void* out, int M,
+                             int K, int N) {
+    using E = typename TR::elem;
+    // Two resident blocks per CU (the 128-column slab of both weights takes 70 KB of LDS at
+    // K = 128), each walking row tiles of 64.
+    dim3 grid(row_blocks(M, 64, 2 * 256), (N + 127) / 128);
+    KernelTimer timer("gdp", st);
+    gdp_stream_kernel<TR, KS><<<grid, 256, 0, st>>>((const E*)x, (const E*)wp, (const E*)bp,
+                                                     (const E*)wg, (const E*)bg, (const E*)mask,
+                                                     (E*)out, M, K, N);
+    return check_launch("gated_dual_proj");
+}
+
 template <typename TR>
 clk_status dispatch_gdp(hipStream_t st, const void* x, const void* wp, const void* bp,
                         const void* wg, const void* bg, const void* mask, void* out, int M, int K,
                         int N) {
     const int KP = (K + 31) / 32 * 32;
+#define CLK_GDPR(KK, NN)                                                                           \
+    if (K == KK && N == NN)                                                                        \
+        return launch_gdp_resident<TR, KK, NN>(st, x, wp, bp, wg, bg, mask, out, M);
+    CLK_GDPR(128, 128) CLK_GDPR(128, 64) CLK_GDPR(64, 128) CLK_GDPR(64, 64)
+#undef CLK_GDPR
+    if (K % 8 == 0 && N >= 64 && K <= 128) {
+        if (KP <= 64) return launch_gdp_stream<TR, 2>(st, x, wp, bp, wg, bg, mask, out, M, K, N);
+        return launch_gdp_stream<TR, 4>(st, x, wp, bp, wg, bg, mask, out, M, K, N);
+    }
     if (K % 8)
         return launch_gdp<TR, 64, false>(st, x, wp, bp, wg, bg, mask, out, M, K, N);
     if (N >= 128 && KP <= 256)

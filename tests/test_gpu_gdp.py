@@ -15,7 +15,8 @@ pytestmark = pytest.mark.gpu
 # reference's bounds-checked K loop, cuda/volta_ops.cu:143-183).
 GDP_SHAPES = [(1000, 128, 128), (77, 256, 256), (300, 128, 64), (33, 64, 200), (5, 40, 8),
               (129, 512, 72), (1, 8, 8), (70, 100, 64), (41, 3, 16), (90, 1100, 128),
-              (65, 777, 40)]
+              (65, 777, 40), (200, 64, 64), (130, 64, 128), (100, 32, 96), (64, 96, 128),
+              (3, 128, 128)]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=dname)
