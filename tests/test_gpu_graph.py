@@ -1,0 +1,72 @@
+"""Every entry point under HIP graph capture. The handlers of the reference declare XLA's
+command-buffer trait (cuda/volta_mma_attn.cu:338-351, cuda/volta_ops.cu:87-95, :254-265), so a
+caller may capture them; the library records only kernel launches on the given stream (no
+allocation, synchronisation or memset). Each graph is captured once after an eager warm-up call,
+then replayed several times with eager work in between that overwrites its outputs; every replay
+must give the eager result bit for bit."""
+import pytest
+import torch
+
+from colabfold_legacy_kernels import ops
+from colabfold_legacy_kernels.workloads import attention_inputs, gdp_weights, layer_norm_inputs
+from test_gpu_triangle import module_case
+
+pytestmark = pytest.mark.gpu
+
+
+def _flatten(x):
+    if isinstance(x, torch.Tensor):
+        return [x]
+    out = []
+    for t in x:
+        out += _flatten(t)
+    return out
+
+
+def _check_replays(fn, replays=3):
+    eager = [t.clone() for t in _flatten(fn())]
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        static = _flatten(fn())
+    for r in range(replays):
+        for t in static:  # eager work between the replays, on the outputs themselves
+            t.fill_(float("nan") if t.is_floating_point() else 0)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for i, (a, b) in enumerate(zip(static, eager)):
+            assert torch.equal(a, b), (r, i)
+
+
+def test_attention_fwd_bwd_graph(cuda):
+    inp = attention_inputs(3, 2, 100, 90, 32, torch.bfloat16, seed=21, device=cuda,
+                           masked_tail=0.1, masked_rows=1)
+    q, k, v, bias, km, dout, s = (inp[n] for n in ("q", "k", "v", "bias", "kmask", "dout", "scale"))
+
+    def step():
+        out, lse = ops.attention_fwd(q, k, v, bias, km, s)
+        return out, lse, ops.attention_bwd(q, k, v, bias, km, out, dout, lse, s)
+
+    _check_replays(step)
+
+
+def test_layer_norm_and_gdp_graph(cuda):
+    li = layer_norm_inputs(3000, 128, torch.bfloat16, seed=5, device=cuda)
+    w = gdp_weights(128, 128, torch.bfloat16, seed=6, device=cuda, bias_std=0.3)
+    wb = gdp_weights(128, 128, torch.bfloat16, seed=7, device=cuda, bias_std=0.3)
+    x, sc, off, mask, dy = li["x"], li["scale"], li["offset"], li["mask"], li["dy"]
+
+    def step():
+        y = ops.layer_norm(x, sc, off)
+        return (y, ops.layer_norm_bwd(x, sc, dy), ops.gated_dual_proj(y, *w, mask),
+                ops.gated_dual_proj_bwd(x, *w, mask, dy),
+                ops.ln_gated_dual_proj(x, sc, off, w, wb, mask))
+
+    _check_replays(step)
+
+
+@pytest.mark.parametrize("outgoing", [True, False], ids=["outgoing", "incoming"])
+def test_triangle_multiply_graph(cuda, outgoing):
+    z, mask, ln_in, ws, bs, ln_c = module_case(72, 64, torch.bfloat16, 9, cuda)
+    _check_replays(lambda: ops.triangle_multiply(z, mask, ln_in, ws, bs, ln_c, outgoing))
