@@ -3,7 +3,7 @@ command-buffer trait (cuda/volta_mma_attn.cu:338-351, cuda/volta_ops.cu:87-95, :
 caller may capture them; the library records only kernel launches on the given stream (no
 allocation, synchronisation or memset). Each graph is captured once after an eager warm-up call,
 then replayed several times with eager work in between that overwrites its outputs; every replay
-must give the eager result bit for bit."""
+must give the eager result bit for bit. Also: calls from several host threads at once."""
 import pytest
 import torch
 
@@ -70,3 +70,47 @@ def test_layer_norm_and_gdp_graph(cuda):
 def test_triangle_multiply_graph(cuda, outgoing):
     z, mask, ln_in, ws, bs, ln_c = module_case(72, 64, torch.bfloat16, 9, cuda)
     _check_replays(lambda: ops.triangle_multiply(z, mask, ln_in, ws, bs, ln_c, outgoing))
+
+
+def test_entry_points_from_concurrent_host_threads(cuda):
+    """Re-entrancy (no mutable statics; errors are thread-local): four host threads, each on its
+    own stream, call the attention forward and backward and LayerNorm at the same time; each
+    thread's results equal the same calls made one after another."""
+    import threading
+
+    cases = [attention_inputs(2, 2, 70 + 10 * i, 64, 32, torch.bfloat16, seed=40 + i,
+                              device=cuda, masked_tail=0.1) for i in range(4)]
+    lis = [layer_norm_inputs(500 + i, 128, torch.bfloat16, seed=60 + i, device=cuda)
+           for i in range(4)]
+
+    def work(i):
+        c, li = cases[i], lis[i]
+        out, lse = ops.attention_fwd(c["q"], c["k"], c["v"], c["bias"], c["kmask"], c["scale"])
+        grads = ops.attention_bwd(c["q"], c["k"], c["v"], c["bias"], c["kmask"], out, c["dout"],
+                                  lse, c["scale"])
+        return _flatten((out, lse, grads, ops.layer_norm(li["x"], li["scale"], li["offset"])))
+
+    serial = [[t.clone() for t in work(i)] for i in range(4)]
+    torch.cuda.synchronize()
+    results, errors = [None] * 4, []
+
+    def run(i):
+        try:
+            s = torch.cuda.Stream(device=cuda)
+            with torch.cuda.stream(s):
+                for _ in range(3):
+                    r = work(i)
+                s.synchronize()
+            results[i] = r
+        except Exception as e:  # reported below, in the main thread
+            errors.append((i, repr(e)))
+
+    threads = [threading.Thread(target=run, args=(i,)) for i in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join(timeout=60)
+    assert not errors, errors
+    for i in range(4):
+        for a, b in zip(results[i], serial[i]):
+            assert torch.equal(a, b), i
