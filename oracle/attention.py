@@ -17,7 +17,7 @@ For rows with at least one unmasked key this equals the reference kernel's outpu
 constant and this -1e9 both give P = 0 to float precision); for fully masked rows it is the
 jnp value mean(V) (the reference kernel divides by the tile-padded key count instead).
 
-Backward (no reference code; the reference is forward-only, SURVEY row A9):
+Backward (no reference code; the reference is forward-only):
   D = rowsum(dO * O), dS = P * (dO . V^T - D),
   dQ = scale * dS . K, dK = scale * dS^T . Q, dV = P^T . dO, dBias[h] = sum_n dS[n, h].
 """

@@ -6,7 +6,7 @@ The reference kernel forms var as max(E[x^2] - mu^2, 0) in float32 (volta_ops.cu
 float64 that is the same number as the two-pass form used here up to rounding, and the HIP kernel
 uses a Chan/Welford merge, which tracks the two-pass value.
 
-Backward (no reference code; SURVEY row A10), with xhat = (x - mu) * r and g = scale * dy:
+Backward (no reference code), with xhat = (x - mu) * r and g = scale * dy:
   dx = r * (g - mean_c(g) - xhat * mean_c(g * xhat)),
   dscale = sum_m dy * xhat, doffset = sum_m dy.
 
