@@ -65,10 +65,12 @@ def attention_flops(n, h, sq, sk, d):
 class AttentionSet:
     """One rotating set of inputs and preallocated outputs for the C ABI."""
 
-    def __init__(self, torch, workloads, native, dev, seed):
-        inp = workloads.attention_inputs(N_ROWS, HEADS, NRES, NRES, HEAD_DIM, torch.bfloat16,
+    def __init__(self, torch, workloads, native, dev, seed, dtype=None):
+        dtype = torch.bfloat16 if dtype is None else dtype
+        inp = workloads.attention_inputs(N_ROWS, HEADS, NRES, NRES, HEAD_DIM, dtype,
                                          seed=seed, device=dev, masked_tail=0.10)
         self.__dict__.update(inp)
+        self.code = native.BF16 if dtype == torch.bfloat16 else native.F16
         self.out = torch.empty_like(self.q)
         self.lse = torch.empty((N_ROWS, HEADS, NRES), device=dev, dtype=torch.float32)
         self.dq = torch.empty_like(self.q)
@@ -82,12 +84,12 @@ class AttentionSet:
 
 def attention_step(lib, native, stream, s):
     dims = (N_ROWS, HEADS, NRES, NRES, HEAD_DIM)
-    st = lib.clk_attention_fwd(stream, native.BF16, s.q.data_ptr(), s.k.data_ptr(),
+    st = lib.clk_attention_fwd(stream, s.code, s.q.data_ptr(), s.k.data_ptr(),
                                s.v.data_ptr(), s.bias.data_ptr(), s.kmask.data_ptr(),
                                s.out.data_ptr(), s.lse.data_ptr(), *dims, s.scale, 64, 64)
     if st != 0:
         raise RuntimeError(native.last_error())
-    st = lib.clk_attention_bwd(stream, native.BF16, s.q.data_ptr(), s.k.data_ptr(),
+    st = lib.clk_attention_bwd(stream, s.code, s.q.data_ptr(), s.k.data_ptr(),
                                s.v.data_ptr(), s.bias.data_ptr(), s.kmask.data_ptr(),
                                s.out.data_ptr(), s.dout.data_ptr(), s.lse.data_ptr(),
                                s.dq.data_ptr(), s.dk.data_ptr(), s.dv.data_ptr(),
@@ -122,6 +124,21 @@ def per_kernel(torch, native, fn, steps):
         tot, cnt = agg.get(name, (0.0, 0))
         agg[name] = (tot + ms, cnt + 1)
     return {k: {"avg_ms": t / c, "launches_per_step": c / steps} for k, (t, c) in agg.items()}
+
+
+def bench_attention_f16(torch, workloads, native, dev, stream, steps, warmup):
+    """The headline step in float16, the reference's own operand type (same shapes, 3 rotating
+    sets)."""
+    lib = native.lib()
+    sets = [AttentionSet(torch, workloads, native, dev, seed=11 + r, dtype=torch.float16)
+            for r in range(ROTATE)]
+
+    def step(i):
+        attention_step(lib, native, stream, sets[i % ROTATE])
+
+    ms = timed(torch, step, steps, warmup, torch.cuda.current_stream(dev))
+    flops = attention_flops(N_ROWS, HEADS, NRES, NRES, HEAD_DIM)["step"]
+    return {"attn_f16_ms": ms, "attn_f16_TFLOPs": flops / (ms * 1e-3) / 1e12}
 
 
 def bench_layer_norm(torch, workloads, native, dev, stream, steps, warmup):
@@ -461,6 +478,9 @@ def main(argv=None):
     if not args.no_secondary:
         print("bench: timing LayerNorm", file=sys.stderr, flush=True)
         sec = bench_layer_norm(torch, workloads, native, dev, stream, args.steps, args.warmup)
+        print("bench: timing the attention step in float16", file=sys.stderr, flush=True)
+        sec.update(bench_attention_f16(torch, workloads, native, dev, stream, args.steps,
+                                       args.warmup))
         sec["ln_fwd_frac_hbm"] = sec["ln_fwd_GBps"] / HBM_PEAK
         sec["ln_bwd_frac_hbm"] = sec["ln_bwd_GBps"] / HBM_PEAK
         print("bench: timing LayerNorm + gated dual projection", file=sys.stderr, flush=True)
