@@ -56,6 +56,28 @@ def test_attention_bwd_parity(cuda, case, dtype):
     assert_close("dBias", dbias, rb, tol)
 
 
+@pytest.mark.parametrize("shape", [(3, 2, 100, 130), (2, 2, 200, 384)], ids=str)
+def test_attention_bwd_bias_past_float16_range(cuda, shape):
+    """bfloat16 biases beyond float16's range (the reference's operand type) stay exact: a query
+    row whose bias is -70000 for every key, one key at +70000 and one at -70000 in other rows."""
+    n, h, sq, sk = shape
+    inp = attention_inputs(n, h, sq, sk, 32, torch.bfloat16, seed=77, masked_tail=0.1)
+    b = inp["bias"].float()
+    b[0, 5, :] = -70000.0
+    b[1, sq - 3, 7] = 70000.0
+    b[1, 40, sk // 2] = -70000.0
+    inp["bias"] = b.to(torch.bfloat16)
+    _, out, lse, (dq, dk, dv, dbias) = _run(inp, cuda)
+    for t in (out, lse, dq, dk, dv, dbias):
+        assert torch.isfinite(t).all()
+    rq, rk, rv, rb = _oracle(inp)
+    tol = TOL["bf16"]["grad"]
+    assert_close("dQ", dq, rq, tol)
+    assert_close("dK", dk, rk, tol)
+    assert_close("dV", dv, rv, tol)
+    assert_close("dBias", dbias, rb, tol)
+
+
 def test_attention_bwd_deterministic(cuda):
     inp = attention_inputs(6, 4, 200, 200, 32, torch.bfloat16, seed=21, masked_tail=0.1,
                            masked_rows=1)
