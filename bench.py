@@ -6,7 +6,8 @@ Headline (one JSON line on stdout): triangle attention forward + backward at N_r
 (q, k, v [384 rows, 4 heads, 384 residues, 32], bf16 in, float32 accumulate), in TFLOP/s of
 algorithmic work 12*N*H*Sq*Sk*D per step. A step is one forward and one backward over the whole
 batch, through the C ABI with preallocated buffers; inputs rotate over 3 sets (~0.9 GB) so the
-256 MB Infinity Cache cannot hold them. Secondary figures: LayerNorm forward/backward and
+256 MB Infinity Cache cannot hold them. ms_per_step is the median of the per-step durations (one
+HIP event between consecutive steps on the launch stream); the bracket mean is reported beside it. Secondary figures: LayerNorm forward/backward and
 LayerNorm + gated dual projection on the 512x512x128 pair representation, and the attention
 output gate of MSA row attention (512 rows x 256 queries, 8 x 32 heads, 256 channels), in HBM
 GB/s; the gated dual projection backward on [512*512, 128] per kernel; the pair-bias projection
@@ -98,18 +99,26 @@ def attention_step(lib, native, stream, s):
         raise RuntimeError(native.last_error())
 
 
-def timed(torch, fn, steps, warmup, stream_obj):
+def timed(torch, fn, steps, warmup, stream_obj, stats=None):
+    """Median ms per step over `steps` timed steps after `warmup` untimed ones: one HIP event on
+    the launch stream before each step and one after the last, so every step has its own
+    duration. `stats` (a dict), when given, also receives the mean over the whole bracket."""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
-    a = torch.cuda.Event(enable_timing=True)
-    b = torch.cuda.Event(enable_timing=True)
-    a.record(stream_obj)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+    ev[0].record(stream_obj)
     for i in range(steps):
         fn(i)
-    b.record(stream_obj)
+        ev[i + 1].record(stream_obj)
     torch.cuda.synchronize()
-    return a.elapsed_time(b) / steps
+    per = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+    mid = len(per) // 2
+    median = per[mid] if len(per) % 2 else 0.5 * (per[mid - 1] + per[mid])
+    if stats is not None:
+        stats["mean_ms"] = ev[0].elapsed_time(ev[steps]) / steps
+        stats["min_ms"], stats["max_ms"] = per[0], per[-1]
+    return median
 
 
 def per_kernel(torch, native, fn, steps):
@@ -449,7 +458,8 @@ def main(argv=None):
         attention_step(lib, native, stream, sets[i % ROTATE])
 
     print("bench: timing attention fwd+bwd", file=sys.stderr, flush=True)
-    ms = timed(torch, step, args.steps, args.warmup, so)
+    step_stats = {}
+    ms = timed(torch, step, args.steps, args.warmup, so, step_stats)
     fl = attention_flops(N_ROWS, HEADS, NRES, NRES, HEAD_DIM)
     tflops = fl["step"] / (ms * 1e-3) / 1e12
     kernels = per_kernel(torch, native, step, args.steps)
@@ -465,6 +475,8 @@ def main(argv=None):
     result = {
         "metric": METRIC, "value": tflops, "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "ms_per_step_mean": step_stats["mean_ms"], "ms_per_step_min": step_stats["min_ms"],
+        "ms_per_step_max": step_stats["max_ms"],
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": "triangle attention fwd+bwd, N_res=384", "rows": N_ROWS,

@@ -8,9 +8,10 @@ locator's ``library_path`` names. This is the counterpart of the reference's per
 (scripts/build_kernels.sh:86-116): one target architecture, no CUTLASS, no XLA headers needed.
 
 ``--asm`` also writes the gfx950 assembly of each kernel source to ``_build/<name>.s`` (device
-code only), which ``tests/test_build.py`` scans for ``v_mfma`` instructions -- the analogue of
-the reference's tensor-core SASS check (scripts/build_kernels.sh:120-150), applied to the AMD
-assembly of code built here.
+code only), for reading. The machine-code check itself -- the analogue of the reference's
+tensor-core SASS check (scripts/build_kernels.sh:120-150) -- is ``tests/test_build.py``: it
+unbundles the gfx950 code objects of the built library, disassembles them and asserts that every
+matrix kernel issues ``v_mfma`` instructions.
 """
 
 import argparse

@@ -52,7 +52,7 @@ KERNELS = tuple(_TABLE)
 
 
 def supported_capabilities():
-    """Give the architectures that this package contains."""
+    """Architectures with libraries in this package: only gfx950."""
     return _CAPABILITIES
 
 
@@ -65,54 +65,64 @@ def _normalise(cc):
 
 
 def _resolve(kernel, cc):
-    """Find the library and the FFI symbol for one kernel and one architecture."""
-    if kernel not in _TABLE:
+    """(architecture, library file name or None, FFI target or None) for ``kernel`` on ``cc``.
+
+    An unknown kernel name is a KeyError (the reference's message); an architecture this
+    package was not built for resolves to no library and no target.
+    """
+    entries = _TABLE.get(kernel)
+    if entries is None:
         raise KeyError(
             "unknown kernel %r, expected one of %s" % (kernel, ", ".join(KERNELS)))
-    cc = _normalise(cc)
-    if cc not in _CAPABILITIES:
-        return cc, None, None
-    for arch, lib, sym in _TABLE[kernel]:
-        if cc == arch:
-            return cc, lib, sym
-    return cc, None, None
+    arch = _normalise(cc)
+    match = next((e for e in entries if arch in _CAPABILITIES and e[0] == arch), None)
+    return (arch, None, None) if match is None else (arch, match[1], match[2])
 
 
 def _dirname(cc):
     return cc if isinstance(cc, str) else "sm%d" % cc
 
 
+def _missing(kernel, arch):
+    return FileNotFoundError("no %s kernel for architecture %s" % (kernel, arch))
+
+
 def kernel_dir(cc):
-    """Give the directory of the libraries for one architecture."""
-    cc, _, _ = _resolve("attention", cc)
-    return str(_KERNEL_DIR / _dirname(cc))
+    """Directory that holds (or would hold) the libraries built for ``cc``."""
+    arch = _resolve("attention", cc)[0]
+    return str(_KERNEL_DIR / _dirname(arch))
 
 
 def library_path(kernel, cc):
-    """Give the path of the library that supplies one kernel."""
-    cc, lib, _ = _resolve(kernel, cc)
+    """Absolute path of the shared library with ``kernel`` for ``cc``.
+
+    FileNotFoundError when the architecture has no build of it, or the file is absent.
+    """
+    arch, lib, _ = _resolve(kernel, cc)
     if lib is None:
-        raise FileNotFoundError("no %s kernel for architecture %s" % (kernel, cc))
-    path = _KERNEL_DIR / _dirname(cc) / lib
-    if not path.is_file():
-        raise FileNotFoundError("%s is not in this package" % path)
-    return str(path)
+        raise _missing(kernel, arch)
+    path = _KERNEL_DIR / _dirname(arch) / lib
+    if path.is_file():
+        return str(path)
+    raise FileNotFoundError("%s is not in this package" % path)
 
 
 def symbol(kernel, cc):
-    """Give the XLA FFI target name that the library exports."""
-    cc, lib, sym = _resolve(kernel, cc)
-    if sym is None:
-        raise FileNotFoundError("no %s kernel for architecture %s" % (kernel, cc))
-    return sym
+    """Name of the XLA FFI handler symbol for ``kernel`` exported by its library."""
+    arch, _, target = _resolve(kernel, cc)
+    if target is None:
+        raise _missing(kernel, arch)
+    return target
+
+
+def _present(kernel, cc):
+    try:
+        library_path(kernel, cc)
+    except (FileNotFoundError, KeyError):
+        return False
+    return True
 
 
 def available(cc, kernel=None):
-    """Tell if the kernels are present. With kernel=None, test all of them."""
-    names = KERNELS if kernel is None else (kernel,)
-    for name in names:
-        try:
-            library_path(name, cc)
-        except (FileNotFoundError, KeyError):
-            return False
-    return True
+    """True when ``kernel`` (every kernel, if None) has its library on disk for ``cc``."""
+    return all(_present(name, cc) for name in (KERNELS if kernel is None else (kernel,)))

@@ -838,7 +838,11 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkv2(
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r16 = lane & 15, g = lane >> 4;
-    const int k0 = blockIdx.x * KB, h = blockIdx.y, n = blockIdx.z;
+    // 1-D grid of (key block, head, row) work items, key block fastest, placed so that the key
+    // blocks of one (row, head) -- which stream the same Q and dO rows -- share an XCD's L2.
+    const int kblocks = (Sk + KB - 1) / KB;
+    const int item = xcd_contiguous(blockIdx.x, gridDim.x);
+    const int k0 = (item % kblocks) * KB, h = (item / kblocks) % H, n = item / (kblocks * H);
     const size_t nh = (size_t)n * H + h;
     const int kw0 = k0 + wave * KW;
     const bool active = kw0 < Sk;
@@ -1213,7 +1217,7 @@ void launch_dkv2(hipStream_t st, const BwdPlan& p, const void* q, const void* k,
                  const float* ndi, const float* rowl, void* dk, void* dv, int N, int H, int Sq,
                  int Sk, float scale) {
     using E = typename TR::elem;
-    const dim3 grid(ceil_div(Sk, 16 * KSUB * NW), H, N);
+    const dim3 grid(ceil_div(Sk, 16 * KSUB * NW) * H * N);
     KernelTimer timer("attn_bwd_dkv", st);
     attn_bwd_dkv2<TR, D, KSUB, NW, VEC><<<grid, 64 * NW, 0, st>>>(
         (const E*)q, (const E*)k, (const E*)v, (const E*)bias_t, kmask, (const E*)dout, lse2,

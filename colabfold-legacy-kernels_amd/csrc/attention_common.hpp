@@ -256,8 +256,8 @@ inline clk_status validate_attention(const char* who, clk_dtype dtype, int64_t N
                     who, (long long)N, (long long)H, (long long)Sq, (long long)Sk);
     if (N * H * (Sq > Sk ? Sq : Sk) * D > ((int64_t)1 << 40) || H * Sq * Sk > ((int64_t)1 << 40))
         return fail(CLK_INVALID_ARGUMENT, "%s: tensor too large", who);
-    if (N * H * ((Sq + 63) / 64) >= ((int64_t)1 << 31))  // 1-D grids of query tiles
-        return fail(CLK_INVALID_ARGUMENT, "%s: too many query tiles", who);
+    if (N * H * (((Sq > Sk ? Sq : Sk) + 63) / 64) >= ((int64_t)1 << 31))  // 1-D grids of tiles
+        return fail(CLK_INVALID_ARGUMENT, "%s: too many query or key tiles", who);
     return CLK_OK;
 }
 

@@ -43,7 +43,8 @@ template <bool VEC>
 __device__ __forceinline__ RowFlags row_flags(const uint8_t* mrow, int Sk) {
     const int lane = threadIdx.x & 63;
     const int ntiles = (Sk + 63) / 64;
-    uint64_t bits = Sk % 64 ? 1ull << (ntiles - 1) : 0ull;  // the ragged last tile
+    // The ragged last tile (tiles from the 64th on are always checked: no bit for them).
+    uint64_t bits = (Sk % 64 && ntiles <= 64) ? 1ull << (ntiles - 1) : 0ull;
     bool any_present = false;
     if (mrow) {
         for (int base = 0; base < Sk; base += 512) {
@@ -301,6 +302,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
             // skip the rescale of O and l (a wave-uniform branch).
             const bool move = mt * kLog2e > m_run[qt] * kLog2e + kRescaleSlack;
             if (__any(move)) {
+                // Opaque to if-conversion: without it the compiler runs the rescale on every
+                // tile (alpha = 1 when nothing moved gives the same values).
+                asm volatile("");
                 const float m_new = move ? mt : m_run[qt];
                 const float alpha = fast_exp2((m_run[qt] - m_new) * kLog2e);
                 m_run[qt] = m_new;

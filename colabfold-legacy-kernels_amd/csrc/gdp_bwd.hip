@@ -559,6 +559,22 @@ clk_status run_gdp_bwd(hipStream_t st, const void* x, const void* wp, const void
     return check_launch("gated_dual_proj_bwd");
 }
 
+// M = 0: the weight and bias gradients are sums over no rows, i.e. zero. The sum kernel with no
+// partials writes exactly that (a fill kernel, so the call stays graph-capturable).
+clk_status zero_gdp_bwd(hipStream_t st, float* dwp, float* dbp, float* dwg, float* dbg, int K,
+                        int N) {
+#define CLK_GDPZ(KK, NN)                                                                       \
+    if (K == (KK) && N == (NN)) {                                                              \
+        constexpr int count = 2 * NN * KK + 2 * NN;                                            \
+        gdp_bwd_sum_kernel<KK, NN><<<count / 64, 256, 0, st>>>(nullptr, 0, nullptr, 0, dwp,     \
+                                                               dwg, dbp, dbg);                 \
+        return check_launch("gated_dual_proj_bwd");                                             \
+    }
+    CLK_GDPZ(128, 128) CLK_GDPZ(64, 64) CLK_GDPZ(128, 64) CLK_GDPZ(64, 128)
+#undef CLK_GDPZ
+    return fail(CLK_INVALID_ARGUMENT, "gated_dual_proj_bwd: K=%d, N=%d not supported", K, N);
+}
+
 template <typename TR>
 clk_status dispatch_gdp_bwd(hipStream_t st, const void* x, const void* wp, const void* bp,
                             const void* wg, const void* bg, const void* mask, const void* dout,
@@ -598,7 +614,11 @@ extern "C" clk_status clk_gated_dual_proj_bwd(hipStream_t stream, clk_dtype dtyp
                     (long long)K, (long long)N);
     if (M * 2 * N * 2 >= ((int64_t)1 << 31) || M * K * 2 >= ((int64_t)1 << 31))
         return fail(CLK_INVALID_ARGUMENT, "%s: M=%lld too large", who, (long long)M);
-    if (M == 0) return ok();
+    if (M == 0) {
+        if (!dwp || !dbp || !dwg || !dbg)
+            return fail(CLK_INVALID_ARGUMENT, "%s: null gradient pointer", who);
+        return zero_gdp_bwd(stream, dwp, dbp, dwg, dbg, (int)K, (int)N);
+    }
     if (!x || !wp || !bp || !wg || !bg || !mask || !dout || !dx || !dwp || !dbp || !dwg || !dbg ||
         !workspace)
         return fail(CLK_INVALID_ARGUMENT, "%s: null operand pointer", who);

@@ -93,18 +93,24 @@ class Frame {
         return true;
     }
 
-    hipStream_t stream() const {
+    // Asks XLA for the platform stream of this call. On failure returns XLA's own error, which
+    // the handler passes back unchanged: launching on the default stream instead would leave the
+    // kernels unordered with XLA's work.
+    Error* fetch_stream() {
         StreamGetArgs a;
         a.struct_size = sizeof(StreamGetArgs);
         a.extension_start = nullptr;
         a.ctx = f_->ctx;
         a.stream = nullptr;
-        if (f_->api->stream_get(&a) != nullptr) return nullptr;
-        return static_cast<hipStream_t>(a.stream);
+        if (Error* e = f_->api->stream_get(&a)) return e;
+        stream_ = static_cast<hipStream_t>(a.stream);
+        return nullptr;
     }
+    hipStream_t stream() const { return stream_; }
 
    private:
     CallFrame* f_;
+    hipStream_t stream_ = nullptr;
 };
 
 // The metadata query XLA makes when it registers a handler: report the API version and traits.
@@ -127,6 +133,7 @@ Error* run(CallFrame* frame, Body body) {
     if (answer_metadata(frame)) return nullptr;
     if (frame->stage != kExecute) return nullptr;
     Frame f(frame);
+    if (Error* e = f.fetch_stream()) return e;
     const clk_status s = body(f);
     if (s == CLK_OK) return nullptr;
     return f.error(s, clk_last_error());

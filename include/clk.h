@@ -130,6 +130,7 @@ clk_status clk_gated_dual_proj(hipStream_t stream, clk_dtype dtype, const void* 
  * [K,N] and dbp, dbg [N] in float32. x, weights, biases, mask, dout, dx of dtype CLK_F16 or
  * CLK_BF16. K and N in {64, 128}. Deterministic: the weight and bias gradients are summed from
  * per-block partials in a fixed order. Workspace: clk_gated_dual_proj_bwd_workspace_size bytes.
+ * M = 0 writes zero weight and bias gradients (sums over no rows).
  */
 size_t clk_gated_dual_proj_bwd_workspace_size(int64_t M, int64_t K, int64_t N);
 clk_status clk_gated_dual_proj_bwd(hipStream_t stream, clk_dtype dtype, const void* x,

@@ -89,9 +89,10 @@ class FakeXla:
     """Owns an Api table whose Error_Create records (code, message) and whose Stream_Get returns
     a fixed stream handle; builds call frames and keeps every ctypes object alive."""
 
-    def __init__(self, stream=0):
+    def __init__(self, stream=0, stream_error=False):
         self.errors = []
         self.stream = stream
+        self.stream_gets = 0
         self._keep = []
 
         def error_create(args):
@@ -100,6 +101,9 @@ class FakeXla:
             return len(self.errors)  # any non-null pointer
 
         def stream_get(args):
+            self.stream_gets += 1
+            if stream_error:  # XLA's failure: a non-null error pointer, no stream
+                return 0xE5
             args.contents.stream = self.stream
             return None
 

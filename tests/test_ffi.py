@@ -145,3 +145,15 @@ def test_new_targets_decode_errors(lib):
                  [x.buffer(BF16, (4, 4, 4), FAKE)], [])
     assert x.call(lib, "ClkLnPairBias", fr) is not None
     assert "eps" in x.errors[-1][1]
+
+
+@pytest.mark.parametrize("name", TARGETS)
+def test_stream_get_failure_fails_the_call(lib, name):
+    """When XLA cannot hand over the platform stream the handler returns XLA's own error and
+    launches nothing (the frame's operands are fake addresses: a launch would fault)."""
+    x = FakeXla(stream_error=True)
+    fr = attention_frame(x) if "Attention" in name or name.startswith("VoltaMma") or \
+        name == "VoltaWmma" else x.frame([], [])
+    err = x.call(lib, name, fr)
+    assert err == 0xE5
+    assert x.stream_gets == 1 and x.errors == []

@@ -20,6 +20,7 @@ CASES = [
     (1, 1, 1, 1, 32, 0.0, 0),
     (2, 3, 257, 129, 32, 0.05, 1),
     (2, 2, 33, 300, 64, 0.0, 0),
+    (1, 1, 16, 4100, 32, 0.1, 0),  # more than 64 key tiles, ragged last tile
 ]
 
 

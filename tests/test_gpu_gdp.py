@@ -148,6 +148,23 @@ def test_gdp_bwd_parity(cuda, m, k, n, dtype):
         assert_close(name, a, b, tol)
 
 
+@pytest.mark.parametrize("k,n", [(128, 128), (64, 128)])
+def test_gdp_bwd_no_rows_gives_zero_weight_grads(cuda, k, n):
+    """M = 0: the weight and bias gradients are sums over no rows, so they must come back zero
+    even when their buffers held other values."""
+    dt = torch.bfloat16
+    w = [t.to(cuda) for t in gdp_weights(k, n, dt, seed=3, bias_std=0.3)]
+    x = torch.empty((0, k), device=cuda, dtype=dt)
+    mask = torch.empty((0,), device=cuda, dtype=dt)
+    dout = torch.empty((0, n), device=cuda, dtype=dt)
+    junk = [torch.full((k * n,), 7.0, device=cuda) for _ in range(8)]
+    del junk  # the gradients below reuse these nonzero blocks
+    dx, dwp, dbp, dwg, dbg = ops.gated_dual_proj_bwd(x, *w, mask, dout)
+    assert dx.shape == (0, k)
+    for t in (dwp, dbp, dwg, dbg):
+        assert torch.count_nonzero(t).item() == 0
+
+
 def test_gdp_bwd_accumulates_and_repeats(cuda):
     """dx accumulation (two branches reading one x) and bit-identical repeated runs."""
     dt = torch.bfloat16
