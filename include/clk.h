@@ -94,6 +94,24 @@ clk_status clk_attention_bwd(hipStream_t stream, clk_dtype dtype, const void* q,
                              int64_t D, float scale);
 
 /*
+ * Attention backward that allocates nothing. No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). Same operands and results as clk_attention_bwd, without the
+ * workspace: it uses the library's fixed per-GPU scratch array of
+ * clk_attention_bwd_noalloc_limit() bytes (64 MiB), held by each GPU from first use until the
+ * process ends. Sizes whose clk_attention_bwd_workspace_size() exceeds the limit are rejected
+ * with CLK_INVALID_ARGUMENT before any device work. Calls that overlap on one GPU (several
+ * streams or threads) share that array and race: serialise them.
+ */
+size_t clk_attention_bwd_noalloc_limit(void);
+clk_status clk_attention_bwd_noalloc(hipStream_t stream, clk_dtype dtype, const void* q,
+                                     const void* k, const void* v, const void* bias,
+                                     const uint8_t* kmask, const void* out, const void* dout,
+                                     const float* lse, void* dq, void* dk, void* dv,
+                                     float* dbias, int64_t N, int64_t H, int64_t Sq, int64_t Sk,
+                                     int64_t D, float scale);
+
+/*
  * LayerNorm forward over the last axis. Replaces VoltaLayerNorm (cuda/volta_ops.cu:62-95):
  * x and y of dtype CLK_F16, CLK_BF16 or CLK_F32; scale and offset float32; attribute eps.
  */

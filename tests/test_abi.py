@@ -95,6 +95,20 @@ def test_attention_bwd_validation():
     assert "head dim" in _native.last_error()
 
 
+def test_attention_bwd_noalloc_refuses_sizes_beyond_its_scratch():
+    """Host-side check before any device call: the 1024-residue problem needs more workspace
+    than the fixed scratch array holds."""
+    lib = _native.lib()
+    limit = lib.clk_attention_bwd_noalloc_limit()
+    assert limit == 64 << 20
+    dims = (1024, 4, 1024, 1024, 32)
+    assert lib.clk_attention_bwd_workspace_size(*dims) > limit
+    assert lib.clk_attention_bwd_noalloc(None, BF16, *([FAKE] * 12), *dims, 0.17) == INVALID
+    assert "scratch" in _native.last_error()
+    assert lib.clk_attention_bwd_noalloc(None, BF16, *([FAKE] * 12), -1, 4, 8, 8, 32,
+                                         0.17) == INVALID
+
+
 def test_workspace_sizes_are_deterministic():
     lib = _native.lib()
     a = lib.clk_attention_bwd_workspace_size(384, 4, 384, 384, 32)
