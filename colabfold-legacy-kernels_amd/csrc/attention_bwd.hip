@@ -490,8 +490,8 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
     float* __restrict__ row_logit, float* __restrict__ lse2_out,
     float* __restrict__ ndi_out, typename TR::elem* __restrict__ dq,
     float* __restrict__ dq_part, float* __restrict__ dbias_dst, int N, int H, int Sq, int Sk,
-    int NB, int nranges, float scale, typename TR::elem* __restrict__ bias_t, int SqP,
-    int tiles_q, int tiles_k) {
+    int NB, int nranges, float scale, LogitForm lf, typename TR::elem* __restrict__ bias_t,
+    int SqP, int tiles_q, int tiles_k) {
     using E = typename TR::elem;
     using V8 = typename TR::vec8;
     using T = SwzTile<D>;
@@ -503,8 +503,12 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
 
     __shared__ __attribute__((aligned(16))) char kv0[2 * KVB];
     __shared__ __attribute__((aligned(16))) char kv1[2 * KVB];
-    __shared__ __attribute__((aligned(16))) char qd0[3 * QB];
-    __shared__ __attribute__((aligned(16))) char qd1[3 * QB];
+    // Per-row extras staged with Q/dO/O when VEC: lse of the block's 64 queries (256 bytes),
+    // then the mask bytes of the key range (MSK bytes, whole waves of 4-byte loads).
+    constexpr int MSK = (RK + 255) / 256 * 256;
+    constexpr int XB = VEC ? 256 + MSK : 0;
+    __shared__ __attribute__((aligned(16))) char qd0[3 * QB + XB];
+    __shared__ __attribute__((aligned(16))) char qd1[3 * QB + XB];
     __shared__ __attribute__((aligned(16))) char xch_raw[8 * 2 * DT * 64 * 16];
     f32x4* const xch = reinterpret_cast<f32x4*>(xch_raw);
 
@@ -524,22 +528,26 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
 #pragma unroll
     for (int qt = 0; qt < 2; ++qt) qrow[qt] = q0 + 32 * qg + 16 * qt + r16;
 
-    // Resident bias: chunk i, sub-tile qt -> bias[h][qrow][kbeg + 32j + 8g + 0..7].
-    u32x4 braw[KCW][2];
+    // Resident bias in the logit form's units (bias * lf.bscale, float32), laid out as the
+    // accumulator input of S^T: chunk i, sub-tile qt, half t -> keys kbeg + 32j + 8g + 4t + 0..3
+    // of query qrow[qt] (j = i*KQ + kq). The S^T product then yields the logit up to the factor
+    // lf.cexp, and no per-row instruction touches the bias.
+    f32x4 bacc[KCW][2][2];
 #pragma unroll
     for (int i = 0; i < KCW; ++i)
 #pragma unroll
         for (int qt = 0; qt < 2; ++qt) {
             const int kk = kbeg + 32 * (i * KQ + kq) + 8 * g;
             const E* brow = bias + ((size_t)h * Sq + min(qrow[qt], Sq - 1)) * Sk;
+            float b[8];
             if constexpr (VEC) {
-                braw[i][qt] = ld16(brow + min(kk, Sk - 8));
+                unpack8<TR>(ld16(brow + min(kk, Sk - 8)), b);
             } else {
-                E e[8];
 #pragma unroll
-                for (int j = 0; j < 8; ++j) e[j] = kk + j < Sk ? brow[kk + j] : E(0.f);
-                __builtin_memcpy(&braw[i][qt], e, 16);
+                for (int j = 0; j < 8; ++j) b[j] = kk + j < Sk ? TR::to_f(brow[kk + j]) : 0.f;
             }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) bacc[i][qt][j >> 2][j & 3] = lf.bias_units(b[j]);
         }
 
     f32x4 dbias[KCW][2][2];
@@ -558,19 +566,30 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
         stage_rows<D, BQ, 512>(buffer_rsrc(q + nh * Sq * D, qb), q0, qd);
         stage_rows<D, BQ, 512>(buffer_rsrc(dout + nh * Sq * D, qb), q0, qd + QB);
         stage_rows<D, BQ, 512>(buffer_rsrc(out + nh * Sq * D, qb), q0, qd + 2 * QB);
+        if constexpr (VEC) {
+            // Queries past Sq and keys past Sk read zeros. Mask rows are 8-byte aligned (VEC).
+            char* ex = qd + 3 * QB;
+            if (wave == 0) buf_dma4(buffer_rsrc(lse + nh * Sq, (uint32_t)Sq * 4), lane * 4, q0 * 4, ex);
+            if (kmask && wave >= 1 && wave <= MSK / 256)
+                buf_dma4(buffer_rsrc(kmask + (size_t)n * Sk, (uint32_t)Sk),
+                         (64 * (wave - 1) + lane) * 4, kbeg, ex + 256 * wave);
+        }
     };
-    // Per-row values kept in registers one row ahead, raw: anything computed from them right
-    // after the load would wait for the row's direct-to-LDS loads too.
-    float lse_nx[2], ml_nx = kMaskedLogit;
-    u32x2 mask_nx[KCW];
+    // Per-row values kept in registers one row ahead when they are not staged (not VEC), raw:
+    // anything computed from them right after the load would wait for the row's direct-to-LDS
+    // loads too.
+    float lse_nx[VEC ? 1 : 2], ml_nx = kMaskedLogit;
+    u32x2 mask_nx[VEC ? 1 : KCW];
     auto prefetch = [&](int n) {
-        const size_t nh = (size_t)n * H + h;
+        if constexpr (!VEC) {
+            const size_t nh = (size_t)n * H + h;
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) lse_nx[qt] = lse[nh * Sq + min(qrow[qt], Sq - 1)];
-        const uint8_t* mrow = kmask ? kmask + (size_t)n * Sk : nullptr;
+            for (int qt = 0; qt < 2; ++qt) lse_nx[qt] = lse[nh * Sq + min(qrow[qt], Sq - 1)];
+            const uint8_t* mrow = kmask ? kmask + (size_t)n * Sk : nullptr;
 #pragma unroll
-        for (int i = 0; i < KCW; ++i)
-            mask_nx[i] = mask_bytes8<VEC>(mrow, kbeg + 32 * (i * KQ + kq) + 8 * g, Sk);
+            for (int i = 0; i < KCW; ++i)
+                mask_nx[i] = mask_bytes8<VEC>(mrow, kbeg + 32 * (i * KQ + kq) + 8 * g, Sk);
+        }
         ml_nx = kmask ? row_logit[n] : kMaskedLogit;
     };
 
@@ -598,19 +617,33 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
         const size_t nh = (size_t)n * H + h;
         async_wait();
         __syncthreads();  // row n in (kvc, qdc); every wave is done with row n-1
-        // The packed bias is loop-invariant; hiding that keeps the compiler from hoisting its
-        // unpacked (twice as large) form out of the row loop.
-#pragma unroll
-        for (int i = 0; i < KCW; ++i)
-#pragma unroll
-            for (int qt = 0; qt < 2; ++qt) asm volatile("" : "+v"(braw[i][qt]));
         float lse2c[2];
-#pragma unroll
-        for (int qt = 0; qt < 2; ++qt) lse2c[qt] = qrow[qt] < Sq ? lse_nx[qt] * kLog2e : INFINITY;
         const float mlc = ml_nx;
-        u32x2 maskc[KCW];
+        // Presence bits of this wave's keys: chunk i in bits 8i .. 8i+7 (one register).
+        unsigned vbits = 0;
+        if constexpr (VEC) {
+            const char* ex = qdc + 3 * QB;
 #pragma unroll
-        for (int i = 0; i < KCW; ++i) maskc[i] = mask_nx[i];
+            for (int qt = 0; qt < 2; ++qt)
+                lse2c[qt] = qrow[qt] < Sq
+                                ? reinterpret_cast<const float*>(ex)[32 * qg + 16 * qt + r16] * kLog2e
+                                : INFINITY;
+            if (kmask) {
+#pragma unroll
+                for (int i = 0; i < KCW; ++i)
+                    vbits |= nonzero_bits8(*reinterpret_cast<const u32x2*>(
+                                 ex + 256 + 32 * (i * KQ + kq) + 8 * g))
+                             << (8 * i);
+            } else {
+                vbits = 0xffffffu;
+            }
+        } else {
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt)
+                lse2c[qt] = qrow[qt] < Sq ? lse_nx[qt] * kLog2e : INFINITY;
+#pragma unroll
+            for (int i = 0; i < KCW; ++i) vbits |= nonzero_bits8(mask_nx[i]) << (8 * i);
+        }
 
         V8 qf[2], dof[2];
         float di[2];
@@ -618,6 +651,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
         for (int qt = 0; qt < 2; ++qt) {
             const int row = 32 * qg + 16 * qt + r16;
             qf[qt] = swz_row_operand<V8, D>(qdc, row, 0, g);
+            if (lf.qzero) qf[qt] = V8{};
             dof[qt] = swz_row_operand<V8, D>(qdc + QB, row, 0, g);
             const V8 of = swz_row_operand<V8, D>(qdc + 2 * QB, row, 0, g);
             // Packed pair dot products: the element products are exact in float32.
@@ -669,23 +703,26 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
             for (int t = 0; t < 2; ++t)
 #pragma unroll
                 for (int qt = 0; qt < 2; ++qt) {
-                    s[qt][t] = TR::mfma(kf[t], qf[qt], f32x4{0.f, 0.f, 0.f, 0.f});
+                    s[qt][t] = TR::mfma(kf[t], qf[qt], bacc[i][qt][t]);
                     dp[qt][t] = TR::mfma(vf[t], dof[qt], f32x4{-di[qt], -di[qt], -di[qt], -di[qt]});
                 }
-            const bool nm = kbeg + c0 + 32 > Sk || __any(has_zero_byte(maskc[i]));
+            const unsigned valid = (vbits >> (8 * i)) & 0xffu;
+            const bool nm = kbeg + c0 + 32 > Sk || __any(valid != 0xffu);
+            // x = log2(P) = logit * log2(e) - lse * log2(e), one FMA per score.
             float x[2][8];
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt) {
-                float b[8];
-                unpack8<TR>(braw[i][qt], b);
+            for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) x[qt][j] = fmaf(s[qt][j >> 2][j & 3], scale, b[j]);
-            }
+                for (int j = 0; j < 8; ++j)
+                    x[qt][j] = fmaf(s[qt][j >> 2][j & 3], lf.cexp, -lse2c[qt]);
             if (nm) {
                 // One block for the chunk, opaque to speculation: nothing of it is hoisted into
                 // (or merged across sub-tiles onto) the unmasked path.
                 asm volatile("");
-                const unsigned valid = nonzero_bits8(maskc[i]);
+                // An absent key's log2(P): its row's masked logit, in the same units.
+                float mx[2];
+#pragma unroll
+                for (int qt = 0; qt < 2; ++qt) mx[qt] = fmaf(mlc, kLog2e, -lse2c[qt]);
                 if (kbeg + c0 + 32 > Sk) {  // wave-uniform: the chunk runs past the last key
                     int lim = Sk - (kbeg + c0 + 8 * g);  // keys j >= lim are past Sk
                     // Opaque, so the eight compares are not hoisted out of the row loop (their
@@ -696,17 +733,17 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
 #pragma unroll
                         for (int j = 0; j < 8; ++j)
                             x[qt][j] = j >= lim ? -INFINITY
-                                                : (((valid >> j) & 1u) ? x[qt][j] : mlc);
+                                                : (((valid >> j) & 1u) ? x[qt][j] : mx[qt]);
                 } else {
                     // Bit j of `valid` spread over a word (0 or ~0) selects x or the absent
-                    // key's logit bitwise.
+                    // key's value bitwise.
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
                         const int sel = __builtin_amdgcn_sbfe((int)valid, j, 1);
 #pragma unroll
                         for (int qt = 0; qt < 2; ++qt)
                             x[qt][j] = __int_as_float((sel & __float_as_int(x[qt][j])) |
-                                                      (~sel & __float_as_int(mlc)));
+                                                      (~sel & __float_as_int(mx[qt])));
                     }
                 }
             }
@@ -715,7 +752,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
             for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const float p = fast_exp2(fmaf(x[qt][j], kLog2e, -lse2c[qt]));
+                    const float p = fast_exp2(x[qt][j]);
                     const float ds = p * dp[qt][j >> 2][j & 3];
                     dbias[i][qt][j >> 2][j & 3] += ds;
                     dsf[qt][j] = TR::from_f(ds);
@@ -1208,7 +1245,8 @@ void launch_dq2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, 
     attn_bwd_dq2<TR, D, KCW, VEC><<<grid, 512, 0, st>>>(
         (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (const E*)out,
         (const E*)dout, lse, rowl, lse2, ndi, (E*)dq, dq_part, dbias_dst, N, H, Sq, Sk, p.NB,
-        p.nranges, scale, (E*)bias_t, p.SqP, ceil_div(p.SqP, 64), ceil_div(Sk, 64));
+        p.nranges, scale, LogitForm::make(scale), (E*)bias_t, p.SqP, ceil_div(p.SqP, 64),
+        ceil_div(Sk, 64));
 }
 
 template <typename TR, int D, int KSUB, int NW, bool VEC>

@@ -238,6 +238,25 @@ __device__ __forceinline__ void store4(typename TR::elem* p, f32x4 v) {
     st8(p, raw);
 }
 
+// How the backward kernels form log2(P) with one FMA per score: the MFMA that computes q.k
+// takes the bias, in "bias units", as its accumulator input, so its result r = q.k + bias*bscale
+// and log2(e) * logit = cexp * r. For scale != 0: bscale = 1/scale, cexp = scale*log2(e). For a
+// scale too small to invert (|scale| < 2^-100, including 0) the logit is the bias alone to
+// float32 precision: Q is replaced by zeros, bscale = 1, cexp = log2(e). A bias whose scaled
+// value exceeds 1e38 in magnitude saturates there (NaN stays NaN).
+struct LogitForm {
+    float bscale, cexp;
+    int qzero;
+    static LogitForm make(float scale) {
+        if (fabsf(scale) < 0x1p-100f) return {1.f, kLog2e, 1};
+        return {1.f / scale, scale * kLog2e, 0};
+    }
+    __device__ __forceinline__ float bias_units(float b) const {
+        const float v = b * bscale;
+        return fabsf(v) > 1e38f ? copysignf(1e38f, v) : v;
+    }
+};
+
 // Host-side shape/dtype validation shared by the forward and backward entry points. The
 // reference checks only the rank of q (cuda/volta_mma_attn.cu:310-314); every size is checked
 // here before any launch.
