@@ -194,6 +194,24 @@ def bench_layer_norm(torch, workloads, native, dev, stream, steps, warmup):
     }
 
 
+def bench_hbm_copy(torch, native, dev, stream, steps, warmup):
+    """The library's own streaming copy (clk_stream_copy) of 512 MiB, two rotating buffer pairs
+    (2 GiB): the HBM rate its HBM-bound kernels can reach, read + write bytes per second."""
+    lib = native.lib()
+    nbytes = 512 << 20
+    pairs = [(torch.empty(nbytes, device=dev, dtype=torch.uint8).fill_(r),
+              torch.empty(nbytes, device=dev, dtype=torch.uint8)) for r in range(2)]
+
+    def run(i):
+        a, b = pairs[i % 2]
+        st = lib.clk_stream_copy(stream, a.data_ptr(), b.data_ptr(), nbytes)
+        if st != 0:
+            raise RuntimeError(native.last_error())
+
+    t = timed(torch, run, steps, warmup, torch.cuda.current_stream(dev))
+    return {"hbm_copy_GBps": 2.0 * nbytes / (t * 1e-3) / 1e9, "hbm_copy_ms": t}
+
+
 def bench_ln_gdp(torch, workloads, native, dev, stream, steps, warmup):
     """LayerNorm + both gated branches on z [512*512, 128] bf16 (a, b [512*512, 128])."""
     m, c, n = 512 * 512, 128, 128
@@ -488,13 +506,18 @@ def main(argv=None):
         "kernels_ms_per_step": per_step,
     }
     if not args.no_secondary:
+        print("bench: timing the streaming copy", file=sys.stderr, flush=True)
+        sec = bench_hbm_copy(torch, native, dev, stream, args.steps, args.warmup)
         print("bench: timing LayerNorm", file=sys.stderr, flush=True)
-        sec = bench_layer_norm(torch, workloads, native, dev, stream, args.steps, args.warmup)
+        sec.update(bench_layer_norm(torch, workloads, native, dev, stream, args.steps,
+                                    args.warmup))
         print("bench: timing the attention step in float16", file=sys.stderr, flush=True)
         sec.update(bench_attention_f16(torch, workloads, native, dev, stream, args.steps,
                                        args.warmup))
         sec["ln_fwd_frac_hbm"] = sec["ln_fwd_GBps"] / HBM_PEAK
         sec["ln_bwd_frac_hbm"] = sec["ln_bwd_GBps"] / HBM_PEAK
+        sec["ln_fwd_frac_copy"] = sec["ln_fwd_GBps"] / sec["hbm_copy_GBps"]
+        sec["ln_bwd_frac_copy"] = sec["ln_bwd_GBps"] / sec["hbm_copy_GBps"]
         print("bench: timing LayerNorm + gated dual projection", file=sys.stderr, flush=True)
         sec.update(bench_ln_gdp(torch, workloads, native, dev, stream, args.steps, args.warmup))
         sec["ln_gdp_frac_hbm"] = sec["ln_gdp_GBps"] / HBM_PEAK

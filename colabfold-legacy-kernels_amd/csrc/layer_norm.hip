@@ -14,6 +14,11 @@ namespace clk {
 namespace {
 
 constexpr int kThreads = 256;
+// Row blocking, chosen by measurement on [512*512, 128] bf16 (each block owns a contiguous run
+// of rows; the forward is fastest with one round of 16 rows per block, the backward with eight
+// rounds of two rows per lane, which also keeps its partial column sums few).
+constexpr int kFwdRowsPerLane = 1, kFwdRounds = 1;
+constexpr int kBwdRowsPerLane = 2, kBwdRounds = 8;
 
 template <typename TR>
 struct Vec {
@@ -62,11 +67,21 @@ __device__ __forceinline__ float row_sum(float v) {
     return group_sum<LPR>(v);
 }
 
-template <typename TR, int LPR, int NV>
+// Stores of results that nothing in the kernel reads again: non-temporal, so they stream to HBM
+// without displacing inputs still to be read from the caches.
+__device__ __forceinline__ void st16_stream(void* p, u32x4 v) {
+    __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
+
+// Forward. A lane group of LPR lanes owns a row; each lane handles RB rows per round (rows
+// row0 + r*stride), issuing all RB*NV 16-byte loads before any arithmetic so that RB loads per
+// lane are in flight.
+template <typename TR, int LPR, int NV, int RB>
 __global__ __launch_bounds__(kThreads) void ln_fwd_kernel(const void* __restrict__ xv,
                                                           const float* __restrict__ scale,
                                                           const float* __restrict__ offset,
-                                                          void* __restrict__ yv, int M, float eps) {
+                                                          void* __restrict__ yv, int M,
+                                                          int rows_per_block, float eps) {
     using E = typename TR::elem;
     constexpr int VEC = Vec<TR>::N;
     constexpr int C = LPR * NV * VEC;
@@ -75,6 +90,7 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_kernel(const void* __restrict
     E* y = static_cast<E*>(yv);
     const int s = threadIdx.x % LPR;
     const int slot = threadIdx.x / LPR;
+    const int stride = gridDim.x * ROWS;
 
     float g[NV][VEC], b[NV][VEC];
 #pragma unroll
@@ -86,34 +102,83 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_kernel(const void* __restrict
             b[v][i] = offset[c];
         }
 
-    for (int row = blockIdx.x * ROWS + slot; row < M; row += gridDim.x * ROWS) {
-        const E* xr = x + (size_t)row * C;
-        float xs[NV][VEC];
+    // Block b owns the contiguous rows [b*rpb, (b+1)*rpb): consecutive blocks stream
+    // consecutive memory, which spreads the traffic over the HBM channels best.
+    const int rpb = rows_per_block;
+    const int rend = min(M, (blockIdx.x + 1) * rpb);
+    (void)stride;
+    for (int row0 = blockIdx.x * rpb + slot; row0 < rend; row0 += RB * ROWS) {
+        u32x4 raw[RB][NV];
 #pragma unroll
-        for (int v = 0; v < NV; ++v) unpack<TR>(ld16(xr + (v * LPR + s) * VEC), xs[v]);
-        float sum = 0.f;
+        for (int r = 0; r < RB; ++r) {
+            const int row = row0 + r * ROWS;
 #pragma unroll
-        for (int v = 0; v < NV; ++v)
+            for (int v = 0; v < NV; ++v)
+                raw[r][v] = row < rend ? ld16(x + (size_t)row * C + (v * LPR + s) * VEC)
+                                       : u32x4{0u, 0u, 0u, 0u};
+        }
 #pragma unroll
-            for (int i = 0; i < VEC; ++i) sum += xs[v][i];
-        float mean = sum * (1.f / (NV * VEC));
-        float m2 = 0.f;
+        for (int r = 0; r < RB; ++r) {
+            // Rows past the block's range run on zeros (every lane of a group takes part in the
+            // reductions) and store nothing.
+            const int row = row0 + r * ROWS;
+            float xs[NV][VEC];
 #pragma unroll
-        for (int v = 0; v < NV; ++v)
+            for (int v = 0; v < NV; ++v) unpack<TR>(raw[r][v], xs[v]);
+            float sum = 0.f;
 #pragma unroll
-            for (int i = 0; i < VEC; ++i) {
-                const float d = xs[v][i] - mean;
-                m2 += d * d;
+            for (int v = 0; v < NV; ++v)
+#pragma unroll
+                for (int i = 0; i < VEC; ++i) sum += xs[v][i];
+            float mean = sum * (1.f / (NV * VEC));
+            float m2 = 0.f;
+#pragma unroll
+            for (int v = 0; v < NV; ++v)
+#pragma unroll
+                for (int i = 0; i < VEC; ++i) {
+                    const float d = xs[v][i] - mean;
+                    m2 += d * d;
+                }
+            merge_stats<LPR>(mean, m2, (float)(NV * VEC));
+            const float rstd = rsqrtf(m2 * (1.f / C) + eps);
+            if (row < rend) {
+                E* yr = y + (size_t)row * C;
+#pragma unroll
+                for (int v = 0; v < NV; ++v) {
+                    float o[VEC];
+#pragma unroll
+                    for (int i = 0; i < VEC; ++i)
+                        o[i] = (xs[v][i] - mean) * rstd * g[v][i] + b[v][i];
+                    st16_stream(yr + (v * LPR + s) * VEC, pack<TR>(o));
+                }
             }
-        merge_stats<LPR>(mean, m2, (float)(NV * VEC));
-        const float rstd = rsqrtf(m2 * (1.f / C) + eps);
-        E* yr = y + (size_t)row * C;
+        }
+    }
+}
+
+// Streaming copy with the LayerNorm kernels' access pattern (16-byte loads, four per lane in
+// flight before the stores, non-temporal stores): the HBM rate this library can reach with its
+// own code, against which the LayerNorm and projection kernels are measured.
+// Block b copies the contiguous 16-byte vectors [b*kCopyChunk, (b+1)*kCopyChunk) (32 KiB), four
+// per thread in flight per round.
+constexpr int kCopyChunk = 2048;
+__global__ __launch_bounds__(kThreads) void stream_copy_kernel(const u32x4* __restrict__ src,
+                                                               u32x4* __restrict__ dst,
+                                                               size_t n16) {
+    constexpr int RB = 4;
+    const size_t beg = (size_t)blockIdx.x * kCopyChunk;
+    const size_t end = beg + kCopyChunk < n16 ? beg + kCopyChunk : n16;
+    for (size_t i0 = beg + threadIdx.x; i0 < end; i0 += RB * kThreads) {
+        u32x4 v[RB];
 #pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            float o[VEC];
+        for (int r = 0; r < RB; ++r) {
+            const size_t i = i0 + r * kThreads;
+            v[r] = i < end ? src[i] : u32x4{0u, 0u, 0u, 0u};
+        }
 #pragma unroll
-            for (int i = 0; i < VEC; ++i) o[i] = (xs[v][i] - mean) * rstd * g[v][i] + b[v][i];
-            st16(yr + (v * LPR + s) * VEC, pack<TR>(o));
+        for (int r = 0; r < RB; ++r) {
+            const size_t i = i0 + r * kThreads;
+            if (i < end) st16_stream(dst + i, v[r]);
         }
     }
 }
@@ -152,13 +217,13 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_generic(const void* __restric
 // Backward. Per row: dx = r*(g - mean(g) - xhat*mean(g*xhat)), g = scale*dy. Column sums of
 // dy*xhat and dy accumulate per lane over the rows the lane visits, then over the block's row
 // slots in a fixed order, into part[block][2][C]; ln_colsum adds the blocks in a fixed order.
-template <typename TR, int LPR, int NV>
+template <typename TR, int LPR, int NV, int RB>
 __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const void* __restrict__ xv,
                                                           const float* __restrict__ scale,
                                                           const void* __restrict__ dyv,
                                                           void* __restrict__ dxv,
                                                           float* __restrict__ part, int M,
-                                                          float eps) {
+                                                          int rows_per_block, float eps) {
     using E = typename TR::elem;
     constexpr int VEC = Vec<TR>::N;
     constexpr int C = LPR * NV * VEC;
@@ -168,6 +233,8 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const void* __restrict
     E* dx = static_cast<E*>(dxv);
     const int s = threadIdx.x % LPR;
     const int slot = threadIdx.x / LPR;
+    // Block b owns the contiguous rows [b*rows_per_block, (b+1)*rows_per_block).
+    const int rend = min(M, (blockIdx.x + 1) * rows_per_block);
 
     float g[NV][VEC], acc_g[NV][VEC], acc_b[NV][VEC];
 #pragma unroll
@@ -179,52 +246,76 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const void* __restrict
             acc_b[v][i] = 0.f;
         }
 
-    for (int row = blockIdx.x * ROWS + slot; row < M; row += gridDim.x * ROWS) {
-        const size_t base = (size_t)row * C;
-        float xs[NV][VEC], ds[NV][VEC];
+    // RB rows per lane per round, all their loads issued before any arithmetic. Rows past M run
+    // on zeros (every lane of a group takes part in the reductions), add zero to the column
+    // sums and store nothing.
+    for (int row0 = blockIdx.x * rows_per_block + slot; row0 < rend; row0 += RB * ROWS) {
+        u32x4 rx[RB][NV], rd[RB][NV];
 #pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            unpack<TR>(ld16(x + base + (v * LPR + s) * VEC), xs[v]);
-            unpack<TR>(ld16(dy + base + (v * LPR + s) * VEC), ds[v]);
+        for (int r = 0; r < RB; ++r) {
+            const int row = row0 + r * ROWS;
+            const size_t base = (size_t)row * C;
+#pragma unroll
+            for (int v = 0; v < NV; ++v) {
+                rx[r][v] = u32x4{0u, 0u, 0u, 0u};
+                rd[r][v] = u32x4{0u, 0u, 0u, 0u};
+                if (row < rend) {
+                    rx[r][v] = ld16(x + base + (v * LPR + s) * VEC);
+                    rd[r][v] = ld16(dy + base + (v * LPR + s) * VEC);
+                }
+            }
         }
-        float sum = 0.f;
 #pragma unroll
-        for (int v = 0; v < NV; ++v)
+        for (int r = 0; r < RB; ++r) {
+            const int row = row0 + r * ROWS;
+            const size_t base = (size_t)row * C;
+            float xs[NV][VEC], ds[NV][VEC];
 #pragma unroll
-            for (int i = 0; i < VEC; ++i) sum += xs[v][i];
-        float mean = sum * (1.f / (NV * VEC));
-        float m2 = 0.f;
-#pragma unroll
-        for (int v = 0; v < NV; ++v)
-#pragma unroll
-            for (int i = 0; i < VEC; ++i) {
-                const float d = xs[v][i] - mean;
-                m2 += d * d;
+            for (int v = 0; v < NV; ++v) {
+                unpack<TR>(rx[r][v], xs[v]);
+                unpack<TR>(rd[r][v], ds[v]);
             }
-        merge_stats<LPR>(mean, m2, (float)(NV * VEC));
-        const float rstd = rsqrtf(m2 * (1.f / C) + eps);
-        float sg = 0.f, sgx = 0.f;
+            float sum = 0.f;
 #pragma unroll
-        for (int v = 0; v < NV; ++v)
+            for (int v = 0; v < NV; ++v)
 #pragma unroll
-            for (int i = 0; i < VEC; ++i) {
-                const float xh = (xs[v][i] - mean) * rstd;
-                const float gg = g[v][i] * ds[v][i];
-                xs[v][i] = xh;
-                sg += gg;
-                sgx += gg * xh;
-                acc_g[v][i] += ds[v][i] * xh;
-                acc_b[v][i] += ds[v][i];
+                for (int i = 0; i < VEC; ++i) sum += xs[v][i];
+            float mean = sum * (1.f / (NV * VEC));
+            float m2 = 0.f;
+#pragma unroll
+            for (int v = 0; v < NV; ++v)
+#pragma unroll
+                for (int i = 0; i < VEC; ++i) {
+                    const float d = xs[v][i] - mean;
+                    m2 += d * d;
+                }
+            merge_stats<LPR>(mean, m2, (float)(NV * VEC));
+            const float rstd = rsqrtf(m2 * (1.f / C) + eps);
+            float sg = 0.f, sgx = 0.f;
+#pragma unroll
+            for (int v = 0; v < NV; ++v)
+#pragma unroll
+                for (int i = 0; i < VEC; ++i) {
+                    const float xh = (xs[v][i] - mean) * rstd;
+                    const float gg = g[v][i] * ds[v][i];
+                    xs[v][i] = xh;
+                    sg += gg;
+                    sgx += gg * xh;
+                    acc_g[v][i] += ds[v][i] * xh;
+                    acc_b[v][i] += ds[v][i];
+                }
+            sg = row_sum<LPR>(sg) * (1.f / C);
+            sgx = row_sum<LPR>(sgx) * (1.f / C);
+            if (row < rend) {
+#pragma unroll
+                for (int v = 0; v < NV; ++v) {
+                    float o[VEC];
+#pragma unroll
+                    for (int i = 0; i < VEC; ++i)
+                        o[i] = rstd * (g[v][i] * ds[v][i] - sg - xs[v][i] * sgx);
+                    st16_stream(dx + base + (v * LPR + s) * VEC, pack<TR>(o));
+                }
             }
-        sg = row_sum<LPR>(sg) * (1.f / C);
-        sgx = row_sum<LPR>(sgx) * (1.f / C);
-#pragma unroll
-        for (int v = 0; v < NV; ++v) {
-            float o[VEC];
-#pragma unroll
-            for (int i = 0; i < VEC; ++i)
-                o[i] = rstd * (g[v][i] * ds[v][i] - sg - xs[v][i] * sgx);
-            st16(dx + base + (v * LPR + s) * VEC, pack<TR>(o));
         }
     }
 
@@ -363,6 +454,17 @@ int fwd_blocks(int64_t M, int rows_per_block) {
     const int64_t b = (M + rows_per_block - 1) / rows_per_block;
     return (int)(b < 4096 ? b : 4096);
 }
+// Rows per block of the fast backward: kBwdRounds times the block's row slots (rounds of
+// kBwdRowsPerLane rows per lane cover it in kBwdRounds / kBwdRowsPerLane), and few enough blocks that the partial column sums stay within the generic
+// path's workspace (kMaxBwdBlocks * 5 partial rows).
+int fast_bwd_rows_per_block(int64_t M, int lpr) {
+    const int64_t round = kThreads / lpr;
+    int64_t rpb = round * kBwdRounds;
+    const int64_t cap_blocks = (int64_t)kMaxBwdBlocks * (kThreads / 64 + 1);
+    while ((M + rpb - 1) / rpb > cap_blocks) rpb += round;
+    return (int)rpb;
+}
+
 int bwd_blocks(int64_t M, int rows_per_block) {
     const int64_t b = (M + rows_per_block - 1) / rows_per_block;
     return (int)(b < kMaxBwdBlocks ? b : kMaxBwdBlocks);
@@ -520,9 +622,12 @@ bool dispatch_bias(hipStream_t st, const void* x, const float* sc, const float* 
 template <typename TR, int LPR, int NV>
 void launch_fwd(hipStream_t st, const void* x, const float* sc, const float* of, void* y, int M,
                 float eps) {
-    const int grid = fwd_blocks(M, kThreads / LPR);
+    constexpr int RB = kFwdRowsPerLane;
+    constexpr int ROWS = kThreads / LPR;
+    const int rpb = ROWS * RB * kFwdRounds;
+    const int grid = ceil_div(M, rpb);
     KernelTimer timer("ln_fwd", st);
-    ln_fwd_kernel<TR, LPR, NV><<<grid, kThreads, 0, st>>>(x, sc, of, y, M, eps);
+    ln_fwd_kernel<TR, LPR, NV, RB><<<grid, kThreads, 0, st>>>(x, sc, of, y, M, rpb, eps);
 }
 
 template <typename TR>
@@ -547,9 +652,11 @@ bool dispatch_fwd(hipStream_t st, const void* x, const float* sc, const float* o
 template <typename TR, int LPR, int NV>
 void launch_bwd(hipStream_t st, const void* x, const float* sc, const void* dy, void* dx,
                 float* part, int M, float eps) {
-    const int grid = bwd_blocks(M, kThreads / LPR);
+    constexpr int RB = kBwdRowsPerLane;
+    const int rpb = fast_bwd_rows_per_block(M, LPR);
+    const int grid = ceil_div(M, rpb);
     KernelTimer timer("ln_bwd", st);
-    ln_bwd_kernel<TR, LPR, NV><<<grid, kThreads, 0, st>>>(x, sc, dy, dx, part, M, eps);
+    ln_bwd_kernel<TR, LPR, NV, RB><<<grid, kThreads, 0, st>>>(x, sc, dy, dx, part, M, rpb, eps);
 }
 
 // Returns the number of partial rows written and their stride (floats).
@@ -560,7 +667,7 @@ void dispatch_bwd(hipStream_t st, const void* x, const float* sc, const void* dy
 #define CLK_LN_CASE(L, V)                                          \
     if (rs.lpr == (L) && rs.nv == (V)) {                           \
         launch_bwd<TR, L, V>(st, x, sc, dy, dx, part, M, eps);     \
-        *nblocks = bwd_blocks(M, kThreads / (L));                  \
+        *nblocks = ceil_div(M, fast_bwd_rows_per_block(M, L));     \
         *stride = 2 * (size_t)C;                                   \
         return;                                                    \
     }
@@ -601,6 +708,23 @@ clk_status validate(const char* who, clk_dtype dtype, const void* x, const float
 }  // namespace clk
 
 using namespace clk;
+
+extern "C" clk_status clk_stream_copy(hipStream_t stream, const void* src, void* dst,
+                                      size_t bytes) {
+    if (bytes == 0) return ok();
+    if (!src || !dst || !aligned16(src) || !aligned16(dst) || bytes % 16)
+        return fail(CLK_INVALID_ARGUMENT,
+                    "stream_copy: src and dst must be 16-byte aligned, bytes a multiple of 16");
+    const size_t n16 = bytes / 16;
+    const size_t blocks = (n16 + kCopyChunk - 1) / kCopyChunk;
+    if (blocks >= ((size_t)1 << 31))
+        return fail(CLK_INVALID_ARGUMENT, "stream_copy: %zu bytes too large", bytes);
+    const int grid = (int)blocks;
+    KernelTimer timer("stream_copy", stream);
+    stream_copy_kernel<<<grid, kThreads, 0, stream>>>(static_cast<const u32x4*>(src),
+                                                      static_cast<u32x4*>(dst), n16);
+    return check_launch("stream_copy");
+}
 
 extern "C" clk_status clk_layer_norm_fwd(hipStream_t stream, clk_dtype dtype, const void* x,
                                          const float* scale, const float* offset, void* y,

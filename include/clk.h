@@ -112,6 +112,13 @@ clk_status clk_attention_bwd_noalloc(hipStream_t stream, clk_dtype dtype, const 
                                      int64_t D, float scale);
 
 /*
+ * Streaming device-to-device copy of `bytes` bytes (16-byte aligned, a multiple of 16) with the
+ * access pattern of this library's HBM-bound kernels. No reference counterpart: it is the
+ * measured HBM ceiling the benchmark reports the LayerNorm and projection rates against.
+ */
+clk_status clk_stream_copy(hipStream_t stream, const void* src, void* dst, size_t bytes);
+
+/*
  * LayerNorm forward over the last axis. Replaces VoltaLayerNorm (cuda/volta_ops.cu:62-95):
  * x and y of dtype CLK_F16, CLK_BF16 or CLK_F32; scale and offset float32; attribute eps.
  */

@@ -109,6 +109,14 @@ def test_attention_bwd_noalloc_refuses_sizes_beyond_its_scratch():
                                          0.17) == INVALID
 
 
+def test_stream_copy_validation():
+    lib = _native.lib()
+    assert lib.clk_stream_copy(None, FAKE, FAKE, 0) == _native.OK
+    assert lib.clk_stream_copy(None, FAKE, FAKE, 40) == INVALID       # not a multiple of 16
+    assert lib.clk_stream_copy(None, FAKE + 8, FAKE, 64) == INVALID   # misaligned
+    assert lib.clk_stream_copy(None, None, FAKE, 64) == INVALID
+
+
 def test_workspace_sizes_are_deterministic():
     lib = _native.lib()
     a = lib.clk_attention_bwd_workspace_size(384, 4, 384, 384, 32)

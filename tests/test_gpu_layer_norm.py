@@ -94,3 +94,17 @@ def test_ln_pair_bias_parity(cuda, sq, sk, c, h, dtype):
     out = ops.ln_pair_bias(z.to(cuda), sc.to(cuda), of.to(cuda), w.to(cuda))
     r = ref.ln_pair_bias(np64(z), np64(sc), np64(of), np64(w))
     assert_close("bias", out, r, TOL[dname(dtype)]["ln"])
+
+
+@pytest.mark.parametrize("nbytes", [16, 4096 + 48, 3 << 20])
+def test_stream_copy(cuda, nbytes):
+    """The HBM ceiling probe copies exactly (ragged tails included)."""
+    from colabfold_legacy_kernels import _native
+    a = torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device=cuda)
+    b = torch.zeros_like(a)
+    lib = _native.lib()
+    st = lib.clk_stream_copy(torch.cuda.current_stream(cuda).cuda_stream, a.data_ptr(),
+                             b.data_ptr(), nbytes)
+    assert st == _native.OK, _native.last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
