@@ -94,8 +94,11 @@ def build(jobs=None, asm=False, verbose=True):
         if asm:
             list(pool.map(_asm, [s for s in srcs if s.suffix == ".hip"]))
     tmp = LIB.with_name(LIB.name + ".tmp")
-    _run([HIPCC, "-shared", "-fPIC", "--offload-arch=" + ARCH, "-o", str(tmp)]
-         + [str(o) for o in objs])
+    # libstdc++ and libgcc linked statically (as the reference's build does,
+    # scripts/build_kernels.sh:78-84): the library then needs only libc, libm, the loader and the
+    # HIP runtime at load time (tests/test_packaging.py audits that).
+    _run([HIPCC, "-shared", "-fPIC", "--offload-arch=" + ARCH, "-static-libstdc++",
+          "-static-libgcc", "-o", str(tmp)] + [str(o) for o in objs])
     os.replace(tmp, LIB)
     if verbose:
         print("built %s (%d units)" % (LIB, len(objs)))
