@@ -357,6 +357,62 @@ def bench_attn_gate(torch, native, dev, stream, steps, warmup):
             "attn_gate_bytes": nbytes}
 
 
+def bench_gated_attention(torch, workloads, native, dev, stream, steps, warmup):
+    """Gated attention forward on the two gated workloads (MSA row attention with a 256-channel
+    gate, 1024-residue triangle attention with a 128-channel gate), bf16: the fused entry
+    (clk_attention_fwd_gated, O never stored) against the forward followed by the separate gate
+    kernel. Two rotating sets each (> 512 MB)."""
+    lib = native.lib()
+    res = {}
+    for name, tag in (("msa_row_attn", "msa"), ("triangle_attn_1024", "tri1024")):
+        c = workloads.GATED_ATTENTION_WORKLOADS[name]
+        sets = []
+        for r in range(2):
+            inp = workloads.attention_workload(name, torch.bfloat16, device=dev, with_dout=False)
+            n, h, sq, d = inp["q"].shape
+            sk = inp["k"].shape[2]
+            x, wg, bg = workloads.gate_inputs(n, sq, c, h * d, torch.bfloat16, seed=70 + r,
+                                              device=dev)
+            inp.update(x=x, wg=wg, bg=bg, out=torch.empty_like(inp["q"]),
+                       gated=torch.empty((n, sq, h * d), dtype=torch.bfloat16, device=dev))
+            sets.append(inp)
+        dims = (n, h, sq, sk, d)
+
+        def fused(i):
+            s = sets[i % 2]
+            st = lib.clk_attention_fwd_gated(
+                stream, native.BF16, s["q"].data_ptr(), s["k"].data_ptr(), s["v"].data_ptr(),
+                s["bias"].data_ptr(), s["kmask"].data_ptr(), s["x"].data_ptr(),
+                s["wg"].data_ptr(), s["bg"].data_ptr(), s["gated"].data_ptr(), None, None,
+                *dims, c, s["scale"])
+            if st != 0:
+                raise RuntimeError(native.last_error())
+
+        def separate(i):
+            s = sets[i % 2]
+            st = lib.clk_attention_fwd(stream, native.BF16, s["q"].data_ptr(),
+                                       s["k"].data_ptr(), s["v"].data_ptr(),
+                                       s["bias"].data_ptr(), s["kmask"].data_ptr(),
+                                       s["out"].data_ptr(), None, *dims, s["scale"], 64, 64)
+            if st == 0:
+                st = lib.clk_attention_gate(stream, native.BF16, s["out"].data_ptr(),
+                                            s["x"].data_ptr(), s["wg"].data_ptr(),
+                                            s["bg"].data_ptr(), s["gated"].data_ptr(), n, h, sq,
+                                            d, c)
+            if st != 0:
+                raise RuntimeError(native.last_error())
+
+        so = torch.cuda.current_stream(dev)
+        tf = timed(torch, fused, steps, warmup, so)
+        ts = timed(torch, separate, steps, warmup, so)
+        flops = attention_flops(n, h, sq, sk, d)["fwd"]
+        res.update({"gated_%s_fused_ms" % tag: tf, "gated_%s_separate_ms" % tag: ts,
+                    "gated_%s_fused_TFLOPs" % tag: flops / (tf * 1e-3) / 1e12,
+                    "gated_%s_speedup" % tag: ts / tf})
+        del sets
+    return res
+
+
 def bench_triangle(torch, native, dev, stream, steps, warmup):
     """Triangle multiplication (outgoing and incoming) on z [512,512,128] bf16 ~N(0,1), mask
     Bernoulli(0.95), six 128x128 weights ~N(0,1/128), biases 0, LayerNorm scales 1 + N(0,0.1)
@@ -532,6 +588,9 @@ def main(argv=None):
         print("bench: timing the attention output gate", file=sys.stderr, flush=True)
         sec.update(bench_attn_gate(torch, native, dev, stream, args.steps, args.warmup))
         sec["attn_gate_frac_hbm"] = sec["attn_gate_GBps"] / HBM_PEAK
+        print("bench: timing gated attention, fused and separate", file=sys.stderr, flush=True)
+        sec.update(bench_gated_attention(torch, workloads, native, dev, stream, args.steps,
+                                         args.warmup))
         print("bench: timing the triangle multiplication", file=sys.stderr, flush=True)
         sec.update(bench_triangle(torch, native, dev, stream, args.steps, args.warmup))
         result["secondary"] = sec

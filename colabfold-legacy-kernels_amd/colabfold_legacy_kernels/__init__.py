@@ -43,6 +43,7 @@ _TABLE = {
     "layer_norm_bwd": ((_ARCH, _LIB, "ClkLayerNormBwd"),),
     "ln_gated_dual_proj": ((_ARCH, _LIB, "ClkLnGdp"),),
     "attention_gate": ((_ARCH, _LIB, "ClkAttentionGate"),),
+    "attention_gated": ((_ARCH, _LIB, "ClkAttentionGated"),),
     "ln_pair_bias": ((_ARCH, _LIB, "ClkLnPairBias"),),
     "gated_dual_proj_bwd": ((_ARCH, _LIB, "ClkGdpBwd"),),
     "triangle_multiply": ((_ARCH, _LIB, "ClkTriangleMultiply"),),

@@ -29,6 +29,10 @@ PROTOTYPES = {
     "clk_attention_fwd": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                                   c_void_p, c_void_p, c_void_p, c_i64, c_i64, c_i64, c_i64,
                                   c_i64, c_f32, c_i64, c_i64]),
+    "clk_attention_fwd_gated": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p,
+                                        c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                        c_void_p, c_void_p, c_void_p, c_i64, c_i64, c_i64,
+                                        c_i64, c_i64, c_i64, c_f32]),
     "clk_attention_bwd_workspace_size": (c_size, [c_i64, c_i64, c_i64, c_i64, c_i64]),
     "clk_attention_bwd": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                                   c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,

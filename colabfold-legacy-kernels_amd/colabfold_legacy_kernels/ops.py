@@ -26,6 +26,7 @@ from . import _native
 __all__ = [
     "ClkError", "InvalidArgument", "InternalError",
     "attention", "attention_fwd", "attention_bwd",
+    "attention_gate", "attention_gated", "attention_gated_fwd",
     "layer_norm", "layer_norm_bwd",
     "gated_dual_proj", "ln_gated_dual_proj",
     "AttentionFunction", "LayerNormFunction",
@@ -358,6 +359,45 @@ def attention_gate(o, x, wg, bg):
         _check(_native.lib().clk_attention_gate(_stream(dev), code, _ptr(o), _ptr(x), _ptr(wg),
                                                 _ptr(bg), _ptr(out), n, h, sq, d, c))
     return out
+
+
+def _gated_call(q, k, v, bias, kmask, x, wg, bg, scale, residuals, what):
+    dev = _require([("q", q), ("k", k), ("v", v), ("bias", bias), ("kmask", kmask), ("x", x),
+                    ("wg", wg), ("bg", bg)], what)
+    n, h, sq, sk, d = _attn_dims(q, k, v, bias, kmask, what)
+    _shape_check(x.dim() == 3 and tuple(x.shape[:2]) == (n, sq), what, "x must be [N,Sq,C]")
+    c = x.shape[2]
+    _shape_check(tuple(wg.shape) == (c, h * d), what, "wg must be [C,H*D]")
+    _shape_check(tuple(bg.shape) == (h * d,), what, "bg must be [H*D]")
+    _shape_check(all(t.dtype == q.dtype for t in (x, wg, bg)), what,
+                 "x, wg and bg must have the dtype of q")
+    code = _dtype_code(q, (_native.F16, _native.BF16), what)
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    gated = torch.empty((n, sq, h * d), device=dev, dtype=q.dtype)
+    out = torch.empty_like(q) if residuals else None
+    lse = torch.empty((n, h, sq), device=dev, dtype=torch.float32) if residuals else None
+    with torch.cuda.device(dev):
+        _check(_native.lib().clk_attention_fwd_gated(
+            _stream(dev), code, _ptr(q), _ptr(k), _ptr(v), _ptr(bias), _ptr(kmask), _ptr(x),
+            _ptr(wg), _ptr(bg), _ptr(gated), _ptr(out), _ptr(lse), n, h, sq, sk, d, c,
+            float(scale)))
+    return gated, out, lse
+
+
+def attention_gated(q, k, v, bias, kmask, x, wg, bg, scale=None):
+    """attention(q, k, v, bias, kmask) gated by sigmoid(x.wg + bg) in one kernel, in the output
+    projection's layout: q [N,H,Sq,D], k/v [N,H,Sk,D], bias [H,Sq,Sk], kmask uint8 [N,Sk] or
+    None, x [N,Sq,C] with C % 32 == 0, wg [C,H*D], bg [H*D] -> [N,Sq,H*D]. The ungated
+    attention output never reaches memory."""
+    gated, _, _ = _gated_call(q, k, v, bias, kmask, x, wg, bg, scale, False, "attention_gated")
+    return gated
+
+
+def attention_gated_fwd(q, k, v, bias, kmask, x, wg, bg, scale=None):
+    """(gated, out, lse): attention_gated plus the ungated output [N,H,Sq,D] and the float32
+    logsumexp [N,H,Sq] that attention_bwd needs."""
+    return _gated_call(q, k, v, bias, kmask, x, wg, bg, scale, True, "attention_gated_fwd")
 
 
 def triangle_einsum(a, b):

@@ -11,14 +11,16 @@ reads those same rounded values. N(mu, var) below names a variance.
   msa_row_attn        q,k,v [512,8,256,32], bias [8,256,256], 102 fully padded sequences,
                       sigmoid gate from a 256x256 weight ~N(0,1/256)
   ln_gdp_512          z [512,512,128], Bernoulli(0.95) mask, four 128x128 weights ~N(0,1/128)
-  triangle_attn_1024  q,k,v [1024,4,1024,32], bias ~N(0,2), keys >= 870 masked (forward only)
+  triangle_attn_1024  q,k,v [1024,4,1024,32], bias ~N(0,2), keys >= 870 masked (forward only),
+                      sigmoid gate from x [1024,1024,128] by a 128x128 weight ~N(0,1/128)
 """
 
 import math
 
 import torch
 
-__all__ = ["attention_inputs", "layer_norm_inputs", "gdp_weights", "ATTENTION_WORKLOADS"]
+__all__ = ["attention_inputs", "gate_inputs", "layer_norm_inputs", "gdp_weights",
+           "ATTENTION_WORKLOADS", "GATED_ATTENTION_WORKLOADS"]
 
 
 def _gen(seed, device):
@@ -73,6 +75,20 @@ def attention_workload(name, dtype=torch.bfloat16, device="cpu", with_dout=None)
     n, h, s, d, seed, bvar, tail, rows, bwd = ATTENTION_WORKLOADS[name]
     return attention_inputs(n, h, s, s, d, dtype, seed, device, bvar, tail, rows,
                             bwd if with_dout is None else with_dout)
+
+
+# Attention workloads whose output is gated: name -> gate input channels C (the gate maps
+# x [N,Sq,C] to H*D columns).
+GATED_ATTENTION_WORKLOADS = {"msa_row_attn": 256, "triangle_attn_1024": 128}
+
+
+def gate_inputs(n, sq, c, hd, dtype=torch.bfloat16, seed=0, device="cpu", bias_std=0.0):
+    """x [N,Sq,C] ~N(0,1), wg [C,HD] ~N(0,1/C), bg [HD] ~N(0,bias_std^2): the output gate."""
+    g = _gen(seed + 2000, device)
+    x = _randn((n, sq, c), g, device).to(dtype)
+    wg = _randn((c, hd), g, device, std=1.0 / math.sqrt(c)).to(dtype)
+    bg = _randn((hd,), g, device, std=bias_std).to(dtype)
+    return x, wg, bg
 
 
 def layer_norm_inputs(m, c, dtype=torch.bfloat16, seed=3, device="cpu", mask_p=0.95):

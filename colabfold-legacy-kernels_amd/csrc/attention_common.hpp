@@ -207,6 +207,28 @@ __device__ __forceinline__ void stage_rows(Rsrc r, int r0, char* lds) {
     }
 }
 
+// stage_rows for D-column rows that lie `ld` elements apart (a column block of a wider
+// row-major matrix): row r of the resource starts at byte 2*r*ld. Rows past the resource read
+// zeros. `tid` is the thread's index in the block (taken as an argument so that a caller can
+// keep its offsets from being shared with, and kept live across, earlier code).
+template <int D, int ROWS, int NTHREADS>
+__device__ __forceinline__ void stage_rows_ld(Rsrc r, int r0, int ld, char* lds, int tid) {
+    using T = SwzTile<D>;
+    constexpr int SLOTS = ROWS * T::PL;
+    static_assert(SLOTS % 64 == 0, "tile must be whole wave instructions");
+    const int lane = tid & 63, wave = tid >> 6;
+#pragma unroll
+    for (int i = 0; i < (SLOTS + NTHREADS - 1) / NTHREADS; ++i) {
+        const int b = wave * 64 + i * NTHREADS;
+        if (SLOTS % NTHREADS != 0 && b >= SLOTS) break;
+        const int slot = b + lane;
+        const int row = slot / T::PL;
+        const int piece = (slot % T::PL) ^ T::swz(row);
+        const int voff = piece < T::P ? (row * ld + piece * 8) * 2 : kPastEnd;
+        buf_dma16(r, voff, r0 * ld * 2, lds + b * 16);
+    }
+}
+
 
 // Row operand from a swizzled tile: row `row`, head dims 32*ks + 8*g + 0..7 (zero beyond D).
 template <typename V8, int D>

@@ -121,12 +121,25 @@ struct TilePrefetch {
     }
 };
 
-template <typename TR, int D, int QT, bool VEC>
+// Operands of the output gate fused into the forward's epilogue:
+//   gated[n, s, h*D + d] = O[n, h, s, d] * sigmoid(x[n, s, :] . wg[:, h*D + d] + bg[h*D + d])
+// with x [N, Sq, C], wg [C, HD] row-major, bg [HD], gated [N, Sq, HD], HD = H*D, C % 32 == 0.
+template <typename E>
+struct GateArgs {
+    const E* x;
+    const E* wg;
+    const E* bg;
+    E* gated;
+    int C, HD;
+};
+
+template <typename TR, int D, int QT, bool VEC, bool GATE>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && VEC ? 3 : 1))) void attn_fwd_kernel(
     const typename TR::elem* __restrict__ q, const typename TR::elem* __restrict__ k,
     const typename TR::elem* __restrict__ v, const typename TR::elem* __restrict__ bias,
     const uint8_t* __restrict__ kmask, typename TR::elem* __restrict__ out,
-    float* __restrict__ lse, int H, int Sq, int Sk, float scale) {
+    float* __restrict__ lse, int H, int Sq, int Sk, float scale,
+    GateArgs<typename TR::elem> ga) {
     using E = typename TR::elem;
     using V8 = typename TR::vec8;
     using G = AttnGeom<D>;
@@ -331,61 +344,151 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
         if (kt + 1 < ntiles) tile(kt + 1, kv1, kv0, cb, ca);
     }
 
-    // Normalise and store: lane holds O[row][16*dt + 4*g + i], i = 0..3.
+    // Gate pre-activations in O^T's accumulator layout (lane: rows 16*dt + 4*g + i of head h's
+    // columns, query r16), so gate and O pair up element for element.
+    f32x4 gacc[GATE ? QT : 1][G::DT];
+    if constexpr (GATE) {
+        // G^T = Wg_h^T . X^T + bg_h over 64-channel chunks: A = channels c0..c0+63 of head h's D
+        // columns of wg, staged like a V tile (rows `HD` apart) and read transposed; B = eight
+        // consecutive channels of the lane's query row of x, straight from global memory
+        // (zero for rows past Sq and channels past C). Chunks alternate between the two K/V
+        // buffers, one barrier each; chunk i+1's wg rows load while chunk i computes, and its x
+        // operands as soon as chunk i's products have read theirs.
+        const int C = ga.C, HD = ga.HD;
+        // Thread coordinates recomputed from an opaque copy of the thread index: shared with
+        // the key loop, the epilogue's offsets would stay live (in registers) through it.
+        int tid = threadIdx.x;
+        asm volatile("" : "+v"(tid));
+        const int gr16 = tid & 15, gg = (tid >> 4) & 3;
+        const Rsrc rw = buffer_rsrc(ga.wg + h * D, (uint32_t)((C - 1) * HD + D) * 2);
+#pragma unroll
+        for (int dt = 0; dt < G::DT; ++dt) {
+            const int d = 16 * dt + 4 * g;
+            f32x4 b0 = {0.f, 0.f, 0.f, 0.f};
+            if (d < D)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) b0[i] = TR::to_f(ga.bg[h * D + d + i]);
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) gacc[qt][dt] = b0;
+        }
+        auto load_x = [&](int c0, V8 (&xo)[QT][2]) {
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+                for (int cc = 0; cc < 2; ++cc) {
+                    const int c = c0 + 32 * cc, row = qbase + qt * 16 + gr16;
+                    u32x4 raw = {0u, 0u, 0u, 0u};
+                    if (c < C && row < Sq) raw = ld16(ga.x + ((size_t)n * Sq + row) * C + c + 8 * gg);
+                    xo[qt][cc] = bits_as<V8>(raw);
+                }
+        };
+        const int nchunks = (C + 63) / 64;
+        V8 xo[QT][2];
+        auto chunk = [&](int ch, const char* cur, char* nxt) {
+            async_wait();
+            __syncthreads();  // chunk ch visible; every wave is done with the other buffer
+            if (ch + 1 < nchunks) stage_rows_ld<D, 64, 256>(rw, 64 * (ch + 1), HD, nxt, tid);
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) {
+                if (64 * ch + 32 * cc >= C) break;  // wave-uniform: the last chunk's empty half
+#pragma unroll
+                for (int dt = 0; dt < G::DT; ++dt) {
+                    const V8 a = swz_tr_operand<V8, D>(cur, 32 * cc, dt, gr16, gg);
+#pragma unroll
+                    for (int qt = 0; qt < QT; ++qt)
+                        gacc[qt][dt] = TR::mfma(a, xo[qt][cc], gacc[qt][dt]);
+                }
+            }
+            if (ch + 1 < nchunks) load_x(64 * (ch + 1), xo);
+        };
+        __syncthreads();  // every wave is done with the last K/V tile
+        stage_rows_ld<D, 64, 256>(rw, 0, HD, kv0, tid);
+        load_x(0, xo);
+        for (int ch = 0; ch < nchunks; ch += 2) {
+            chunk(ch, kv0, kv1);
+            if (ch + 1 < nchunks) chunk(ch + 1, kv1, kv0);
+        }
+    }
+
+    // Normalise and store: lane holds O[row][16*dt + 4*g + i], i = 0..3. With the gate, O is
+    // stored only when `out` is given, and the gated row goes to its [N, Sq, HD] place.
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
         const float l_tot = lsum[qt][0];
         const float inv = 1.0f / fmaxf(l_tot, 1e-30f);
         const int row = qbase + qt * 16 + r16;
         if (row >= Sq) continue;
-        E* orow = out + (nh * Sq + row) * D;
 #pragma unroll
         for (int dt = 0; dt < G::DT; ++dt) {
             const int d = 16 * dt + 4 * g;
-            if (d < D) store4<TR>(orow + d, acc[qt][dt] * inv);
+            if (d >= D) continue;
+            const f32x4 o = acc[qt][dt] * inv;
+            if (!GATE || out) store4<TR>(out + (nh * Sq + row) * D + d, o);
+            if constexpr (GATE) {
+                f32x4 r;
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    r[i] = o[i] * fast_rcp(1.f + fast_exp2(-kLog2e * gacc[qt][dt][i]));
+                store4<TR>(ga.gated + ((size_t)n * Sq + row) * ga.HD + h * D + d, r);
+            }
         }
         if (lse && g == 0) lse[nh * Sq + row] = m_run[qt] + logf(l_tot);
     }
 }
 
-template <typename TR, int D, int QT>
+template <typename TR, int D, int QT, bool GATE>
 void launch_fwd_qt(hipStream_t st, const void* q, const void* k, const void* v, const void* bias,
                    const uint8_t* kmask, void* out, float* lse, int N, int H, int Sq, int Sk,
-                   float scale) {
+                   float scale, GateArgs<typename TR::elem> ga) {
     using E = typename TR::elem;
     const dim3 grid(ceil_div(Sq, 64 * QT) * H * N);
     const bool vec = Sk % 8 == 0 && (reinterpret_cast<uintptr_t>(kmask) & 7u) == 0;
     if (vec)
-        attn_fwd_kernel<TR, D, QT, true><<<grid, 256, 0, st>>>(
+        attn_fwd_kernel<TR, D, QT, true, GATE><<<grid, 256, 0, st>>>(
             (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (E*)out, lse, H, Sq, Sk,
-            scale);
+            scale, ga);
     else
-        attn_fwd_kernel<TR, D, QT, false><<<grid, 256, 0, st>>>(
+        attn_fwd_kernel<TR, D, QT, false, GATE><<<grid, 256, 0, st>>>(
             (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (E*)out, lse, H, Sq, Sk,
-            scale);
+            scale, ga);
 }
 
-template <typename TR, int D>
+template <typename TR, int D, bool GATE>
 void launch_fwd(hipStream_t st, const void* q, const void* k, const void* v, const void* bias,
                 const uint8_t* kmask, void* out, float* lse, int N, int H, int Sq, int Sk,
-                float scale) {
-    KernelTimer timer("attn_fwd", st);
+                float scale, GateArgs<typename TR::elem> ga) {
+    KernelTimer timer(GATE ? "attn_fwd_gated" : "attn_fwd", st);
     if (Sq <= 64)
-        launch_fwd_qt<TR, D, 1>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk, scale);
+        launch_fwd_qt<TR, D, 1, GATE>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk, scale, ga);
     else
-        launch_fwd_qt<TR, D, 2>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk, scale);
+        launch_fwd_qt<TR, D, 2, GATE>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk, scale, ga);
+}
+
+template <typename TR, bool GATE>
+void dispatch_fwd(hipStream_t st, int64_t D, const void* q, const void* k, const void* v,
+                  const void* bias, const uint8_t* kmask, void* out, float* lse, int N, int H,
+                  int Sq, int Sk, float scale, GateArgs<typename TR::elem> ga) {
+    switch (D) {
+        case 8:
+            launch_fwd<TR, 8, GATE>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk, scale, ga);
+            break;
+        case 16:
+            launch_fwd<TR, 16, GATE>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk, scale, ga);
+            break;
+        case 32:
+            launch_fwd<TR, 32, GATE>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk, scale, ga);
+            break;
+        default:
+            launch_fwd<TR, 64, GATE>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk, scale, ga);
+            break;
+    }
 }
 
 template <typename TR>
-void dispatch_fwd(hipStream_t st, int64_t D, const void* q, const void* k, const void* v,
-                  const void* bias, const uint8_t* kmask, void* out, float* lse, int N, int H,
-                  int Sq, int Sk, float scale) {
-    switch (D) {
-        case 8: launch_fwd<TR, 8>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk, scale); break;
-        case 16: launch_fwd<TR, 16>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk, scale); break;
-        case 32: launch_fwd<TR, 32>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk, scale); break;
-        default: launch_fwd<TR, 64>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk, scale); break;
-    }
+GateArgs<typename TR::elem> gate_args(const void* x, const void* wg, const void* bg, void* gated,
+                                      int C, int HD) {
+    using E = typename TR::elem;
+    return {(const E*)x, (const E*)wg, (const E*)bg, (E*)gated, C, HD};
 }
 
 }  // namespace
@@ -408,10 +511,44 @@ extern "C" clk_status clk_attention_fwd(hipStream_t stream, clk_dtype dtype, con
     if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(bias) || !aligned16(out))
         return fail(CLK_INVALID_ARGUMENT, "attention: q, k, v, bias, out must be 16-byte aligned");
     if (dtype == CLK_BF16)
-        dispatch_fwd<BF16>(stream, D, q, k, v, bias, kmask, out, lse, (int)N, (int)H, (int)Sq,
-                           (int)Sk, scale);
+        dispatch_fwd<BF16, false>(stream, D, q, k, v, bias, kmask, out, lse, (int)N, (int)H,
+                                  (int)Sq, (int)Sk, scale, {});
     else
-        dispatch_fwd<F16>(stream, D, q, k, v, bias, kmask, out, lse, (int)N, (int)H, (int)Sq,
-                          (int)Sk, scale);
+        dispatch_fwd<F16, false>(stream, D, q, k, v, bias, kmask, out, lse, (int)N, (int)H,
+                                 (int)Sq, (int)Sk, scale, {});
     return check_launch("attention");
+}
+
+extern "C" clk_status clk_attention_fwd_gated(hipStream_t stream, clk_dtype dtype, const void* q,
+                                              const void* k, const void* v, const void* bias,
+                                              const uint8_t* kmask, const void* x, const void* wg,
+                                              const void* bg, void* gated, void* out, float* lse,
+                                              int64_t N, int64_t H, int64_t Sq, int64_t Sk,
+                                              int64_t D, int64_t C, float scale) {
+    const char* who = "attention_gated";
+    clk_status s = validate_attention(who, dtype, N, H, Sq, Sk, D);
+    if (s != CLK_OK) return s;
+    if (C <= 0 || C % 32)
+        return fail(CLK_INVALID_ARGUMENT, "%s: C=%lld must be a positive multiple of 32", who,
+                    (long long)C);
+    const int64_t HD = H * D;
+    // Buffer offsets into a row block of x and into wg are 32-bit.
+    if (Sq * C * 2 >= ((int64_t)1 << 30) || C * HD * 2 >= ((int64_t)1 << 30))
+        return fail(CLK_INVALID_ARGUMENT, "%s: Sq*C or C*H*D too large", who);
+    if (N * H * Sq == 0) return ok();
+    if (!q || !k || !v || !bias || !x || !wg || !bg || !gated)
+        return fail(CLK_INVALID_ARGUMENT, "%s: null operand pointer", who);
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(bias) || !aligned16(x) ||
+        !aligned16(wg) || !aligned16(gated) || (out && !aligned16(out)))
+        return fail(CLK_INVALID_ARGUMENT,
+                    "%s: q, k, v, bias, x, wg, gated, out must be 16-byte aligned", who);
+    if (dtype == CLK_BF16)
+        dispatch_fwd<BF16, true>(stream, D, q, k, v, bias, kmask, out, lse, (int)N, (int)H,
+                                 (int)Sq, (int)Sk, scale,
+                                 gate_args<BF16>(x, wg, bg, gated, (int)C, (int)HD));
+    else
+        dispatch_fwd<F16, true>(stream, D, q, k, v, bias, kmask, out, lse, (int)N, (int)H,
+                                (int)Sq, (int)Sk, scale,
+                                gate_args<F16>(x, wg, bg, gated, (int)C, (int)HD));
+    return check_launch(who);
 }

@@ -13,6 +13,8 @@
 //       x, wp, bp, wg, bg, mask -> out
 // and accept bf16 as well as f16. Targets without a reference counterpart:
 //   ClkAttentionFwd   q, k, v, bias, kmask -> out, lse (f32 [N,H,Sq]); attribute scale
+//   ClkAttentionGated q, k, v, bias, kmask, x [N,Sq,C], wg [C,H*D], bg [H*D] -> gated
+//                     [N,Sq,H*D] (attention with the output gate fused in); attribute scale
 //   ClkAttentionBwd   q, k, v, bias, kmask, out, dout, lse -> dq, dk, dv, dbias (f32 [H,Sq,Sk]),
 //                     workspace (u8, clk_attention_bwd_workspace_size bytes); attribute scale
 //   ClkLayerNormBwd   x, scale, dy -> dx, dscale, doffset, workspace (u8); attribute eps
@@ -210,6 +212,32 @@ clk_status attention_fwd(const char* who, const Frame& f, bool with_lse) {
                              f.arg(1)->data, f.arg(2)->data, f.arg(3)->data,
                              static_cast<const uint8_t*>(f.arg(4)->data), out->data, lse, d.N,
                              d.H, d.Sq, d.Sk, d.D, scale, bq, bk);
+}
+
+clk_status attention_gated(const Frame& f) {
+    const char* who = "ClkAttentionGated";
+    if (f.nargs() != 8 || f.nrets() != 1)
+        return bad(who, "expects 8 operands (q, k, v, bias, kmask, x, wg, bg) and 1 result");
+    AttnDims d;
+    clk_status s = decode_attention(who, f, &d);
+    if (s != CLK_OK) return s;
+    const Buffer *x = f.arg(5), *wg = f.arg(6), *bg = f.arg(7), *gated = f.ret(0);
+    if (!x || !wg || !bg || !gated) return bad(who, "operands must be buffers");
+    if (x->rank != 3 || x->dims[0] != d.N || x->dims[1] != d.Sq)
+        return bad(who, "x must be [N,Sq,C]");
+    const int64_t C = x->dims[2], HD = d.H * d.D;
+    if (!dims_are(wg, {C, HD}) || !dims_are(bg, {HD}) || !dims_are(gated, {d.N, d.Sq, HD}))
+        return bad(who, "wg [C,H*D], bg [H*D], result [N,Sq,H*D] expected");
+    const DataType t = f.arg(0)->dtype;
+    if (x->dtype != t || wg->dtype != t || bg->dtype != t || gated->dtype != t)
+        return bad(who, "x, wg, bg and the result must have the dtype of q");
+    float scale = 0.f;
+    if (!f.attr_f32("scale", &scale)) return bad(who, "missing f32 attribute 'scale'");
+    return clk_attention_fwd_gated(f.stream(), static_cast<clk_dtype>(t), f.arg(0)->data,
+                                   f.arg(1)->data, f.arg(2)->data, f.arg(3)->data,
+                                   static_cast<const uint8_t*>(f.arg(4)->data), x->data,
+                                   wg->data, bg->data, gated->data, nullptr, nullptr, d.N, d.H,
+                                   d.Sq, d.Sk, d.D, C, scale);
 }
 
 clk_status attention_bwd(const Frame& f) {
@@ -466,6 +494,9 @@ CLK_FFI_EXPORT Error* VoltaWmma(CallFrame* frame) {
 }
 CLK_FFI_EXPORT Error* ClkAttentionFwd(CallFrame* frame) {
     return run(frame, [](const Frame& f) { return attention_fwd("ClkAttentionFwd", f, true); });
+}
+CLK_FFI_EXPORT Error* ClkAttentionGated(CallFrame* frame) {
+    return run(frame, [](const Frame& f) { return attention_gated(f); });
 }
 CLK_FFI_EXPORT Error* ClkAttentionBwd(CallFrame* frame) {
     return run(frame, [](const Frame& f) { return attention_bwd(f); });

@@ -74,6 +74,25 @@ clk_status clk_attention_fwd(hipStream_t stream, clk_dtype dtype, const void* q,
                              float* lse, int64_t N, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
                              float scale, int64_t block_q, int64_t block_k);
 
+/*
+ * Attention forward with the output gate fused into its epilogue: the reference's epilogue
+ * normalises and stores O (cuda/volta_mma_attn.cu:256-272) and its caller's Attention module
+ * then gates it; here
+ *   gated[n, s, h*D + d] = O[n, h, s, d] * sigmoid(x[n, s, :] . wg[:, h*D + d] + bg[h*D + d])
+ * is written directly in the [N, Sq, H*D] layout the output projection reads, and O itself
+ * never reaches memory unless `out` is given. q, k, v, bias, kmask, lse, scale as in
+ * clk_attention_fwd; x [N, Sq, C] (the attention's query-side input), wg [C, H*D] row-major,
+ * bg [H*D], all of the attention's dtype; C a positive multiple of 32. out (the ungated O
+ * [N,H,Sq,D], for a backward pass) and lse may be NULL. The gate GEMM runs on MFMA with float32
+ * accumulation; O is not rounded to the dtype before it is gated.
+ */
+clk_status clk_attention_fwd_gated(hipStream_t stream, clk_dtype dtype, const void* q,
+                                   const void* k, const void* v, const void* bias,
+                                   const uint8_t* kmask, const void* x, const void* wg,
+                                   const void* bg, void* gated, void* out, float* lse, int64_t N,
+                                   int64_t H, int64_t Sq, int64_t Sk, int64_t D, int64_t C,
+                                   float scale);
+
 /* Bytes of device workspace clk_attention_bwd needs for these sizes. */
 size_t clk_attention_bwd_workspace_size(int64_t N, int64_t H, int64_t Sq, int64_t Sk, int64_t D);
 

@@ -161,6 +161,30 @@ def test_attention_gate_validation(n, h, sq, d, c, msg):
     assert msg in _native.last_error()
 
 
+def attn_gated(**kw):
+    a = dict(stream=None, dtype=BF16, q=FAKE, k=FAKE, v=FAKE, bias=FAKE, kmask=FAKE, x=FAKE,
+             wg=FAKE, bg=FAKE, gated=FAKE, out=None, lse=None, N=2, H=2, Sq=16, Sk=16, D=32,
+             C=64, scale=0.17)
+    a.update(kw)
+    return _native.lib().clk_attention_fwd_gated(*a.values())
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(C=48), "multiple of 32"), (dict(C=0), "multiple of 32"), (dict(D=24), "head dim"),
+    (dict(dtype=F32), "dtype"), (dict(x=None), "null"), (dict(gated=None), "null"),
+    (dict(wg=FAKE + 8), "aligned"), (dict(out=FAKE + 8), "aligned"),
+    (dict(Sq=1 << 20, C=1024), "too large"), (dict(H=64, D=64, C=1 << 17), "too large"),
+])
+def test_attention_gated_validation(kw, msg):
+    assert attn_gated(**kw) == INVALID
+    assert msg in _native.last_error()
+
+
+def test_attention_gated_empty_is_ok():
+    assert attn_gated(N=0) == _native.OK
+    assert attn_gated(Sq=0, x=None) == _native.OK  # no work: pointers are not needed
+
+
 @pytest.mark.parametrize("m,k,n,msg", [(4, 96, 128, "64 or 128"), (4, 128, 32, "64 or 128"),
                                        (-1, 128, 128, "64 or 128")])
 def test_gdp_bwd_validation(m, k, n, msg):

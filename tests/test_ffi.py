@@ -13,7 +13,7 @@ pytestmark = pytest.mark.skipif(not clk.available("gfx950"), reason="library not
 
 TARGETS = ["VoltaMma", "VoltaWmma", "ClkAttentionFwd", "ClkAttentionBwd", "VoltaLayerNorm",
            "ClkLayerNormBwd", "VoltaGdp", "VoltaGdpWmma", "ClkLnGdp", "ClkAttentionGate",
-           "ClkLnPairBias", "ClkGdpBwd", "ClkTriangleMultiply"]
+           "ClkAttentionGated", "ClkLnPairBias", "ClkGdpBwd", "ClkTriangleMultiply"]
 FAKE = 0x100000
 
 
@@ -130,6 +130,32 @@ def test_attention_gate_decode_errors(lib):
     fr = x.frame([x.buffer(BF16, (2, 8, 16, 32), FAKE)], [x.buffer(BF16, (2, 16, 256), FAKE)], [])
     assert x.call(lib, "ClkAttentionGate", fr) is not None
     assert "4 operands" in x.errors[-1][1]
+
+
+def test_attention_gated_decode_errors(lib):
+    x = FakeXla()
+    attn = [x.buffer(BF16, (2, 8, 16, 32), FAKE)] * 3 + [x.buffer(BF16, (8, 16, 16), FAKE),
+                                                          x.buffer(U8, (2, 16), FAKE)]
+    gate = [x.buffer(BF16, (2, 16, 128), FAKE), x.buffer(BF16, (128, 256), FAKE),
+            x.buffer(BF16, (256,), FAKE)]
+    res = [x.buffer(BF16, (2, 16, 256), FAKE)]
+    scale = [("scale", F32, 0.17)]
+    fr = x.frame(attn + gate[:2] + [x.buffer(BF16, (128,), FAKE)], res, scale)
+    assert x.call(lib, "ClkAttentionGated", fr) is not None
+    assert "bg [H*D]" in x.errors[-1][1]
+    fr = x.frame(attn + gate, [x.buffer(BF16, (2, 8, 16, 32), FAKE)], scale)
+    assert x.call(lib, "ClkAttentionGated", fr) is not None
+    assert "result [N,Sq,H*D]" in x.errors[-1][1]
+    fr = x.frame(attn + gate, res, [])
+    assert x.call(lib, "ClkAttentionGated", fr) is not None
+    assert "scale" in x.errors[-1][1]
+    fr = x.frame(attn, res, scale)
+    assert x.call(lib, "ClkAttentionGated", fr) is not None
+    assert "8 operands" in x.errors[-1][1]
+    fr = x.frame(attn + [x.buffer(BF16, (2, 16, 48), FAKE), x.buffer(BF16, (48, 256), FAKE),
+                         gate[2]], res, scale)
+    assert x.call(lib, "ClkAttentionGated", fr) is not None
+    assert "multiple of 32" in x.errors[-1][1]
 
 
 def test_new_targets_decode_errors(lib):

@@ -129,7 +129,8 @@ def test_layer_norm_and_gdp_targets(cuda):
 
 
 def test_new_targets_match_the_c_abi(cuda):
-    """ClkAttentionGate, ClkLnPairBias, ClkGdpBwd and ClkTriangleMultiply on device buffers."""
+    """ClkAttentionGate, ClkAttentionGated, ClkLnPairBias, ClkGdpBwd and ClkTriangleMultiply on
+    device buffers."""
     lib, x = lib_and_runtime(cuda)
     g = torch.Generator().manual_seed(21)
     bf = lambda *s, std=1.0: (torch.randn(s, generator=g) * std).to(torch.bfloat16).to(cuda)  # noqa
@@ -141,6 +142,15 @@ def test_new_targets_match_the_c_abi(cuda):
     assert x.call(lib, "ClkAttentionGate", fr) is None, x.errors
     torch.cuda.synchronize()
     assert torch.equal(out, ops.attention_gate(o, xin, wgt, bgt))
+
+    q, k, v = bf(2, 8, 40, 32), bf(2, 8, 40, 32), bf(2, 8, 40, 32)
+    ab, km = bf(8, 40, 40), (torch.rand((2, 40), generator=g) > 0.2).to(torch.uint8).to(cuda)
+    gated = torch.empty((2, 40, 256), dtype=torch.bfloat16, device=cuda)
+    fr = x.frame([buf(x, t) for t in (q, k, v, ab, km, xin, wgt, bgt)], [buf(x, gated)],
+                 [("scale", F32, 0.17)])
+    assert x.call(lib, "ClkAttentionGated", fr) is None, x.errors
+    torch.cuda.synchronize()
+    assert torch.equal(gated, ops.attention_gated(q, k, v, ab, km, xin, wgt, bgt, 0.17))
 
     z, sc, of, w = bf(16, 24, 128), f32(128, base=1.0), f32(128), bf(128, 4, std=1 / 11.3)
     bias = torch.empty((4, 16, 24), dtype=torch.bfloat16, device=cuda)
