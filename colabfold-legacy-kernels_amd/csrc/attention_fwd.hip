@@ -31,6 +31,7 @@ namespace clk {
 namespace {
 
 constexpr float kRescaleSlack = 8.f;  // log2 of the largest P before the running max moves
+constexpr int kGateChannels = 128;    // gate channels (wg rows) per K/V buffer in the epilogue
 
 // Per-tile "some key absent or past Sk" flags of one mask row, as bits of a 64-bit word (tiles of
 // 64 keys; tiles past the 64th always take the checked path), worked out by each wave on its
@@ -175,6 +176,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
     const Rsrc rv = buffer_rsrc(vp, (uint32_t)Sk * D * 2);
     // The block's bias rows (queries q0 .. q0+BQ-1 that exist).
     const Rsrc rb = buffer_rsrc(bp + (size_t)q0 * Sk, (uint32_t)(min(BQ, Sq - q0) * Sk * 2));
+    // Head h's D columns of the gate weight: row c (channel) starts HD elements after row c-1.
+    const Rsrc rw = GATE ? buffer_rsrc(ga.wg + h * D, (uint32_t)((ga.C - 1) * ga.HD + D) * 2)
+                         : rb;
     auto stage = [&](int k0, char* kv) {
         stage_rows<D, BK, 256>(rk, k0, kv);
         stage_rows<D, BK, 256>(rv, k0, kv + TILE);
@@ -240,6 +244,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
         if (kt + 1 < ntiles) {
             stage(k0 + BK, kvn);
             nxt.load(brow, mp, k0 + BK, g, Sk);
+        } else if constexpr (GATE) {
+            // The last key tile leaves the other buffer free: the wg rows of the first
+            // kGateChannels gate channels go there now, ready for the epilogue.
+            int t = threadIdx.x;
+            asm volatile("" : "+v"(t));
+            stage_rows_ld<D, kGateChannels, 256>(rw, 0, ga.HD, kvn, t);
         }
         V8 kf[4][G::KS];
 #pragma unroll
@@ -348,22 +358,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
     // columns, query r16), so gate and O pair up element for element.
     f32x4 gacc[GATE ? QT : 1][G::DT];
     if constexpr (GATE) {
-        // G^T = Wg_h^T . X^T + bg_h over 64-channel chunks: A = channels c0..c0+63 of head h's D
-        // columns of wg, staged like a V tile (rows `HD` apart) and read transposed; B = eight
-        // consecutive channels of the lane's query row of x, straight from global memory
-        // (zero for rows past Sq and channels past C). Chunks alternate between the two K/V
-        // buffers, one barrier each; chunk i+1's wg rows load while chunk i computes, and its x
-        // operands as soon as chunk i's products have read theirs.
+        // G^T = Wg_h^T . X^T + bg_h, 2*kGateChannels channels per round: A = head h's wg
+        // columns for kGateChannels channels per K/V buffer (both buffers hold 128 rows of D),
+        // staged like a V tile and read transposed; B = eight consecutive channels of the
+        // lane's query row of x, straight from global memory into registers (zero for rows past
+        // Sq and channels past C). The first buffer's rows were fetched during the last key
+        // tile, and the x loads are issued before the barrier, so a round costs one wait.
         const int C = ga.C, HD = ga.HD;
         // Thread coordinates recomputed from an opaque copy of the thread index: shared with
         // the key loop, the epilogue's offsets would stay live (in registers) through it.
         int tid = threadIdx.x;
         asm volatile("" : "+v"(tid));
         const int gr16 = tid & 15, gg = (tid >> 4) & 3;
-        const Rsrc rw = buffer_rsrc(ga.wg + h * D, (uint32_t)((C - 1) * HD + D) * 2);
 #pragma unroll
         for (int dt = 0; dt < G::DT; ++dt) {
-            const int d = 16 * dt + 4 * g;
+            const int d = 16 * dt + 4 * gg;
             f32x4 b0 = {0.f, 0.f, 0.f, 0.f};
             if (d < D)
 #pragma unroll
@@ -371,56 +380,61 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt) gacc[qt][dt] = b0;
         }
-        auto load_x = [&](int c0, V8 (&xo)[QT][2]) {
+        constexpr int GC = kGateChannels, NX = 2 * GC / 32;
+        static_assert(GC * T::ROWB <= 2 * TILE, "a K/V buffer holds kGateChannels wg rows");
+        char* const kfree = (ntiles & 1) ? kv1 : kv0;  // not read by the last key tile
+        char* const klast = (ntiles & 1) ? kv0 : kv1;
+        for (int c0 = 0; c0 < C; c0 += 2 * GC) {
+            V8 xo[QT][NX];
 #pragma unroll
-            for (int qt = 0; qt < QT; ++qt)
+            for (int qt = 0; qt < QT; ++qt) {
+                const int row = qbase + qt * 16 + gr16;
 #pragma unroll
-                for (int cc = 0; cc < 2; ++cc) {
-                    const int c = c0 + 32 * cc, row = qbase + qt * 16 + gr16;
+                for (int j = 0; j < NX; ++j) {
+                    const int c = c0 + 32 * j;
                     u32x4 raw = {0u, 0u, 0u, 0u};
-                    if (c < C && row < Sq) raw = ld16(ga.x + ((size_t)n * Sq + row) * C + c + 8 * gg);
-                    xo[qt][cc] = bits_as<V8>(raw);
-                }
-        };
-        const int nchunks = (C + 63) / 64;
-        V8 xo[QT][2];
-        auto chunk = [&](int ch, const char* cur, char* nxt) {
-            async_wait();
-            __syncthreads();  // chunk ch visible; every wave is done with the other buffer
-            if (ch + 1 < nchunks) stage_rows_ld<D, 64, 256>(rw, 64 * (ch + 1), HD, nxt, tid);
-#pragma unroll
-            for (int cc = 0; cc < 2; ++cc) {
-                if (64 * ch + 32 * cc >= C) break;  // wave-uniform: the last chunk's empty half
-#pragma unroll
-                for (int dt = 0; dt < G::DT; ++dt) {
-                    const V8 a = swz_tr_operand<V8, D>(cur, 32 * cc, dt, gr16, gg);
-#pragma unroll
-                    for (int qt = 0; qt < QT; ++qt)
-                        gacc[qt][dt] = TR::mfma(a, xo[qt][cc], gacc[qt][dt]);
+                    if (c < C && row < Sq)
+                        raw = ld16(ga.x + ((size_t)n * Sq + row) * C + c + 8 * gg);
+                    xo[qt][j] = bits_as<V8>(raw);
                 }
             }
-            if (ch + 1 < nchunks) load_x(64 * (ch + 1), xo);
-        };
-        __syncthreads();  // every wave is done with the last K/V tile
-        stage_rows_ld<D, 64, 256>(rw, 0, HD, kv0, tid);
-        load_x(0, xo);
-        for (int ch = 0; ch < nchunks; ch += 2) {
-            chunk(ch, kv0, kv1);
-            if (ch + 1 < nchunks) chunk(ch + 1, kv1, kv0);
+            __syncthreads();  // every wave is done with both buffers
+            if (c0 > 0 || ntiles == 0) stage_rows_ld<D, GC, 256>(rw, c0, HD, kfree, tid);
+            if (c0 + GC < C) stage_rows_ld<D, GC, 256>(rw, c0 + GC, HD, klast, tid);
+            async_wait();
+            __syncthreads();  // this round's wg rows are visible
+#pragma unroll
+            for (int half = 0; half < 2; ++half)
+#pragma unroll
+                for (int cc = 0; cc < GC / 32; ++cc) {
+                    if (c0 + GC * half + 32 * cc >= C) break;  // wave-uniform
+#pragma unroll
+                    for (int dt = 0; dt < G::DT; ++dt) {
+                        const V8 a =
+                            swz_tr_operand<V8, D>(half ? klast : kfree, 32 * cc, dt, gr16, gg);
+#pragma unroll
+                        for (int qt = 0; qt < QT; ++qt)
+                            gacc[qt][dt] = TR::mfma(a, xo[qt][(GC / 32) * half + cc], gacc[qt][dt]);
+                    }
+                }
         }
     }
 
     // Normalise and store: lane holds O[row][16*dt + 4*g + i], i = 0..3. With the gate, O is
-    // stored only when `out` is given, and the gated row goes to its [N, Sq, HD] place.
+    // stored only when `out` is given, and the gated row goes to its [N, Sq, HD] place (its
+    // lane coordinates again from an opaque thread index, as in the gate products).
+    int etid = threadIdx.x;
+    if constexpr (GATE) asm volatile("" : "+v"(etid));
+    const int er16 = etid & 15, eg = (etid >> 4) & 3;
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
         const float l_tot = lsum[qt][0];
         const float inv = 1.0f / fmaxf(l_tot, 1e-30f);
-        const int row = qbase + qt * 16 + r16;
+        const int row = qbase + qt * 16 + er16;
         if (row >= Sq) continue;
 #pragma unroll
         for (int dt = 0; dt < G::DT; ++dt) {
-            const int d = 16 * dt + 4 * g;
+            const int d = 16 * dt + 4 * eg;
             if (d >= D) continue;
             const f32x4 o = acc[qt][dt] * inv;
             if (!GATE || out) store4<TR>(out + (nh * Sq + row) * D + d, o);
@@ -432,7 +446,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
                 store4<TR>(ga.gated + ((size_t)n * Sq + row) * ga.HD + h * D + d, r);
             }
         }
-        if (lse && g == 0) lse[nh * Sq + row] = m_run[qt] + logf(l_tot);
+        if (lse && eg == 0) lse[nh * Sq + row] = m_run[qt] + logf(l_tot);
     }
 }
 
