@@ -48,6 +48,12 @@ HBM_PEAK = 8000.0        # GB/s
 N_ROWS, HEADS, NRES, HEAD_DIM = 384, 4, 384, 32
 ROTATE = 3
 
+# Issue rates of one MI355X (256 CUs x 4 SIMDs at 2.4 GHz): a wave64 VALU instruction occupies a
+# 16-lane SIMD for 4 cycles (the published 157.3 TFLOP/s vector fp32 counts two lanes per packed
+# instruction); a 16x16x32 bf16 MFMA (16384 flops) takes 16 cycles at the 2516.6 TFLOP/s peak.
+SIMDS, CLOCK_HZ = 1024, 2.4e9
+VALU_CYCLES, MFMA_CYCLES = 4, 16
+
 
 def _cores():
     try:
@@ -467,6 +473,69 @@ def recorded_traffic(kernel):
     return found
 
 
+def recorded_instructions(kernel):
+    """{"valu", "trans", "mfma"}: wave instructions per launch of `kernel` (VALU excluding MFMA
+    and transcendentals; float32 transcendentals; MFMA) from the committed rocprofv3
+    instruction-mix summaries, lines "<kind>_instructions_per_launch[<kernel>]: <n>"; None when
+    no summary covers the kernel."""
+    pat = re.compile(r"^(valu|trans|mfma)_instructions_per_launch\[(\w+)\]:\s*([0-9.eE+]+)\s*$")
+    found = {}
+    for f in sorted((ROOT / "profiles").glob("*instruction_mix*.md")):
+        for line in f.read_text().splitlines():
+            m = pat.match(line.strip())
+            if m and m.group(2) == kernel:
+                found[m.group(1)] = float(m.group(3))
+    return found if len(found) == 3 else None
+
+
+def issue_bound(kernel, avg_ms, scores):
+    """The kernel's instruction-issue floor: its recorded wave instructions at one per SIMD every
+    VALU_CYCLES cycles (transcendentals at a quarter of that rate, MFMA every MFMA_CYCLES) over
+    all SIMDs at CLOCK_HZ, added, since a wave issues one instruction at a time.
+    frac = floor / measured duration."""
+    rec = recorded_instructions(kernel)
+    if rec is None:
+        return None
+    cyc = SIMDS * CLOCK_HZ / 1e3
+    valu_ms = (rec["valu"] * VALU_CYCLES + rec["trans"] * 4 * VALU_CYCLES) / cyc
+    mfma_ms = rec["mfma"] * MFMA_CYCLES / cyc
+    lane_ops = (rec["valu"] + rec["trans"]) * 64
+    return {"valu_instructions": rec["valu"], "trans_instructions": rec["trans"],
+            "mfma_instructions": rec["mfma"], "scores": scores,
+            "valu_lane_ops_per_score": lane_ops / scores if scores else None,
+            "valu_ms": valu_ms, "mfma_ms": mfma_ms, "bound_ms": valu_ms + mfma_ms,
+            "frac": (valu_ms + mfma_ms) / avg_ms}
+
+
+def counter_summary(paths):
+    """Markdown rows: per kernel and grid (workgroups; one workload each), dispatch count and the
+    median per dispatch of each counter in rocprofv3 --pmc csv files (values of one dispatch
+    summed over its dimension instances)."""
+    import csv
+    import statistics
+    per = {}
+    for path in paths:
+        with open(path) as fh:
+            for r in csv.DictReader(fh):
+                name = r["Kernel_Name"].replace("(anonymous namespace)::", "")
+                name = re.sub(r"^void |clk::", "", name.split("(")[0])
+                wgs = int(r["Grid_Size"]) // max(1, int(r["Workgroup_Size"]))
+                key = (r["Dispatch_Id"], r["Counter_Name"])
+                d = per.setdefault((name, wgs), {})
+                d[key] = d.get(key, 0.0) + float(r["Counter_Value"])
+    counters = sorted({c for d in per.values() for (_, c) in d})
+    print("| kernel | workgroups | dispatches | " + " | ".join(counters) + " |")
+    print("|---" * (len(counters) + 3) + "|")
+    for (name, wgs), d in sorted(per.items()):
+        cols = []
+        for c in counters:
+            vals = [v for (disp, cn), v in d.items() if cn == c]
+            cols.append("%.4g" % statistics.median(vals) if vals else "-")
+        disp = len({disp for (disp, _) in d})
+        print("| `%s` | %d | %d | %s |" % (name, wgs, disp, " | ".join(cols)))
+    return 0
+
+
 def copy_calibration(mib, reps=5):
     """A plain device-to-device copy of `mib` MiB, `reps` times: the known-size reference that
     the FETCH_SIZE / WRITE_SIZE counters are scaled by (reads and writes mib MiB each)."""
@@ -507,7 +576,11 @@ def main(argv=None):
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (counter calibration)")
+    ap.add_argument("--counter-summary", nargs="+", metavar="CSV",
+                    help="only summarise rocprofv3 --pmc csv files per kernel (no GPU)")
     args = ap.parse_args(argv)
+    if args.counter_summary:
+        return counter_summary(args.counter_summary)
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
     if args.gpus != 1:
@@ -544,7 +617,8 @@ def main(argv=None):
     roofline = {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": MFMA_PEAK_BF16,
                 "unit": "TFLOP/s", "frac": (achieved / MFMA_PEAK_BF16) if achieved else None,
                 "traffic": recorded_traffic(dom), "avg_ms": kernels[dom]["avg_ms"],
-                "algorithmic_flops_per_launch": dom_flops}
+                "algorithmic_flops_per_launch": dom_flops,
+                "issue": issue_bound(dom, kernels[dom]["avg_ms"], N_ROWS * HEADS * NRES * NRES)}
 
     result = {
         "metric": METRIC, "value": tflops, "unit": "TFLOP/s", "n_gpus": 1,

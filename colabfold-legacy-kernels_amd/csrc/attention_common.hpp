@@ -251,6 +251,19 @@ __device__ __forceinline__ V8 swz_tr_operand(const char* lds, int rbase, int dt,
     return lds_tr8<V8>(lo, hi);
 }
 
+// swz_tr_operand for a split key order: lane (r16, g) gets column 16*dt + r16 of rows
+// rbase + 4g + 0..3 and rbase + 16 + 4g + 0..3.
+template <typename V8, int D>
+__device__ __forceinline__ V8 swz_tr_operand_split(const char* lds, int rbase, int dt, int r16,
+                                                   int g) {
+    const int row = rbase + 4 * g + (r16 >> 2);
+    const int col = 16 * dt + 4 * (r16 & 3);
+    const int piece = col >> 3, inner = (col & 7) * 2;
+    const char* lo = lds + SwzTile<D>::off(row, piece) + inner;
+    const char* hi = lds + SwzTile<D>::off(row + 16, piece) + inner;
+    return lds_tr8<V8>(lo, hi);
+}
+
 template <typename TR>
 __device__ __forceinline__ void store4(typename TR::elem* p, f32x4 v) {
     using E = typename TR::elem;

@@ -25,6 +25,8 @@
 // rounding unit there is 128), which would scale P by up to 2^64.
 // lse = m + log(l) (natural log) is written when requested, for the backward pass; for an
 // all-masked row it is therefore ln(Sk), relative to the masked logit.
+#include <cmath>
+
 #include "attention_common.hpp"
 
 namespace clk {
@@ -81,7 +83,7 @@ __device__ __forceinline__ RowFlags row_flags(const uint8_t* mrow, int Sk) {
 // and, unless the bias tile travels through LDS (VEC), the bias of those keys for each of the
 // lane's query rows. VEC (Sk % 8 == 0, 8-byte aligned mask rows): 8-byte mask loads whose address
 // is clamped into the row (keys past Sk are forced to -inf anyway); otherwise element loads.
-template <typename TR, int QT, bool VEC>
+template <typename TR, int QT, bool VEC, bool BM = false>
 struct TilePrefetch {
     u32x2 mask[2];
     u32x4 bias[VEC ? 1 : QT][2];
@@ -92,8 +94,18 @@ struct TilePrefetch {
         for (int c = 0; c < 2; ++c) {
             const int kk = k0 + 32 * c + 8 * g;
             if constexpr (VEC) {
-                mask[c] = mrow ? *reinterpret_cast<const u32x2*>(mrow + min(kk, Sk - 8))
-                               : u32x2{~0u, ~0u};
+                if constexpr (BM) {
+                    // Keys k0 + 32c + 4g + 0..3 and k0 + 32c + 16 + 4g + 0..3 (the bias-MFMA
+                    // key order), 4-byte loads clamped into the row.
+                    const int k4 = k0 + 32 * c + 4 * g;
+                    mask[c] = mrow ? u32x2{*reinterpret_cast<const unsigned*>(mrow + min(k4, Sk - 4)),
+                                           *reinterpret_cast<const unsigned*>(
+                                               mrow + min(k4 + 16, Sk - 4))}
+                                   : u32x2{~0u, ~0u};
+                } else {
+                    mask[c] = mrow ? *reinterpret_cast<const u32x2*>(mrow + min(kk, Sk - 8))
+                                   : u32x2{~0u, ~0u};
+                }
             } else {
                 uint8_t m[8];
 #pragma unroll
@@ -134,18 +146,31 @@ struct GateArgs {
     int C, HD;
 };
 
-template <typename TR, int D, int QT, bool VEC, bool GATE>
+// How the logits reach the softmax. Plain: logit = fmaf(q.k, scale, bias) per score (bias
+// unpacked to float32). Bias MFMA (`bm`, used when the bias tile is in LDS and scale > 0): the
+// accumulator of S^T starts as bias / scale, added by one more MFMA per 16x16 tile whose A
+// operand is [hi*I | lo*I] (hi + lo = 1/scale as two values of the input type, each product
+// with a bias value exact in float32) and whose B operand is the tile's bias, duplicated over
+// the two halves of the contraction; S^T then holds logit / scale, and log2(e) * logit =
+// cexp * S with cexp = scale * log2(e). No per-score instruction touches the bias. A bias of
+// magnitude above 3.4e38 * scale overflows there (float32 cannot hold bias / scale).
+struct BiasMfma {
+    float hi, lo, bscale, cexp;
+};
+
+template <typename TR, int D, int QT, bool VEC, bool GATE, bool BM>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && VEC ? 3 : 1))) void attn_fwd_kernel(
     const typename TR::elem* __restrict__ q, const typename TR::elem* __restrict__ k,
     const typename TR::elem* __restrict__ v, const typename TR::elem* __restrict__ bias,
     const uint8_t* __restrict__ kmask, typename TR::elem* __restrict__ out,
     float* __restrict__ lse, int H, int Sq, int Sk, float scale,
-    GateArgs<typename TR::elem> ga) {
+    GateArgs<typename TR::elem> ga, BiasMfma bm) {
+    static_assert(!BM || VEC, "the bias MFMA reads the bias tile from LDS");
     using E = typename TR::elem;
     using V8 = typename TR::vec8;
     using G = AttnGeom<D>;
     using T = SwzTile<D>;
-    using PF = TilePrefetch<TR, QT, VEC>;
+    using PF = TilePrefetch<TR, QT, VEC, BM>;
     constexpr int BQ = 4 * 16 * QT;
     constexpr int BK = G::BK;
     constexpr int TILE = BK * T::ROWB;  // bytes of one K or V tile
@@ -219,7 +244,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
     if (ntiles > 0) ca.load(brow, mp, 0, g, Sk);
     // The mask row's tile flags, with the Q and first-tile loads already in flight.
     const RowFlags rf = row_flags<VEC>(mp, Sk);
-    const float masked_logit = rf.masked_logit;
+    // In the bias-MFMA form every score is in units of 1/scale of the logit (xs = scale*log2e
+    // per unit); otherwise in logit units (xs = log2e).
+    const float masked_logit = BM ? rf.masked_logit * bm.bscale : rf.masked_logit;
+    const float xs = BM ? bm.cexp : kLog2e;
+    // A operand [hi*I | lo*I] of the bias MFMA: lane (row r16, group g) holds columns
+    // 8g .. 8g+7, so its one nonzero is element r16 % 8 when g % 2 == r16 / 8.
+    V8 idn;
+    if constexpr (BM) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            idn[j] = TR::from_f((j == (r16 & 7) && (g & 1) == (r16 >> 3)) ? (g < 2 ? bm.hi : bm.lo)
+                                                                      : 0.f);
+    }
 
     // Running max, and O^T plus one extra accumulator per sub-tile: the MFMA of an all-ones
     // A operand with P^T, i.e. the row sum of the (rounded) P that the P.V product uses.
@@ -256,16 +293,34 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
         for (int t = 0; t < 4; ++t)
 #pragma unroll
             for (int ks = 0; ks < G::KS; ++ks)
-                kf[t][ks] = swz_row_operand<V8, D>(kvc, perm_key(t, r16), ks, g);
+                kf[t][ks] = swz_row_operand<V8, D>(kvc, BM ? 16 * t + r16 : perm_key(t, r16), ks, g);
         V8 vf[G::DT][2];
 #pragma unroll
         for (int dt = 0; dt < G::DT; ++dt)
 #pragma unroll
             for (int c = 0; c < 2; ++c)
-                vf[dt][c] = swz_tr_operand<V8, D>(kvc + TILE, 32 * c, dt, r16, g);
+                vf[dt][c] = BM ? swz_tr_operand_split<V8, D>(kvc + TILE, 32 * c, dt, r16, g)
+                               : swz_tr_operand<V8, D>(kvc + TILE, 32 * c, dt, r16, g);
 
         // S^T = K . Q^T for the four 16-key sub-tiles (chunk c = t/2, half t%2).
         f32x4 s[QT][4];
+        if constexpr (BM) {
+            // Bias / scale first. S^T tile t holds keys 16t + 0..15 of the key tile here, so
+            // rows 8g' + j of the B operand (g' = g % 2, duplicated for the lo half) are keys
+            // 16t + 8g' + 0..7 of the lane's query row: one 16-byte piece, 2t + g', of the
+            // swizzled bias rows (piece p of row r at p ^ (r & 7)).
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+                const int row = wave * 16 * QT + 16 * qt + r16;
+                const char* brow_l = kvc + 2 * TILE + row * 128;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const u32x4 raw = *reinterpret_cast<const u32x4*>(
+                        brow_l + 16 * ((2 * t + (g & 1)) ^ (row & 7)));
+                    s[qt][t] = TR::mfma(idn, bits_as<V8>(raw), f32x4{0.f, 0.f, 0.f, 0.f});
+                }
+            }
+        }
 #pragma unroll
         for (int t = 0; t < 4; ++t)
 #pragma unroll
@@ -273,13 +328,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
 #pragma unroll
                 for (int qt = 0; qt < QT; ++qt)
                     s[qt][t] = TR::mfma(kf[t][ks], qf[qt][ks],
-                                        ks == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : s[qt][t]);
+                                        (BM || ks > 0) ? s[qt][t] : f32x4{0.f, 0.f, 0.f, 0.f});
 
         float x[QT][2][8];
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
+                if constexpr (BM) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        x[qt][c][j] = s[qt][2 * c][j];
+                        x[qt][c][4 + j] = s[qt][2 * c + 1][j];
+                    }
+                    continue;
+                }
                 float bv[8];
                 if constexpr (VEC) {
                     const int row = wave * 16 * QT + 16 * qt + r16;
@@ -301,14 +364,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
             asm volatile("");
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
-                const int lim = Sk - (k0 + 32 * c + 8 * g);  // keys j >= lim are past Sk
+                // Slot j is key k0 + 32c + 8g + j, or in the bias-MFMA order
+                // k0 + 32c + 4g + j (j < 4) and k0 + 32c + 12 + 4g + j (j >= 4): it is past Sk
+                // when j (j + 12 for the upper four of that order) >= lim.
+                const int lim = Sk - (k0 + 32 * c + (BM ? 4 : 8) * g);
                 const unsigned valid = cur.valid(c);
 #pragma unroll
                 for (int qt = 0; qt < QT; ++qt)
 #pragma unroll
                     for (int j = 0; j < 8; ++j)
-                        x[qt][c][j] = j >= lim ? -INFINITY
-                                               : (((valid >> j) & 1u) ? x[qt][c][j] : masked_logit);
+                        x[qt][c][j] = (BM && j >= 4 ? j + 12 : j) >= lim
+                                          ? -INFINITY
+                                          : (((valid >> j) & 1u) ? x[qt][c][j] : masked_logit);
             }
         }
 
@@ -323,24 +390,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
             // Lazy rescaling: the running max moves only when the tile's max exceeds it by more
             // than kRescaleSlack (in log2 units), so P stays below 2^kRescaleSlack and most tiles
             // skip the rescale of O and l (a wave-uniform branch).
-            const bool move = mt * kLog2e > m_run[qt] * kLog2e + kRescaleSlack;
+            const bool move = mt * xs > m_run[qt] * xs + kRescaleSlack;
             if (__any(move)) {
                 // Opaque to if-conversion: without it the compiler runs the rescale on every
                 // tile (alpha = 1 when nothing moved gives the same values).
                 asm volatile("");
                 const float m_new = move ? mt : m_run[qt];
-                const float alpha = fast_exp2((m_run[qt] - m_new) * kLog2e);
+                const float alpha = fast_exp2((m_run[qt] - m_new) * xs);
                 m_run[qt] = m_new;
                 lsum[qt][0] *= alpha;  // only component 0 is read
 #pragma unroll
                 for (int dt = 0; dt < G::DT; ++dt) acc[qt][dt] *= alpha;
             }
-            const float neg = -m_run[qt] * kLog2e;
+            const float neg = -m_run[qt] * xs;
             V8 pf[2];
 #pragma unroll
             for (int c = 0; c < 2; ++c)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) pf[c][j] = TR::from_f(fast_exp2(fmaf(x[qt][c][j], kLog2e, neg)));
+                for (int j = 0; j < 8; ++j) pf[c][j] = TR::from_f(fast_exp2(fmaf(x[qt][c][j], xs, neg)));
 #pragma unroll
             for (int c = 0; c < 2; ++c) lsum[qt] = TR::mfma(ones, pf[c], lsum[qt]);
 #pragma unroll
@@ -446,8 +513,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
                 store4<TR>(ga.gated + ((size_t)n * Sq + row) * ga.HD + h * D + d, r);
             }
         }
-        if (lse && eg == 0) lse[nh * Sq + row] = m_run[qt] + logf(l_tot);
+        if (lse && eg == 0) lse[nh * Sq + row] = (BM ? m_run[qt] * scale : m_run[qt]) + logf(l_tot);
     }
+}
+
+// The bias-MFMA constants for `scale`, when that form applies: scale > 0 with 1/scale finite
+// and within the input type's range (hi + lo = 1/scale to about 16 bits).
+template <typename TR>
+bool bias_mfma_for(float scale, BiasMfma* bm) {
+    using E = typename TR::elem;
+    if (!(scale > 0.f) || !std::isfinite(scale)) return false;
+    const float b = 1.f / scale;
+    if (!std::isfinite(b) || b > 6.0e4f) return false;
+    const float hi = (float)(E)b;
+    *bm = {hi, (float)(E)(b - hi), b, scale * kLog2e};
+    return true;
 }
 
 template <typename TR, int D, int QT, bool GATE>
@@ -457,14 +537,19 @@ void launch_fwd_qt(hipStream_t st, const void* q, const void* k, const void* v, 
     using E = typename TR::elem;
     const dim3 grid(ceil_div(Sq, 64 * QT) * H * N);
     const bool vec = Sk % 8 == 0 && (reinterpret_cast<uintptr_t>(kmask) & 7u) == 0;
-    if (vec)
-        attn_fwd_kernel<TR, D, QT, true, GATE><<<grid, 256, 0, st>>>(
+    BiasMfma bm{};
+    if (vec && bias_mfma_for<TR>(scale, &bm))
+        attn_fwd_kernel<TR, D, QT, true, GATE, true><<<grid, 256, 0, st>>>(
             (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (E*)out, lse, H, Sq, Sk,
-            scale, ga);
+            scale, ga, bm);
+    else if (vec)
+        attn_fwd_kernel<TR, D, QT, true, GATE, false><<<grid, 256, 0, st>>>(
+            (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (E*)out, lse, H, Sq, Sk,
+            scale, ga, bm);
     else
-        attn_fwd_kernel<TR, D, QT, false, GATE><<<grid, 256, 0, st>>>(
+        attn_fwd_kernel<TR, D, QT, false, GATE, false><<<grid, 256, 0, st>>>(
             (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (E*)out, lse, H, Sq, Sk,
-            scale, ga);
+            scale, ga, bm);
 }
 
 template <typename TR, int D, bool GATE>
