@@ -487,7 +487,8 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
     const typename TR::elem* __restrict__ v, const typename TR::elem* __restrict__ bias,
     const uint8_t* __restrict__ kmask, const typename TR::elem* __restrict__ out,
     const typename TR::elem* __restrict__ dout, const float* __restrict__ lse,
-    float* __restrict__ row_logit, float* __restrict__ lse2_out,
+    float* __restrict__ row_logit, unsigned long long* __restrict__ mbits,
+    float* __restrict__ lse2_out,
     float* __restrict__ ndi_out, typename TR::elem* __restrict__ dq,
     float* __restrict__ dq_part, float* __restrict__ dbias_dst, int N, int H, int Sq, int Sk,
     int NB, int nranges, float scale, LogitForm lf, typename TR::elem* __restrict__ bias_t,
@@ -504,9 +505,10 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
     __shared__ __attribute__((aligned(16))) char kv0[2 * KVB];
     __shared__ __attribute__((aligned(16))) char kv1[2 * KVB];
     // Per-row extras staged with Q/dO/O when VEC: lse of the block's 64 queries (256 bytes),
-    // then the mask bytes of the key range (MSK bytes, whole waves of 4-byte loads).
-    constexpr int MSK = (RK + 255) / 256 * 256;
-    constexpr int XB = VEC ? 256 + MSK : 0;
+    // then the row's presence words of the key range (RK/64 64-bit words; one wave of 4-byte
+    // loads, 256 bytes).
+    static_assert(RK % 64 == 0 && RK / 32 <= 64, "presence words of a key range: one wave");
+    constexpr int XB = VEC ? 512 : 0;
     __shared__ __attribute__((aligned(16))) char qd0[3 * QB + XB];
     __shared__ __attribute__((aligned(16))) char qd1[3 * QB + XB];
     __shared__ __attribute__((aligned(16))) char xch_raw[8 * 2 * DT * 64 * 16];
@@ -570,9 +572,12 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
             // Queries past Sq and keys past Sk read zeros. Mask rows are 8-byte aligned (VEC).
             char* ex = qd + 3 * QB;
             if (wave == 0) buf_dma4(buffer_rsrc(lse + nh * Sq, (uint32_t)Sq * 4), lane * 4, q0 * 4, ex);
-            if (kmask && wave >= 1 && wave <= MSK / 256)
-                buf_dma4(buffer_rsrc(kmask + (size_t)n * Sk, (uint32_t)Sk),
-                         (64 * (wave - 1) + lane) * 4, kbeg, ex + 256 * wave);
+            // Words kbeg/64 .. of the row's presence bits (kbeg % 64 == 0); words past the row
+            // read zeros.
+            const int words = (Sk + 63) >> 6;
+            if (kmask && wave == 1)
+                buf_dma4(buffer_rsrc(mbits + (size_t)n * words, (uint32_t)words * 8),
+                         lane * 4, (kbeg >> 6) * 8, ex + 256);
         }
     };
     // Per-row values kept in registers one row ahead when they are not staged (not VEC), raw:
@@ -629,11 +634,16 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
                                 ? reinterpret_cast<const float*>(ex)[32 * qg + 16 * qt + r16] * kLog2e
                                 : INFINITY;
             if (kmask) {
+                // Chunk i's 32 keys start at bit rel % 64 of staged word rel / 64 (rel = key
+                // offset in the range, a multiple of 32); the lane's 8 keys are bits 8g .. 8g+7
+                // of that. The word's address is the same in every lane (an LDS broadcast).
+                const unsigned long long* wd = reinterpret_cast<const unsigned long long*>(ex + 256);
 #pragma unroll
-                for (int i = 0; i < KCW; ++i)
-                    vbits |= nonzero_bits8(*reinterpret_cast<const u32x2*>(
-                                 ex + 256 + 32 * (i * KQ + kq) + 8 * g))
-                             << (8 * i);
+                for (int i = 0; i < KCW; ++i) {
+                    const int rel = 32 * (i * KQ + kq);
+                    const unsigned w32 = (unsigned)(wd[rel >> 6] >> (rel & 32));
+                    vbits |= ((w32 >> (8 * g)) & 0xffu) << (8 * i);
+                }
             } else {
                 vbits = 0xffffffu;
             }
@@ -794,18 +804,23 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
             __syncthreads();
         }
         if (kmask) {
+            // Also each row's presence bits, 64 keys per word (bit j of word i: key 64i + j is
+            // present), read by the row steps in place of the mask bytes (VEC).
+            const int words = (Sk + 63) >> 6;
             for (int nr = n0 + wave; nr < n1; nr += 8) {
                 const uint8_t* m = kmask + (size_t)nr * Sk;
                 bool any = false;
                 if constexpr (VEC) {
-                    for (int i = 8 * lane; i < Sk; i += 512) {
-                        const u32x2 b8 = *reinterpret_cast<const u32x2*>(m + i);
-                        any |= (b8[0] | b8[1]) != 0u;
+                    for (int i = 0; i < words; ++i) {
+                        const int kk = 64 * i + lane;
+                        const unsigned long long b = __ballot(kk < Sk && m[kk] != 0);
+                        any |= b != 0ull;
+                        if (lane == 0) mbits[(size_t)nr * words + i] = b;
                     }
                 } else {
                     for (int i = lane; i < Sk; i += 64) any |= m[i] != 0;
+                    any = __any(any);
                 }
-                any = __any(any);
                 if (lane == 0) row_logit[nr] = any ? kMaskedLogit : 0.f;
             }
             __syncthreads();  // this block's prefetches read them
@@ -1090,7 +1105,8 @@ constexpr int kTargetBlocks = 256;  // one 8-wave row-owner block per CU of an M
 struct BwdPlan {
     bool v2 = false;
     int KT = 0, KCW = 0, KSUB = 0, KNW = 0, nranges = 0, NB = 0, nchunks = 0, SqP = 0;
-    size_t off_di = 0, off_bt = 0, off_rowl = 0, off_lse2 = 0, off_ndi = 0, off_dbias = 0,
+    size_t off_di = 0, off_bt = 0, off_rowl = 0, off_mbits = 0, off_lse2 = 0, off_ndi = 0,
+           off_dbias = 0,
            off_dq = 0, bytes = 0;
 };
 
@@ -1141,6 +1157,8 @@ BwdPlan plan_bwd(int64_t N, int64_t H, int64_t Sq, int64_t Sk, int64_t D) {
         off += align256((size_t)(H * Sk) * p.SqP * 2);
         p.off_rowl = off;
         off += align256((size_t)N * sizeof(float));
+        p.off_mbits = off;  // 64-bit presence words of each mask row
+        off += align256((size_t)N * ((Sk + 63) / 64) * 8);
         p.off_lse2 = off;
         off += align256(rows * sizeof(float));
         p.off_ndi = off;
@@ -1236,15 +1254,15 @@ void run_bwd_v1(hipStream_t st, const BwdPlan& p, const void* q, const void* k, 
 template <typename TR, int D, int KCW, bool VEC>
 void launch_dq2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, const void* v,
                 const void* bias, const uint8_t* kmask, const void* out, const void* dout,
-                const float* lse, float* rowl, float* lse2, float* ndi, void* dq,
-                float* dq_part, float* dbias_dst, void* bias_t, int N, int H, int Sq, int Sk,
-                float scale) {
+                const float* lse, float* rowl, unsigned long long* mbits, float* lse2, float* ndi,
+                void* dq, float* dq_part, float* dbias_dst, void* bias_t, int N, int H, int Sq,
+                int Sk, float scale) {
     using E = typename TR::elem;
     const dim3 grid(ceil_div(Sq, 64) * H * p.nchunks * p.nranges);
     KernelTimer timer("attn_bwd_dq", st);
     attn_bwd_dq2<TR, D, KCW, VEC><<<grid, 512, 0, st>>>(
         (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (const E*)out,
-        (const E*)dout, lse, rowl, lse2, ndi, (E*)dq, dq_part, dbias_dst, N, H, Sq, Sk, p.NB,
+        (const E*)dout, lse, rowl, mbits, lse2, ndi, (E*)dq, dq_part, dbias_dst, N, H, Sq, Sk, p.NB,
         p.nranges, scale, LogitForm::make(scale), (E*)bias_t, p.SqP, ceil_div(p.SqP, 64),
         ceil_div(Sk, 64));
 }
@@ -1270,6 +1288,7 @@ void run_bwd_v2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, 
     using E = typename TR::elem;
     E* bias_t = reinterpret_cast<E*>(ws + p.off_bt);
     float* rowl = reinterpret_cast<float*>(ws + p.off_rowl);
+    unsigned long long* mbits = reinterpret_cast<unsigned long long*>(ws + p.off_mbits);
     float* lse2 = reinterpret_cast<float*>(ws + p.off_lse2);
     float* ndi = reinterpret_cast<float*>(ws + p.off_ndi);
     float* dbias_part = reinterpret_cast<float*>(ws + p.off_dbias);
@@ -1278,8 +1297,9 @@ void run_bwd_v2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, 
     switch (p.KCW) {
 #define CLK_KCW(V)                                                                               \
     case V:                                                                                      \
-        launch_dq2<TR, D, V, VEC>(st, p, q, k, v, bias, kmask, out, dout, lse, rowl, lse2, ndi,  \
-                                  dq, dq_part, dbias_dst, bias_t, N, H, Sq, Sk, scale);          \
+        launch_dq2<TR, D, V, VEC>(st, p, q, k, v, bias, kmask, out, dout, lse, rowl, mbits,     \
+                                  lse2, ndi, dq, dq_part, dbias_dst, bias_t, N, H, Sq, Sk,       \
+                                  scale);                                                        \
         break;
         CLK_KCW(1) CLK_KCW(2) CLK_KCW(3)
 #undef CLK_KCW

@@ -216,7 +216,8 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_generic(const void* __restric
 
 // Backward. Per row: dx = r*(g - mean(g) - xhat*mean(g*xhat)), g = scale*dy. Column sums of
 // dy*xhat and dy accumulate per lane over the rows the lane visits, then over the block's row
-// slots in a fixed order, into part[block][2][C]; ln_colsum adds the blocks in a fixed order.
+// slots in a fixed order, into the column-major partials part[which*C + c][block];
+// ln_colsum_runs adds each column's blocks in a fixed order.
 template <typename TR, int LPR, int NV, int RB>
 __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const void* __restrict__ xv,
                                                           const float* __restrict__ scale,
@@ -330,11 +331,13 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const void* __restrict
             red[slot][1][c] = acc_b[v][i];
         }
     __syncthreads();
+    // Column-major partials, part[t][block] for t = which*C + c, so that each column's sums
+    // over the blocks are one contiguous run for ln_colsum_runs.
     for (int t = threadIdx.x; t < 2 * C; t += kThreads) {
         const int which = t / C, c = t % C;
         float a = 0.f;
         for (int r = 0; r < ROWS; ++r) a += red[r][which][c];
-        part[((size_t)blockIdx.x * 2 + which) * C + c] = a;
+        part[(size_t)t * gridDim.x + blockIdx.x] = a;
     }
 }
 
@@ -431,6 +434,57 @@ __global__ __launch_bounds__(1024) void ln_colsum(const float* __restrict__ part
         for (int i = 0; i < kSplit; ++i) r += red[i][cl];
         if (t < C) dscale[t] = r;
         else doffset[t - C] = r;
+    }
+}
+
+// out[t] (t = which*C + c) = sum of the run part[t*nblocks .. t*nblocks + nblocks-1], one wave
+// per output. With nblocks % 4 == 0 (16-byte aligned runs) lane l adds the 4-float pieces
+// l, l+64, ... into eight 4-wide accumulators (piece p into accumulator (p/64) % 8; 2048 blocks
+// are one round of eight 16-byte loads per lane), otherwise single floats the same way; then
+// the accumulators in order and the lanes in a fixed butterfly. Deterministic.
+__global__ __launch_bounds__(256) void ln_colsum_runs(const float* __restrict__ part, int nblocks,
+                                                      int C, float* __restrict__ dscale,
+                                                      float* __restrict__ doffset) {
+    const int t = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (t >= 2 * C) return;  // whole waves
+    const float* run = part + (size_t)t * nblocks;
+    float a = 0.f;
+    if ((nblocks & 3) == 0) {
+        const f32x4* r4 = reinterpret_cast<const f32x4*>(run);
+        const int n4 = nblocks >> 2;
+        f32x4 acc[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        int b = lane;
+        for (; b + 7 * 64 < n4; b += 8 * 64) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] += r4[b + 64 * i];
+        }
+#pragma unroll
+        for (int i = 0; i < 7; ++i)
+            if (b + 64 * i < n4) acc[i] += r4[b + 64 * i];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a += (acc[i][0] + acc[i][1]) + (acc[i][2] + acc[i][3]);
+    } else {
+        float acc[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc[i] = 0.f;
+        int b = lane;
+        for (; b + 7 * 64 < nblocks; b += 8 * 64) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) acc[i] += run[b + 64 * i];
+        }
+#pragma unroll
+        for (int i = 0; i < 7; ++i)
+            if (b + 64 * i < nblocks) acc[i] += run[b + 64 * i];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) a += acc[i];
+    }
+    a = group_sum<64>(a);
+    if (lane == 0) {
+        if (t < C) dscale[t] = a;
+        else doffset[t - C] = a;
     }
 }
 
@@ -659,7 +713,8 @@ void launch_bwd(hipStream_t st, const void* x, const float* sc, const void* dy, 
     ln_bwd_kernel<TR, LPR, NV, RB><<<grid, kThreads, 0, st>>>(x, sc, dy, dx, part, M, rpb, eps);
 }
 
-// Returns the number of partial rows written and their stride (floats).
+// Returns the number of partial rows written and their stride (floats); stride 0: the fast
+// kernel's column-major runs (part[t][block]).
 template <typename TR>
 void dispatch_bwd(hipStream_t st, const void* x, const float* sc, const void* dy, void* dx,
                   float* part, int M, int C, float eps, int* nblocks, size_t* stride) {
@@ -668,7 +723,7 @@ void dispatch_bwd(hipStream_t st, const void* x, const float* sc, const void* dy
     if (rs.lpr == (L) && rs.nv == (V)) {                           \
         launch_bwd<TR, L, V>(st, x, sc, dy, dx, part, M, eps);     \
         *nblocks = ceil_div(M, fast_bwd_rows_per_block(M, L));     \
-        *stride = 2 * (size_t)C;                                   \
+        *stride = 0; /* column-major runs */                       \
         return;                                                    \
     }
 #define CLK_LN_ROW(L) CLK_LN_CASE(L, 1) CLK_LN_CASE(L, 2) CLK_LN_CASE(L, 3) CLK_LN_CASE(L, 4)
@@ -786,8 +841,12 @@ extern "C" clk_status clk_layer_norm_bwd(hipStream_t stream, clk_dtype dtype, co
             break;
     }
     KernelTimer timer("ln_bwd_colsum", stream);
-    ln_colsum<<<ceil_div(2 * C, kColsumCols), 1024, 0, stream>>>(part, stride, nblocks, (int)C,
-                                                                 dscale, doffset);
+    if (stride == 0)
+        ln_colsum_runs<<<ceil_div(2 * C, 4), 256, 0, stream>>>(part, nblocks, (int)C, dscale,
+                                                              doffset);
+    else
+        ln_colsum<<<ceil_div(2 * C, kColsumCols), 1024, 0, stream>>>(part, stride, nblocks,
+                                                                     (int)C, dscale, doffset);
     return check_launch("layer_norm_bwd");
 }
 
