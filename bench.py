@@ -507,19 +507,49 @@ def issue_bound(kernel, avg_ms, scores):
             "frac": (valu_ms + mfma_ms) / avg_ms}
 
 
+def _kernel_key(r):
+    name = r["Kernel_Name"].replace("(anonymous namespace)::", "")
+    name = re.sub(r"^void |clk::", "", name.split("(")[0])
+    if "Grid_Size" in r:
+        grid, wg = int(r["Grid_Size"]), int(r["Workgroup_Size"])
+    else:
+        grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+        wg = int(r["Workgroup_Size_X"]) * int(r["Workgroup_Size_Y"]) * int(r["Workgroup_Size_Z"])
+    return name, grid // max(1, wg)
+
+
+def trace_summary(path):
+    """Markdown rows from a rocprofv3 --kernel-trace csv: per kernel and grid, calls and the
+    average / min / max duration in microseconds and the share of all kernel time."""
+    import csv
+    per = {}
+    for r in csv.DictReader(open(path)):
+        d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        per.setdefault(_kernel_key(r), []).append(d)
+    total = sum(sum(v) for v in per.values())
+    print("| kernel | workgroups | calls | avg us | min us | max us | total % |")
+    print("|---|---|---|---|---|---|---|")
+    for (name, wgs), v in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+        if name.startswith(("at::", "rocprim::")):  # input generation and timing scaffolding
+            continue
+        print("| `%s` | %d | %d | %.1f | %.1f | %.1f | %.1f |" % (
+            name, wgs, len(v), sum(v) / len(v), min(v), max(v), 100.0 * sum(v) / total))
+    return 0
+
+
 def counter_summary(paths):
     """Markdown rows: per kernel and grid (workgroups; one workload each), dispatch count and the
     median per dispatch of each counter in rocprofv3 --pmc csv files (values of one dispatch
-    summed over its dimension instances)."""
+    summed over its dimension instances). A --kernel-trace csv gives durations instead."""
     import csv
     import statistics
+    if len(paths) == 1 and "Counter_Name" not in open(paths[0]).readline():
+        return trace_summary(paths[0])
     per = {}
     for path in paths:
         with open(path) as fh:
             for r in csv.DictReader(fh):
-                name = r["Kernel_Name"].replace("(anonymous namespace)::", "")
-                name = re.sub(r"^void |clk::", "", name.split("(")[0])
-                wgs = int(r["Grid_Size"]) // max(1, int(r["Workgroup_Size"]))
+                name, wgs = _kernel_key(r)
                 key = (r["Dispatch_Id"], r["Counter_Name"])
                 d = per.setdefault((name, wgs), {})
                 d[key] = d.get(key, 0.0) + float(r["Counter_Value"])
@@ -527,6 +557,8 @@ def counter_summary(paths):
     print("| kernel | workgroups | dispatches | " + " | ".join(counters) + " |")
     print("|---" * (len(counters) + 3) + "|")
     for (name, wgs), d in sorted(per.items()):
+        if name.startswith(("at::", "rocprim::")):  # input generation and timing scaffolding
+            continue
         cols = []
         for c in counters:
             vals = [v for (disp, cn), v in d.items() if cn == c]
@@ -577,7 +609,8 @@ def main(argv=None):
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (counter calibration)")
     ap.add_argument("--counter-summary", nargs="+", metavar="CSV",
-                    help="only summarise rocprofv3 --pmc csv files per kernel (no GPU)")
+                    help="only summarise rocprofv3 --pmc (or one --kernel-trace) csv files per "
+                         "kernel (no GPU)")
     args = ap.parse_args(argv)
     if args.counter_summary:
         return counter_summary(args.counter_summary)
