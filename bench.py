@@ -1,18 +1,22 @@
 """Benchmark of the Evoformer hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--min-warmup-ms T] [--no-cpu-baseline]
 
 Headline (one JSON line on stdout): triangle attention forward + backward at N_res = 384
 (q, k, v [384 rows, 4 heads, 384 residues, 32], bf16 in, float32 accumulate), in TFLOP/s of
 algorithmic work 12*N*H*Sq*Sk*D per step. A step is one forward and one backward over the whole
 batch, through the C ABI with preallocated buffers; inputs rotate over 3 sets (~0.9 GB) so the
-256 MB Infinity Cache cannot hold them. ms_per_step is the median of the per-step durations (one
-HIP event between consecutive steps on the launch stream); the bracket mean is reported beside it. Secondary figures: LayerNorm forward/backward and
-LayerNorm + gated dual projection on the 512x512x128 pair representation, and the attention
-output gate of MSA row attention (512 rows x 256 queries, 8 x 32 heads, 256 channels), in HBM
-GB/s; the gated dual projection backward on [512*512, 128] per kernel; the pair-bias projection
-LN(z).w -> [4,512,512] in GB/s; the triangle multiplication
-(outgoing, incoming) on z [512,512,128] per kernel.
+256 MB Infinity Cache cannot hold them. Exactly K steps are timed after W untimed warm-up steps;
+the warm-up continues past W steps until T ms (default 100) have passed, because the GPU's
+clocks ramp up over its first ~20 ms of work (the first 50 steps of a process run ~8% slower
+than every later pass); the JSON line reports the warm-up steps actually run. ms_per_step is the
+median of the per-step durations (one HIP event between consecutive steps on the launch
+stream); the bracket mean, min and max are reported beside it. Secondary figures: LayerNorm
+forward/backward, LayerNorm + gated dual projection, the plain projection and its backward and
+the pair-bias projection on the 512x512x128 pair representation; the attention output gate of
+MSA row attention (512 rows x 256 queries, 8 x 32 heads, 256 channels); gated attention fused
+and separate on MSA rows and at N_res = 1024; the triangle multiplication (outgoing, incoming)
+on z [512,512,128] per kernel; the library's streaming copy as the HBM ceiling.
 
 The roofline block names the kernel with the most time per step, its algorithmic work per launch
 divided by its average duration from per-launch HIP events on the launch stream (the library's
@@ -21,7 +25,10 @@ roofline.traffic is the dominant kernel's HBM bytes per launch as recorded by th
 rocprofv3 FETCH_SIZE/WRITE_SIZE summaries in profiles/*hbm_traffic*.md (lines
 "traffic_bytes_per_launch[<kernel>]: <bytes>"), null when none covers the kernel. Those runs
 scale each counter by what it reads for a plain device copy of known size, which
-"--copy-calibration MIB" performs (and nothing else).
+"--copy-calibration MIB" performs (and nothing else). roofline.issue is the same kernel's
+instruction-issue floor -- its VALU, transcendental and MFMA wave instructions per launch, from
+the committed profiles/*instruction_mix*.md, at 4, 16 and 16 cycles each over the 1024 SIMDs at
+2.4 GHz -- and frac = floor / measured duration.
 cpu_baseline times the same math in torch float32 on the host cores (oracle/cpu_baseline.py) on
 all 384 rows by default (--cpu-rows for fewer), repeated for about --cpu-seconds (10 s) and
 reported as the median run in the same unit.
@@ -105,13 +112,29 @@ def attention_step(lib, native, stream, s):
         raise RuntimeError(native.last_error())
 
 
-def timed(torch, fn, steps, warmup, stream_obj, stats=None):
+def timed(torch, fn, steps, warmup, stream_obj, stats=None, min_warmup_ms=0.0):
     """Median ms per step over `steps` timed steps after `warmup` untimed ones: one HIP event on
     the launch stream before each step and one after the last, so every step has its own
-    duration. `stats` (a dict), when given, also receives the mean over the whole bracket."""
-    for i in range(warmup):
+    duration. With min_warmup_ms > 0 the warm-up continues past `warmup` steps until that much
+    wall time has passed (the GPU's clocks ramp up over its first ~20 ms of work). `stats` (a
+    dict), when given, also receives the mean over the whole bracket and the warm-up actually
+    run."""
+    t0 = time.perf_counter()
+    i = 0
+    while i < warmup:
         fn(i)
+        i += 1
+    if min_warmup_ms > 0:
+        torch.cuda.synchronize()
+        while (time.perf_counter() - t0) * 1e3 < min_warmup_ms:
+            fn(i)
+            i += 1
+            if i % 16 == 0:
+                torch.cuda.synchronize()
     torch.cuda.synchronize()
+    if stats is not None:
+        stats["warmup_run"] = i
+        stats["warmup_ms"] = (time.perf_counter() - t0) * 1e3
     ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     ev[0].record(stream_obj)
     for i in range(steps):
@@ -603,6 +626,8 @@ def main(argv=None):
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--min-warmup-ms", type=float, default=100.0,
+                    help="keep warming up past --warmup steps until this much time has passed")
     ap.add_argument("--cpu-rows", type=int, default=N_ROWS)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-secondary", action="store_true")
@@ -639,7 +664,8 @@ def main(argv=None):
 
     print("bench: timing attention fwd+bwd", file=sys.stderr, flush=True)
     step_stats = {}
-    ms = timed(torch, step, args.steps, args.warmup, so, step_stats)
+    ms = timed(torch, step, args.steps, args.warmup, so, step_stats,
+               min_warmup_ms=args.min_warmup_ms)
     fl = attention_flops(N_ROWS, HEADS, NRES, NRES, HEAD_DIM)
     tflops = fl["step"] / (ms * 1e-3) / 1e12
     kernels = per_kernel(torch, native, step, args.steps)
@@ -655,7 +681,8 @@ def main(argv=None):
 
     result = {
         "metric": METRIC, "value": tflops, "unit": "TFLOP/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": ms,
+        "steps": args.steps, "warmup": args.warmup, "warmup_run": step_stats["warmup_run"],
+        "warmup_ms": step_stats["warmup_ms"], "ms_per_step": ms,
         "ms_per_step_mean": step_stats["mean_ms"], "ms_per_step_min": step_stats["min_ms"],
         "ms_per_step_max": step_stats["max_ms"],
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",

@@ -699,8 +699,6 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
         for (int i = 0; i < KCW; ++i) {
             const int c0 = 32 * (i * KQ + kq);  // chunk's first key, relative to kbeg
             if (kbeg + c0 >= kend) continue;   // wave-uniform
-            // One chunk's operands live at a time; interleaving chunks only adds registers.
-            __builtin_amdgcn_sched_barrier(0);
             V8 kf[2], vf[2];
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
