@@ -2,6 +2,8 @@
 // staging, MFMA operand reads from LDS, bias/mask loads and host-side validation.
 #pragma once
 
+#include <cmath>
+
 #include "common.hpp"
 
 namespace clk {
@@ -291,6 +293,32 @@ struct LogitForm {
         return fabsf(v) > 1e38f ? copysignf(1e38f, v) : v;
     }
 };
+
+// How the logits reach the softmax in the kernels that stream bias tiles through LDS (the
+// forward and the dK/dV kernel). Plain: logit = fmaf(q.k, scale, bias) per score (bias unpacked
+// to float32). Bias MFMA (when scale > 0): the accumulator of each 16x16 score tile starts as
+// bias / scale, added by one more MFMA per 16x16 tile whose A
+// operand is [hi*I | lo*I] (hi + lo = 1/scale as two values of the input type, each product
+// with a bias value exact in float32) and whose B operand is the tile's bias, duplicated over
+// the two halves of the contraction; the tile then holds logit / scale, and
+// log2(e) * logit = cexp * S with cexp = scale * log2(e). No per-score instruction touches the bias. A bias of
+// magnitude above 3.4e38 * scale overflows there (float32 cannot hold bias / scale).
+struct BiasMfma {
+    float hi, lo, bscale, cexp;
+};
+
+// The bias-MFMA constants for `scale`, when that form applies: scale > 0 with 1/scale finite
+// and within the input type's range (hi + lo = 1/scale to about 16 bits).
+template <typename TR>
+bool bias_mfma_for(float scale, BiasMfma* bm) {
+    using E = typename TR::elem;
+    if (!(scale > 0.f) || !std::isfinite(scale)) return false;
+    const float b = 1.f / scale;
+    if (!std::isfinite(b) || b > 6.0e4f) return false;
+    const float hi = (float)(E)b;
+    *bm = {hi, (float)(E)(b - hi), b, scale * kLog2e};
+    return true;
+}
 
 // Host-side shape/dtype validation shared by the forward and backward entry points. The
 // reference checks only the rank of q (cuda/volta_mma_attn.cu:310-314); every size is checked

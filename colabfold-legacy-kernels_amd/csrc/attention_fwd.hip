@@ -25,8 +25,6 @@
 // rounding unit there is 128), which would scale P by up to 2^64.
 // lse = m + log(l) (natural log) is written when requested, for the backward pass; for an
 // all-masked row it is therefore ln(Sk), relative to the masked logit.
-#include <cmath>
-
 #include "attention_common.hpp"
 
 namespace clk {
@@ -144,18 +142,6 @@ struct GateArgs {
     const E* bg;
     E* gated;
     int C, HD;
-};
-
-// How the logits reach the softmax. Plain: logit = fmaf(q.k, scale, bias) per score (bias
-// unpacked to float32). Bias MFMA (`bm`, used when the bias tile is in LDS and scale > 0): the
-// accumulator of S^T starts as bias / scale, added by one more MFMA per 16x16 tile whose A
-// operand is [hi*I | lo*I] (hi + lo = 1/scale as two values of the input type, each product
-// with a bias value exact in float32) and whose B operand is the tile's bias, duplicated over
-// the two halves of the contraction; S^T then holds logit / scale, and log2(e) * logit =
-// cexp * S with cexp = scale * log2(e). No per-score instruction touches the bias. A bias of
-// magnitude above 3.4e38 * scale overflows there (float32 cannot hold bias / scale).
-struct BiasMfma {
-    float hi, lo, bscale, cexp;
 };
 
 template <typename TR, int D, int QT, bool VEC, bool GATE, bool BM>
@@ -515,19 +501,6 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
         }
         if (lse && eg == 0) lse[nh * Sq + row] = (BM ? m_run[qt] * scale : m_run[qt]) + logf(l_tot);
     }
-}
-
-// The bias-MFMA constants for `scale`, when that form applies: scale > 0 with 1/scale finite
-// and within the input type's range (hi + lo = 1/scale to about 16 bits).
-template <typename TR>
-bool bias_mfma_for(float scale, BiasMfma* bm) {
-    using E = typename TR::elem;
-    if (!(scale > 0.f) || !std::isfinite(scale)) return false;
-    const float b = 1.f / scale;
-    if (!std::isfinite(b) || b > 6.0e4f) return false;
-    const float hi = (float)(E)b;
-    *bm = {hi, (float)(E)(b - hi), b, scale * kLog2e};
-    return true;
 }
 
 template <typename TR, int D, int QT, bool GATE>
