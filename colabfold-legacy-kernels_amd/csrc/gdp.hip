@@ -493,8 +493,10 @@ __global__ __launch_bounds__(64 * NB * N / 32 + 256) void ln_gdp_kernel(
     u32x4 pend[SUB] = {};
     u32x2 pendc[SUB][2] = {};
     Rsrc pend_out = buffer_rsrc(out, 0);
-    int pend_row = 0;
-    const Rsrc plane_out = buffer_rsrc(out, CM ? (uint32_t)((size_t)M * N * 2) : 0u);
+    // CM: the pending tile's first row in channel 0's plane (null before the first tile). The
+    // planes span M*N*2 bytes, past a buffer offset's 32 bits for large M, so the channel-major
+    // stores take 64-bit addresses.
+    E* pend_plane = nullptr;
     auto out_rsrc = [&](int t) {
         const int rows = min(R, M - t * R);
         return buffer_rsrc(out + (size_t)t * R * N, (uint32_t)rows * N * 2);
@@ -503,14 +505,15 @@ __global__ __launch_bounds__(64 * NB * N / 32 + 256) void ln_gdp_kernel(
         if constexpr (CM) {
             // Rows 16g .. 16g+15 of one column: two 16-byte pieces per lane, which with the
             // other three lane groups fill the column's 128-byte line of the tile.
+            if (pend_plane == nullptr) return;
 #pragma unroll
             for (int h = 0; h < 2; ++h) {
                 const int col = 32 * cb + 8 * (r16 >> 2) + 4 * h + (r16 & 3);
+                E* const at = pend_plane + (size_t)col * M + 16 * g;
 #pragma unroll
                 for (int half = 0; half < 2; ++half) {
                     const u32x2 a = pendc[2 * half][h], b = pendc[2 * half + 1][h];
-                    buf_st16(pend_out, (col * M + pend_row + 16 * g + 8 * half) * 2, 0,
-                             u32x4{a[0], a[1], b[0], b[1]});
+                    *reinterpret_cast<u32x4*>(at + 8 * half) = u32x4{a[0], a[1], b[0], b[1]};
                 }
             }
         } else {
@@ -563,8 +566,7 @@ __global__ __launch_bounds__(64 * NB * N / 32 + 256) void ln_gdp_kernel(
             }
         }
         if constexpr (CM) {
-            pend_out = plane_out;
-            pend_row = t * R;
+            pend_plane = out + (size_t)t * R;
         } else {
             pend_out = out_rsrc(t);
         }
@@ -756,7 +758,7 @@ clk_status dispatch_ln_gdp(hipStream_t st, const void* z, const float* gamma, co
 }  // namespace
 
 // LayerNorm + both gated branches with channel-major outputs a, b [N][M], for the triangle-
-// multiplication contraction. Arguments checked by the caller; M % 64 == 0 and M*N*2 < 2^31.
+// multiplication contraction. Arguments checked by the caller; M % 64 == 0.
 clk_status ln_gdp_channel_major(hipStream_t st, clk_dtype dtype, const void* z,
                                 const float* gamma, const float* beta, const void* const* w,
                                 const void* const* bias, const void* mask, void* a, void* b, int M,

@@ -329,17 +329,19 @@ __global__ __launch_bounds__(512) void tri_out_kernel(TriOutParams<typename TR::
     const int ntiles = M / R;
     // Every tile issues DPX + DPZ direct-to-LDS loads and SUBW stores in every wave (tiles past
     // the end load from empty resources; the first store batch goes to an empty resource).
+    // One x load of a wave covers eight channels: its resource starts at the first of them, so
+    // offsets stay below 8*M*2 bytes whatever C*M is.
     auto stage = [&](int t, char* xb, char* zb) {
         const bool live = t < ntiles;
-        const Rsrc rx = buffer_rsrc(live ? pr.x + (size_t)t * R : pr.x,
-                                    live ? (uint32_t)((size_t)(C - 1) * M * 2 + R * 2) : 0u);
         const Rsrc rz = buffer_rsrc(live ? pr.z + (size_t)t * R * C : pr.z,
                                     live ? (uint32_t)(R * C * 2) : 0u);
 #pragma unroll
         for (int k = 0; k < DPX; ++k) {
-            const int b = k * NT + wave * 64, slot = b + lane;
-            const int c = slot / (R / 8), q = slot % (R / 8);
-            buf_dma16(rx, (c * M + q * 8) * 2, 0, xb + b * 16 + (b / 64) * 16);
+            const int b = k * NT + wave * 64, c0 = b / (R / 8);
+            const Rsrc rx = buffer_rsrc(live ? pr.x + (size_t)c0 * M + (size_t)t * R : pr.x,
+                                        live ? (uint32_t)(7u * (uint32_t)M * 2u + R * 2) : 0u);
+            const uint32_t c = lane / (R / 8), q = lane % (R / 8);
+            buf_dma16(rx, (int)((c * (uint32_t)M + q * 8) * 2u), 0, xb + b * 16 + (b / 64) * 16);
         }
 #pragma unroll
         for (int k = 0; k < DPZ; ++k) {
@@ -347,14 +349,13 @@ __global__ __launch_bounds__(512) void tri_out_kernel(TriOutParams<typename TR::
             buf_dma16(rz, (b + lane) * 16, 0, zb + b * 16);
         }
     };
-    const Rsrc out_all = buffer_rsrc(pr.out, (uint32_t)((size_t)M * C * 2));
+    // The pending tile's output rows (an empty resource before the first tile).
     u32x4 pend[SUBW] = {};
     Rsrc pend_out = buffer_rsrc(pr.out, 0);
-    int pend_row = 0;
     auto flush = [&]() {
 #pragma unroll
         for (int s = 0; s < SUBW; ++s) {
-            const int row = pend_row + 16 * (sh * SUBW + s) + r16;
+            const int row = 16 * (sh * SUBW + s) + r16;
             buf_st16(pend_out, (row * C + 32 * cb + 8 * g) * 2, 0, pend[s]);
         }
     };
@@ -429,8 +430,7 @@ __global__ __launch_bounds__(512) void tri_out_kernel(TriOutParams<typename TR::
         }
         lds_barrier();  // xh1, xh2 of tile t ready; xn, zn are free
         stage(t + 2 * gridDim.x, xn, zn);
-        pend_out = out_all;
-        pend_row = t * R;
+        pend_out = buffer_rsrc(pr.out + (size_t)t * R * C, R * C * 2);
 #pragma unroll
         for (int s = 0; s < SUBW; ++s) {
             const int xrow = 16 * (sh * SUBW + s) + r16;
@@ -596,8 +596,10 @@ extern "C" clk_status clk_triangle_multiply(hipStream_t stream, clk_dtype dtype,
                     dtype_name(dtype));
     if (N < 0 || (C != 64 && C != 128))
         return fail(CLK_INVALID_ARGUMENT, "%s: C must be 64 or 128 (C=%lld)", who, (long long)C);
-    if (padded_n(N) * padded_n(N) * C * 2 >= ((int64_t)1 << 31))
-        return fail(CLK_INVALID_ARGUMENT, "%s: N=%lld too large", who, (long long)N);
+    // The contraction's limit (its transposed operands span one channel plane per resource).
+    if (padded_n(N) > 16384)
+        return fail(CLK_INVALID_ARGUMENT, "%s: N=%lld too large (at most 16384)", who,
+                    (long long)N);
     if (N == 0) return ok();
     if (!z || !mask || !ln || !w || !b || !out || !workspace)
         return fail(CLK_INVALID_ARGUMENT, "%s: null operand pointer", who);

@@ -240,8 +240,8 @@ clk_status clk_triangle_einsum(hipStream_t stream, clk_dtype dtype, const void* 
  * w[0..5] = left projection, right projection, left gate, right gate, output projection, output
  * gate, each [C,C] row-major (input channel first); b[0..5] their [C] biases; ln[0..3] = LN_in
  * scale, offset, LN_c scale, offset (float32 [C]). z, mask, weights, biases and out of dtype
- * CLK_F16 or CLK_BF16. C = 64 or 128; any N (a ragged N runs on a zero-padded grid of
- * N rounded up to 8, the padded positions masked). The workspace holds left, right and x
+ * CLK_F16 or CLK_BF16. C = 64 or 128; N up to 16384 (a ragged N runs on a zero-padded grid
+ * of N rounded up to 8, the padded positions masked). The workspace holds left, right and x
  * channel-major, and for a ragged N the padded z, mask and output
  * (clk_triangle_multiply_workspace_size bytes).
  */

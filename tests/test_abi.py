@@ -191,3 +191,33 @@ def test_gdp_bwd_validation(m, k, n, msg):
     lib = _native.lib()
     assert lib.clk_gated_dual_proj_bwd(None, BF16, *([FAKE] * 13), 1 << 30, m, k, n, 0) == INVALID
     assert msg in _native.last_error()
+
+
+def tri_mul(**kw):
+    arr = lambda n: (ctypes.c_void_p * n)(*([FAKE] * n))  # noqa: E731
+    a = dict(stream=None, dtype=BF16, z=FAKE, mask=FAKE, ln=arr(4), w=arr(6), b=arr(6), out=FAKE,
+             workspace=FAKE, workspace_bytes=1 << 62, N=64, C=128, outgoing=1, eps=1e-5)
+    a.update(kw)
+    return _native.lib().clk_triangle_multiply(*a.values())
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(C=96), "64 or 128"), (dict(dtype=F32), "dtype"), (dict(N=16385), "too large"),
+    (dict(N=20000, C=64), "too large"), (dict(z=None), "null"), (dict(ln=None), "null"),
+    (dict(out=FAKE + 8), "aligned"), (dict(workspace_bytes=1024), "workspace"),
+])
+def test_triangle_multiply_validation(kw, msg):
+    assert tri_mul(**kw) == INVALID
+    assert msg in _native.last_error()
+
+
+def test_triangle_multiply_sizes():
+    """The largest grid is accepted up to the workspace check; its workspace holds three
+    channel-major plane sets of 2 bytes per element (ragged N adds the padded z, mask, out)."""
+    lib = _native.lib()
+    assert tri_mul(N=16384, workspace_bytes=1024) == INVALID
+    assert "workspace" in _native.last_error()
+    assert lib.clk_triangle_multiply_workspace_size(16384, 128) == 3 * 128 * 16384 ** 2 * 2
+    assert lib.clk_triangle_multiply_workspace_size(4000, 64) == 3 * 64 * 4000 ** 2 * 2
+    assert lib.clk_triangle_multiply_workspace_size(4001, 64) > 4 * 64 * 4008 ** 2 * 2
+    assert tri_mul(N=0) == _native.OK

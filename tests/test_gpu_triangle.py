@@ -1,4 +1,5 @@
 """Triangle-multiplication contraction on the GPU against the float64 oracle."""
+import numpy as np
 import pytest
 import torch
 
@@ -110,3 +111,31 @@ def test_triangle_multiply_f16_and_repeatable(cuda):
     r = ref.triangle_multiply(np64(z), np64(mask), tuple(map(np64, ln_in)), [np64(w) for w in ws],
                               [np64(b) for b in bs], tuple(map(np64, ln_c)), True)
     assert_close("out", out, r, 1e-2)
+
+
+# Grids whose channel-major planes pass 2^31 bytes (N^2 * C * 2 at C = 128 from N = 2897): offsets
+# into the projection planes, x and out need more than 31 bits. Outgoing at N = 3000 (a multiple
+# of 8); incoming at a ragged N = 2901 (run on the zero-padded 2904 grid). Positions: the four
+# corners, the last 64-position tile, and random ones; every channel of each.
+@pytest.mark.parametrize("n,outgoing", [(3000, True), (2901, False)],
+                         ids=["3000-outgoing", "2901-incoming"])
+def test_triangle_multiply_large_grid_sampled(cuda, n, outgoing):
+    c = 128
+    gd = torch.Generator(device=cuda).manual_seed(n)
+    z = torch.randn((n, n, c), generator=gd, device=cuda).to(torch.bfloat16)
+    mask = (torch.rand((n, n), generator=gd, device=cuda) > 0.1).to(torch.bfloat16)
+    _, _, ln_in, ws, bs, ln_c = module_case(8, c, torch.bfloat16, n, cuda)
+    out = ops.triangle_multiply(z, mask, ln_in, ws, bs, ln_c, outgoing)
+    rng = np.random.default_rng(n)
+    pos = [(0, 0), (n - 1, n - 1), (n - 1, 0), (0, n - 1), (n - 1, n - 40), (n - 2, n - 7)]
+    pos += [tuple(map(int, rng.integers(0, n, 2))) for _ in range(6)]
+
+    def line(kind, idx):
+        if kind == "row":
+            return np64(z[idx]), np64(mask[idx])
+        return np64(z[:, idx]), np64(mask[:, idx])
+
+    r = ref.triangle_multiply_at(line, tuple(map(np64, ln_in)), [np64(w) for w in ws],
+                                 [np64(b) for b in bs], tuple(map(np64, ln_c)), pos, outgoing)
+    got = torch.stack([out[i, j] for i, j in pos])
+    assert_close("out", got, r, 2e-2)

@@ -398,6 +398,25 @@ def test_triangle_multiply_matches_torch():
         np.testing.assert_allclose(out, ref.numpy(), rtol=1e-12, atol=1e-13)
 
 
+def test_triangle_multiply_at_matches_the_whole_grid():
+    """The position-sampled statement equals the whole-grid one at every position, both
+    directions (a swapped i/j, row/column or left/right fails it: the module is not symmetric)."""
+    r = np.random.default_rng(9)
+    n, c = 7, 5
+    z = r.standard_normal((n, n, c))
+    mask = (r.random((n, n)) > 0.2).astype(np.float64)
+    ln_in = (1 + 0.1 * r.standard_normal(c), 0.1 * r.standard_normal(c))
+    ln_c = (1 + 0.1 * r.standard_normal(c), 0.1 * r.standard_normal(c))
+    ws = [r.standard_normal((c, c)) / 2 for _ in range(6)]
+    bs = [r.standard_normal(c) / 2 for _ in range(6)]
+    line = lambda kind, i: (z[i], mask[i]) if kind == "row" else (z[:, i], mask[:, i])  # noqa
+    pos = [(i, j) for i in range(n) for j in range(n)]
+    for outgoing in (True, False):
+        full = TM.triangle_multiply(z, mask, ln_in, ws, bs, ln_c, outgoing)
+        at = TM.triangle_multiply_at(line, ln_in, ws, bs, ln_c, pos, outgoing)
+        np.testing.assert_allclose(at, full.reshape(n * n, c), rtol=1e-12, atol=1e-13)
+
+
 def test_ln_pair_bias_matches_torch_and_pair_block():
     """LN(z).w with the head axis first: an independent torch float64 einsum, and the bias that
     the pair micro-block composes (evoformer.pair_block_fwd)."""
