@@ -22,6 +22,8 @@
 // P is recomputed in 2 and 3 from the saved lse; it is never stored.
 #include "attention_common.hpp"
 
+#include <type_traits>
+
 namespace clk {
 namespace {
 
@@ -552,6 +554,16 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
             for (int j = 0; j < 8; ++j) bacc[i][qt][j >> 2][j & 3] = lf.bias_units(b[j]);
         }
 
+    // Keys absent from every row of the block, or past Sk: bit 8i + j of the lane's keys
+    // kbeg + 32(i*KQ + kq) + 8g + j (the rows' presence is ORed in below). Their resident bias
+    // becomes -inf, so S^T is -inf there and P is 0 without any per-score instruction.
+    unsigned cabs = 0;
+#pragma unroll
+    for (int i = 0; i < KCW; ++i) {
+        const int lim = Sk - (kbeg + 32 * (i * KQ + kq) + 8 * g);
+        cabs |= (lim >= 8 ? 0u : lim <= 0 ? 0xffu : (0xffu << lim) & 0xffu) << (8 * i);
+    }
+
     f32x4 dbias[KCW][2][2];
 #pragma unroll
     for (int i = 0; i < KCW; ++i)
@@ -618,7 +630,15 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
         pend_n = -1;
     };
 
-    auto step = [&](int n, const char* kvc, const char* qdc, char* kvn, char* qdn) {
+    // One row step. MASKED (the block has a row with no present key, or a key present in some
+    // of its rows and absent in others): absent keys take the row's masked logit by per-score
+    // selects. Otherwise every row's absent keys are the block's common ones, whose resident
+    // bias is -inf, and the chunks need no select. Either way the chunks are straight-line code:
+    // a branch between the MFMAs and the exponentials of a chunk, or between chunks, keeps the
+    // scheduler from overlapping them.
+    auto step = [&](int n, const char* kvc, const char* qdc, char* kvn, char* qdn,
+                    auto masked_tag) __attribute__((always_inline)) {
+        constexpr bool MASKED = decltype(masked_tag)::value;
         const size_t nh = (size_t)n * H + h;
         async_wait();
         __syncthreads();  // row n in (kvc, qdc); every wave is done with row n-1
@@ -695,10 +715,16 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) dqa[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+        // An absent key's log2(P) (MASKED): its row's masked logit, in the same units.
+        float mx[2];
+#pragma unroll
+        for (int qt = 0; qt < 2; ++qt) mx[qt] = fmaf(mlc, kLog2e, -lse2c[qt]);
+        // The wave's 32-key chunks: S^T and dP^T - D by MFMA, P, dS, the dBias sums, and
+        // dQ^T += K^T.dS^T.
 #pragma unroll
         for (int i = 0; i < KCW; ++i) {
             const int c0 = 32 * (i * KQ + kq);  // chunk's first key, relative to kbeg
-            if (kbeg + c0 >= kend) continue;   // wave-uniform
+            if (kbeg + c0 >= kend) continue;   // block-uniform, the same for every row
             V8 kf[2], vf[2];
 #pragma unroll
             for (int t = 0; t < 2; ++t) {
@@ -714,37 +740,23 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
                     s[qt][t] = TR::mfma(kf[t], qf[qt], bacc[i][qt][t]);
                     dp[qt][t] = TR::mfma(vf[t], dof[qt], f32x4{-di[qt], -di[qt], -di[qt], -di[qt]});
                 }
-            const unsigned valid = (vbits >> (8 * i)) & 0xffu;
-            const bool nm = kbeg + c0 + 32 > Sk || __any(valid != 0xffu);
             // x = log2(P) = logit * log2(e) - lse * log2(e), one FMA per score.
             float x[2][8];
 #pragma unroll
             for (int qt = 0; qt < 2; ++qt)
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    x[qt][j] = fmaf(s[qt][j >> 2][j & 3], lf.cexp, -lse2c[qt]);
-            if (nm) {
-                // One block for the chunk, opaque to speculation: nothing of it is hoisted into
-                // (or merged across sub-tiles onto) the unmasked path.
-                asm volatile("");
-                // An absent key's log2(P): its row's masked logit, in the same units.
-                float mx[2];
-#pragma unroll
-                for (int qt = 0; qt < 2; ++qt) mx[qt] = fmaf(mlc, kLog2e, -lse2c[qt]);
-                if (kbeg + c0 + 32 > Sk) {  // wave-uniform: the chunk runs past the last key
-                    int lim = Sk - (kbeg + c0 + 8 * g);  // keys j >= lim are past Sk
-                    // Opaque, so the eight compares are not hoisted out of the row loop (their
-                    // lane masks would take 48 scalar registers over the chunks and spill).
-                    asm volatile("" : "+v"(lim));
-#pragma unroll
-                    for (int qt = 0; qt < 2; ++qt)
-#pragma unroll
-                        for (int j = 0; j < 8; ++j)
-                            x[qt][j] = j >= lim ? -INFINITY
-                                                : (((valid >> j) & 1u) ? x[qt][j] : mx[qt]);
-                } else {
-                    // Bit j of `valid` spread over a word (0 or ~0) selects x or the absent
-                    // key's value bitwise.
+                for (int j = 0; j < 8; ++j) x[qt][j] = fmaf(s[qt][j >> 2][j & 3], lf.cexp, -lse2c[qt]);
+            if constexpr (MASKED) {
+                // The selects, for a chunk with a key absent in this row but present in another
+                // row of the block, or in a row with no present key (wave-uniform). Bit j of
+                // `valid` spread over a word (0 or ~0) selects x or mx bitwise. Keys past Sk have
+                // no valid bit: in a row with a present key their P is 0; in a row without one,
+                // P = exp2(-lse2) as for the absent keys in range, which is harmless: their K
+                // rows are staged as zeros and their dBias is never stored.
+                const unsigned valid = (vbits >> (8 * i)) & 0xffu;
+                if (mlc == 0.f || __any((valid | ((cabs >> (8 * i)) & 0xffu)) != 0xffu)) {
+                    // Opaque to speculation: nothing of it is hoisted onto the unmasked path.
+                    asm volatile("");
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
                         const int sel = __builtin_amdgcn_sbfe((int)valid, j, 1);
@@ -788,6 +800,9 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
         }
     };
 
+    // Whether the rows need per-score selects (set below when a mask is given).
+    bool block_masked = false;
+
     // Work of the column-owner pass that would otherwise take a kernel of its own: the
     // transposed bias (one 64 x 64 tile per block, through the dQ exchange buffer, which is
     // idle until the first row ends) and the logit of the absent keys of this block's rows
@@ -803,8 +818,11 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
         }
         if (kmask) {
             // Also each row's presence bits, 64 keys per word (bit j of word i: key 64i + j is
-            // present), read by the row steps in place of the mask bytes (VEC).
+            // present), read by the row steps in place of the mask bytes (VEC); and, lane w
+            // holding word kbeg/64 + w of the key range, their OR and AND over this wave's rows.
             const int words = (Sk + 63) >> 6;
+            unsigned long long seen = 0ull, always = ~0ull;
+            bool empty_row = false;
             for (int nr = n0 + wave; nr < n1; nr += 8) {
                 const uint8_t* m = kmask + (size_t)nr * Sk;
                 bool any = false;
@@ -814,25 +832,94 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
                         const unsigned long long b = __ballot(kk < Sk && m[kk] != 0);
                         any |= b != 0ull;
                         if (lane == 0) mbits[(size_t)nr * words + i] = b;
+                        if (lane == i - (kbeg >> 6)) {
+                            seen |= b;
+                            always &= b;
+                        }
                     }
                 } else {
                     for (int i = lane; i < Sk; i += 64) any |= m[i] != 0;
                     any = __any(any);
                 }
+                empty_row |= !any;
                 if (lane == 0) row_logit[nr] = any ? kMaskedLogit : 0.f;
             }
-            __syncthreads();  // this block's prefetches read them
+            if constexpr (VEC) {
+                // The eight waves' words combined through the second Q/dO/O buffer (idle until
+                // the first row step stages row n0 + 1): the keys present in no row of the block
+                // (their bias becomes -inf), and whether every key of the range is present in
+                // all rows or in none and every row has a present key (then no row needs
+                // per-score selects).
+                constexpr int NWD = RK / 64;
+                unsigned long long* orw = reinterpret_cast<unsigned long long*>(qd1);
+                unsigned long long* andw = orw + 8 * NWD;
+                int* emptyw = reinterpret_cast<int*>(andw + 8 * NWD);
+                static_assert(sizeof(qd1) >= 16 * NWD * 8 + 8 * 4, "presence words fit");
+                if (lane < NWD) {
+                    orw[wave * NWD + lane] = seen;
+                    andw[wave * NWD + lane] = always;
+                }
+                if (lane == 0) emptyw[wave] = empty_row ? 1 : 0;
+                __syncthreads();
+#pragma unroll
+                for (int i = 0; i < KCW; ++i) {
+                    const int rel = 32 * (i * KQ + kq);
+                    unsigned long long w = 0ull;
+#pragma unroll
+                    for (int ww = 0; ww < 8; ++ww) w |= orw[ww * NWD + (rel >> 6)];
+                    const unsigned bits = (unsigned)(w >> ((rel & 32) + 8 * g)) & 0xffu;
+                    cabs |= (~bits & 0xffu) << (8 * i);
+                }
+                bool mixed = false;
+                if (lane < NWD) {
+                    unsigned long long o = 0ull, a = ~0ull;
+#pragma unroll
+                    for (int ww = 0; ww < 8; ++ww) {
+                        o |= orw[ww * NWD + lane];
+                        a &= andw[ww * NWD + lane];
+                    }
+                    const int lim = kend - (kbeg + 64 * lane);  // keys of the word in range
+                    const unsigned long long inr = lim >= 64 ? ~0ull : lim <= 0 ? 0ull
+                                                                      : (1ull << lim) - 1ull;
+                    mixed = ((o ^ a) & inr) != 0ull;
+                }
+                bool empty = false;
+#pragma unroll
+                for (int ww = 0; ww < 8; ++ww) empty |= emptyw[ww] != 0;
+                block_masked = empty || __any(mixed);
+            } else {
+                block_masked = true;
+            }
+            __syncthreads();  // this block's prefetches read them; the combined words are read
         }
     }
+#pragma unroll
+    for (int i = 0; i < KCW; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int sel = __builtin_amdgcn_sbfe((int)cabs, 8 * i + j, 1);
+#pragma unroll
+            for (int qt = 0; qt < 2; ++qt) {
+                const float b = bacc[i][qt][j >> 2][j & 3];
+                bacc[i][qt][j >> 2][j & 3] =
+                    __int_as_float((~sel & __float_as_int(b)) | (sel & __float_as_int(-INFINITY)));
+            }
+        }
 
     if (n0 < n1) {
         stage(n0, kv0, qd0);
         prefetch(n0);
     }
-    for (int n = n0; n < n1; n += 2) {
-        step(n, kv0, qd0, kv1, qd1);
-        if (n + 1 < n1) step(n + 1, kv1, qd1, kv0, qd0);
-    }
+    auto rows = [&](auto masked_tag) __attribute__((always_inline)) {
+        for (int n = n0; n < n1; n += 2) {
+            step(n, kv0, qd0, kv1, qd1, masked_tag);
+            if (n + 1 < n1) step(n + 1, kv1, qd1, kv0, qd0, masked_tag);
+        }
+    };
+    if (block_masked)
+        rows(std::true_type{});
+    else
+        rows(std::false_type{});
     flush_dq();
 
 #pragma unroll
@@ -895,11 +982,13 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkv2(
     const int k0 = (item % kblocks) * KB, h = (item / kblocks) % H, n = item / (kblocks * H);
     const size_t nh = (size_t)n * H + h;
     const int kw0 = k0 + wave * KW;
-    const bool active = kw0 < Sk;
 
+    // In a row with a present key an absent key's P is 0, so its dK and dV are 0: its lane (one
+    // key per lane column of every product) computes without selects and stores zeros. Only a
+    // row without any present key needs the masked logit in place of the logit.
     const float ml = kmask ? row_logit[n] : kMaskedLogit;
     V8 kf[KSUB], vf[KSUB];
-    bool present[KSUB], clean[KSUB];
+    bool present[KSUB], clean[KSUB], none_present = true;
     float absent_logit[KSUB];
 #pragma unroll
     for (int s = 0; s < KSUB; ++s) {
@@ -914,8 +1003,12 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkv2(
         vf[s] = bits_as<V8>(rv);
         present[s] = kin && (kmask == nullptr || kmask[(size_t)n * Sk + key] != 0);
         absent_logit[s] = kin ? ml : -INFINITY;
-        clean[s] = __all(present[s]);  // wave-uniform: no absent key in the sub-tile
+        // Wave-uniform: no key of the sub-tile needs a select.
+        clean[s] = ml != 0.f || __all(present[s]);
+        none_present = none_present && !__any(present[s]);
     }
+    // Wave-uniform: every key of the wave is past Sk, or absent in a row with a present key.
+    const bool active = kw0 < Sk && !(ml != 0.f && none_present);
 
     f32x4 dka[KSUB][DT], dva[KSUB][DT];
 #pragma unroll
@@ -1031,12 +1124,14 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkv2(
     for (int s = 0; s < KSUB; ++s) {
         const int key = kw0 + 16 * s + r16;
         if (key >= Sk) continue;
+        const bool zero = !present[s] && ml != 0.f;
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
             const int d = 16 * dt + 4 * g;
             if (d < D) {
-                store4<TR>(dk + (nh * Sk + key) * D + d, dka[s][dt] * scale);
-                store4<TR>(dv + (nh * Sk + key) * D + d, dva[s][dt]);
+                const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                store4<TR>(dk + (nh * Sk + key) * D + d, zero ? z : dka[s][dt] * scale);
+                store4<TR>(dv + (nh * Sk + key) * D + d, zero ? z : dva[s][dt]);
             }
         }
     }

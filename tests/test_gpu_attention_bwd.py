@@ -79,6 +79,41 @@ def test_attention_bwd_bias_past_float16_range(cuda, shape):
     assert_close("dBias", dbias, rb, tol)
 
 
+# (N, H, Sq, Sk, D): key counts that fill whole 32-key chunks and ones that end inside a chunk,
+# Sk % 8 == 0 (presence words) and not (mask bytes), one and two key ranges.
+MIXED_MASK_SHAPES = [(24, 2, 70, 200, 32), (20, 2, 64, 77, 32), (12, 2, 40, 456, 16),
+                     (16, 1, 64, 384, 32)]
+
+
+@pytest.mark.parametrize("shape", MIXED_MASK_SHAPES, ids=lambda c: "x".join(map(str, c)))
+def test_attention_bwd_mixed_masks(cuda, shape):
+    """Keys absent in every row (a padding tail: their bias is replaced by -inf inside the
+    kernel), keys absent in some rows only (random holes: per-score selects), rows with no
+    present key, and rows with everything present, all in the blocks of one call."""
+    n, h, sq, sk, d = shape
+    inp = attention_inputs(n, h, sq, sk, d, torch.bfloat16, seed=sk + n)
+    g = torch.Generator().manual_seed(sk * 7 + n)
+    km = (torch.rand((n, sk), generator=g) > 0.15).to(torch.uint8)
+    tail = sk - sk // 6
+    km[:, tail:] = 0
+    km[n // 3] = 0
+    km[n // 2, :tail] = 1
+    km[n - 1, :tail] = 1
+    km[n - 1, tail + 1] = 1  # one row reaches into the tail
+    inp["kmask"] = km
+    _, _, _, (dq, dk, dv, dbias) = _run(inp, cuda)
+    rq, rk, rv, rb = _oracle(inp)
+    tol = TOL["bf16"]["grad"]
+    assert_close("dQ", dq, rq, tol)
+    assert_close("dK", dk, rk, tol)
+    assert_close("dV", dv, rv, tol)
+    assert_close("dBias", dbias, rb, tol)
+    absent = (km == 0).nonzero().tolist()
+    present_rows = (km != 0).any(dim=1)
+    zero_dk = [(i, k) for i, k in absent if present_rows[i]]
+    assert all(torch.count_nonzero(dk[i, :, k]).item() == 0 for i, k in zero_dk[:50])
+
+
 def test_attention_bwd_deterministic(cuda):
     inp = attention_inputs(6, 4, 200, 200, 32, torch.bfloat16, seed=21, masked_tail=0.1,
                            masked_rows=1)
