@@ -27,11 +27,14 @@
 // all-masked row it is therefore ln(Sk), relative to the masked logit.
 #include "attention_common.hpp"
 
+#include <type_traits>
+
 namespace clk {
 namespace {
 
 constexpr float kRescaleSlack = 8.f;  // log2 of the largest P before the running max moves
 constexpr int kGateChannels = 128;    // gate channels (wg rows) per K/V buffer in the epilogue
+constexpr int kPresWords = 256;       // most key tiles of the bias-patching forward (LDS words)
 
 // Per-tile "some key absent or past Sk" flags of one mask row, as bits of a 64-bit word (tiles of
 // 64 keys; tiles past the 64th always take the checked path), worked out by each wave on its
@@ -156,6 +159,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
     using V8 = typename TR::vec8;
     using G = AttnGeom<D>;
     using T = SwzTile<D>;
+    // PATCH (bfloat16 with the bias tile in LDS): a key tile with an absent key (or keys past
+    // Sk) has its bias changed in LDS before use -- -1e9, the masked logit, for an absent key
+    // (P = 0 after the exponential once the row's max comes from a present key), 0 for every key
+    // in range in a row without any present key (whose Q^T is zero, so every logit is that
+    // row's masked logit 0) -- and the scores need no per-key select, so the tile's MFMAs and
+    // exponentials stay one straight-line block. (-1e9 is beyond float16's range: float16
+    // keeps the selects. A larger magnitude would not do: the exponent's FMA against the
+    // running max leaves a rounding residue of about 2^-24 of the logit, which must stay far
+    // below float32's exponent range.)
+    constexpr bool PATCH = VEC && std::is_same<TR, BF16>::value;
     using PF = TilePrefetch<TR, QT, VEC, BM>;
     constexpr int BQ = 4 * 16 * QT;
     constexpr int BK = G::BK;
@@ -206,6 +219,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
             }
         }
     };
+    // PATCH: this wave's mask bytes of its first two key tiles (t = wave, wave + 4; lane l:
+    // key 64t + l), loaded before anything else so that the presence words below wait for them
+    // alone.
+    uint32_t mb[2] = {0u, 0u};
+    if constexpr (PATCH) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int kk = (wave + 4 * i) * BK + lane;
+            if (kk < Sk) mb[i] = mp ? mp[kk] : 1u;
+        }
+    }
     if (ntiles > 0) stage(0, kv0);
 
     // B operand Q^T: lane (query r16, group g) holds head dims 32*ks + 8*g + 0..7.
@@ -228,8 +252,73 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
     for (int qt = 0; qt < QT; ++qt) brow[qt] = bp + (size_t)min(qbase + qt * 16 + r16, Sq - 1) * Sk;
     PF ca, cb;
     if (ntiles > 0) ca.load(brow, mp, 0, g, Sk);
-    // The mask row's tile flags, with the Q and first-tile loads already in flight.
-    const RowFlags rf = row_flags<VEC>(mp, Sk);
+    // The mask row's tile flags, with the Q and first-tile loads already in flight (PATCH
+    // reads the same facts from the presence words instead).
+    const RowFlags rf = PATCH ? RowFlags{0ull, kMaskedLogit} : row_flags<VEC>(mp, Sk);
+    // PATCH: the row's presence bits, one 64-bit word per key tile (bit j: key 64t + j is
+    // present and below Sk; the launch keeps ntiles <= kPresWords), and per wave whether its
+    // tiles hold a present key.
+    __shared__ unsigned long long pres[PATCH ? kPresWords : 1];
+    __shared__ int wave_any[PATCH ? 4 : 1];
+    if constexpr (PATCH) {
+        bool any = false;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int t = wave + 4 * i;
+            if (t < ntiles) {
+                const unsigned long long b = __ballot(mb[i] != 0u);
+                any |= b != 0ull;
+                if (lane == 0) pres[t] = b;
+            }
+        }
+        for (int t = wave + 8; t < ntiles; t += 4) {
+            const int kk = t * BK + lane;
+            const unsigned long long b = __ballot(kk < Sk && (mp == nullptr || mp[kk] != 0));
+            any |= b != 0ull;
+            if (lane == 0) pres[t] = b;
+        }
+        if (lane == 0) wave_any[wave] = any ? 1 : 0;
+    }
+    // PATCH: a row without any present key: every logit is its masked logit 0, so Q^T = 0 and
+    // the changed bias tiles hold 0 in range.
+    bool row_empty = false;
+    if constexpr (PATCH) {
+        __syncthreads();  // the presence words and flags are visible
+        row_empty = mp && (wave_any[0] | wave_any[1] | wave_any[2] | wave_any[3]) == 0;
+        if (row_empty) {
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt)
+#pragma unroll
+                for (int ks = 0; ks < G::KS; ++ks) qf[qt][ks] = V8{};
+        }
+    }
+    // PATCH: lane (row r16 of each sub-tile, group g) changes 16-byte pieces 4c + g (keys
+    // k0 + 32c + 8g + 0..7) of its rows of tile kt's bias, one dword (two keys) at a time:
+    // few registers are free here.
+    auto patch = [&](const char* kvc, int kt) {
+        char* const bt = const_cast<char*>(kvc) + 2 * TILE;
+        const uint32_t neg = (uint32_t)__builtin_bit_cast(uint16_t, TR::from_f(kMaskedLogit)) * 0x10001u;
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int kk = kt * BK + 32 * c + 8 * g;
+            // A key past Sk gets the masked logit in every row.
+            const uint32_t fill = kk < Sk && row_empty ? 0u : neg;
+            const uint32_t bits = reinterpret_cast<const uint32_t*>(pres)[2 * kt + c] >> (8 * g);
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+                const int row = wave * 16 * QT + 16 * qt + r16;
+                uint32_t* const at = reinterpret_cast<uint32_t*>(
+                    bt + row * 128 + 16 * ((4 * c + g) ^ (row & 7)));
+                // Dword i holds keys 2i, 2i+1 (low, high half): keep the bias of present keys.
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const uint32_t keep = ((bits >> (2 * i)) & 1u ? 0xffffu : 0u) |
+                                          ((bits >> (2 * i + 1)) & 1u ? 0xffff0000u : 0u);
+                    at[i] = (at[i] & keep) | (fill & ~keep);
+                }
+            }
+        }
+    };
     // In the bias-MFMA form every score is in units of 1/scale of the logit (xs = scale*log2e
     // per unit); otherwise in logit units (xs = log2e).
     const float masked_logit = BM ? rf.masked_logit * bm.bscale : rf.masked_logit;
@@ -249,11 +338,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
     V8 ones;
 #pragma unroll
     for (int j = 0; j < 8; ++j) ones[j] = TR::from_f(1.f);
+    // The running max starts at half the masked logit: a tile whose keys are all absent (its
+    // max the masked logit) then adds P = 0 exactly. Starting lower, the first such tile would
+    // set the max, and P = exp2(x*xs - m*xs) of its keys would be the exponential of the FMA's
+    // rounding residue (up to 2^6 at a logit of 1e9), which float16 cannot hold. In a row with
+    // no present key every logit is the masked logit 0, the start.
     float m_run[QT];
     f32x4 acc[QT][G::DT], lsum[QT];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-        m_run[qt] = -INFINITY;
+        m_run[qt] = 0.5f * masked_logit;
         lsum[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int dt = 0; dt < G::DT; ++dt) acc[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -263,7 +357,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
         const int k0 = kt * BK;
         async_wait();
         __syncthreads();  // tile kt visible; every wave is done with the other buffer
-        const bool need_mask = kt >= 64 || ((rf.bits >> kt) & 1ull) != 0ull;
+        bool need_mask;
+        if constexpr (PATCH) {
+            const int rem = Sk - k0;  // keys of the tile below Sk
+            const unsigned long long full = rem >= 64 ? ~0ull : (1ull << rem) - 1ull;
+            need_mask = (rem < 64) || pres[kt] != full;
+        } else {
+            need_mask = kt >= 64 || ((rf.bits >> kt) & 1ull) != 0ull;
+        }
         if (kt + 1 < ntiles) {
             stage(k0 + BK, kvn);
             nxt.load(brow, mp, k0 + BK, g, Sk);
@@ -273,6 +374,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
             int t = threadIdx.x;
             asm volatile("" : "+v"(t));
             stage_rows_ld<D, kGateChannels, 256>(rw, 0, ga.HD, kvn, t);
+        }
+        // Each wave reads only its own rows of the bias tile: no barrier after the change.
+        if (PATCH && need_mask) {
+            patch(kvc, kt);
+            // Nothing of the tile's work is interleaved with the change (registers).
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
         }
         V8 kf[4][G::KS];
 #pragma unroll
@@ -344,7 +451,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
                     x[qt][c][4 + j] = fmaf(s[qt][2 * c + 1][j], scale, bv[4 + j]);
                 }
             }
-        if (need_mask) {
+        if (!PATCH && need_mask) {
             // One block for the whole tile, opaque to speculation: nothing of it is hoisted
             // into (or merged across sub-tiles onto) the unmasked path.
             asm volatile("");
@@ -509,7 +616,10 @@ void launch_fwd_qt(hipStream_t st, const void* q, const void* k, const void* v, 
                    float scale, GateArgs<typename TR::elem> ga) {
     using E = typename TR::elem;
     const dim3 grid(ceil_div(Sq, 64 * QT) * H * N);
-    const bool vec = Sk % 8 == 0 && (reinterpret_cast<uintptr_t>(kmask) & 7u) == 0;
+    // The bias tile through LDS: whole 8-key pieces and 8-byte aligned mask rows; for bfloat16
+    // (which patches masked bias tiles in LDS) at most kPresWords key tiles.
+    const bool vec = Sk % 8 == 0 && (reinterpret_cast<uintptr_t>(kmask) & 7u) == 0 &&
+                     (!std::is_same<TR, BF16>::value || Sk <= kPresWords * 64);
     BiasMfma bm{};
     if (vec && bias_mfma_for<TR>(scale, &bm))
         attn_fwd_kernel<TR, D, QT, true, GATE, true><<<grid, 256, 0, st>>>(

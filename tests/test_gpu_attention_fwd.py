@@ -21,6 +21,7 @@ CASES = [
     (2, 3, 257, 129, 32, 0.05, 1),
     (2, 2, 33, 300, 64, 0.0, 0),
     (1, 1, 16, 4100, 32, 0.1, 0),  # more than 64 key tiles, ragged last tile
+    (1, 1, 16, 16400, 32, 0.1, 0),  # more key tiles than bfloat16's masked-bias patching covers
 ]
 
 
@@ -50,6 +51,38 @@ def test_attention_fwd_parity(cuda, case, dtype):
     # The inference entry (VoltaMma contract) gives the same bits as the training entry.
     out2 = ops.attention(g["q"], g["k"], g["v"], g["bias"], g["kmask"], g["scale"], 64, 64)
     assert torch.equal(out, out2)
+
+
+# (N, H, Sq, Sk, D): whole and ragged key tiles, the element-wise mask path (Sk % 8 != 0).
+MIXED_MASK_SHAPES = [(8, 2, 70, 200, 32), (6, 2, 64, 77, 32), (6, 2, 40, 456, 16),
+                     (4, 1, 130, 384, 64), (5, 2, 64, 136, 8)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=dname)
+@pytest.mark.parametrize("shape", MIXED_MASK_SHAPES, ids=lambda c: "x".join(map(str, c)))
+def test_attention_fwd_mixed_masks(cuda, shape, dtype):
+    """Per-row masks of every kind in one call: random holes with a padding tail, a row with no
+    present key, a row whose first 64-key tile is entirely absent (its running max starts on
+    absent keys), a row with everything present, and one whose only present key is the last."""
+    n, h, sq, sk, d = shape
+    inp = attention_inputs(n, h, sq, sk, d, dtype, seed=sk + 3 * n, with_dout=False)
+    gen = torch.Generator().manual_seed(sk * 5 + n)
+    km = (torch.rand((n, sk), generator=gen) > 0.2).to(torch.uint8)
+    km[:, sk - sk // 5:] = 0
+    km[1] = 0
+    km[2, :min(64, sk - 1)] = 0
+    km[2, sk - 1] = 1
+    km[3] = 1
+    km[n - 1] = 0
+    km[n - 1, sk - 1] = 1
+    inp["kmask"] = km
+    g = {k: (v.to(cuda) if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    out, lse = ops.attention_fwd(g["q"], g["k"], g["v"], g["bias"], g["kmask"], g["scale"])
+    o_ref, lse_ref = _oracle(inp)
+    assert_close("O", out, o_ref, TOL[dname(dtype)]["o"])
+    empty = (km.numpy() == 0).all(axis=1)[:, None, None]
+    lse_ref = np.where(empty, np.log(sk), lse_ref)
+    assert np.abs(np64(lse) - lse_ref).max() < 5e-2
 
 
 def test_attention_fwd_no_mask_is_all_present(cuda):
