@@ -293,31 +293,41 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
         }
     }
     // PATCH: lane (row r16 of each sub-tile, group g) changes 16-byte pieces 4c + g (keys
-    // k0 + 32c + 8g + 0..7) of its rows of tile kt's bias, one dword (two keys) at a time:
-    // few registers are free here.
+    // k0 + 32c + 8g + 0..7) of its rows of tile kt's bias: all its pieces are read, changed and
+    // written back in one round.
     auto patch = [&](const char* kvc, int kt) {
         char* const bt = const_cast<char*>(kvc) + 2 * TILE;
         const uint32_t neg = (uint32_t)__builtin_bit_cast(uint16_t, TR::from_f(kMaskedLogit)) * 0x10001u;
+        u32x4* at[2][QT];
+        u32x4 v[2][QT];
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) {
+                const int row = wave * 16 * QT + 16 * qt + r16;
+                at[c][qt] = reinterpret_cast<u32x4*>(bt + row * 128 + 16 * ((4 * c + g) ^ (row & 7)));
+                v[c][qt] = *at[c][qt];
+            }
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             const int kk = kt * BK + 32 * c + 8 * g;
             // A key past Sk gets the masked logit in every row.
             const uint32_t fill = kk < Sk && row_empty ? 0u : neg;
             const uint32_t bits = reinterpret_cast<const uint32_t*>(pres)[2 * kt + c] >> (8 * g);
+            // Dword i holds keys 2i, 2i+1 (low, high half): keep the bias of present keys.
 #pragma unroll
-            for (int qt = 0; qt < QT; ++qt) {
-                const int row = wave * 16 * QT + 16 * qt + r16;
-                uint32_t* const at = reinterpret_cast<uint32_t*>(
-                    bt + row * 128 + 16 * ((4 * c + g) ^ (row & 7)));
-                // Dword i holds keys 2i, 2i+1 (low, high half): keep the bias of present keys.
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t keep = ((bits >> (2 * i)) & 1u ? 0xffffu : 0u) |
+                                      ((bits >> (2 * i + 1)) & 1u ? 0xffff0000u : 0u);
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const uint32_t keep = ((bits >> (2 * i)) & 1u ? 0xffffu : 0u) |
-                                          ((bits >> (2 * i + 1)) & 1u ? 0xffff0000u : 0u);
-                    at[i] = (at[i] & keep) | (fill & ~keep);
-                }
+                for (int qt = 0; qt < QT; ++qt)
+                    v[c][qt][i] = (v[c][qt][i] & keep) | (fill & ~keep);
             }
         }
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) *at[c][qt] = v[c][qt];
     };
     // In the bias-MFMA form every score is in units of 1/scale of the logit (xs = scale*log2e
     // per unit); otherwise in logit units (xs = log2e).
