@@ -740,6 +740,10 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
                     s[qt][t] = TR::mfma(kf[t], qf[qt], bacc[i][qt][t]);
                     dp[qt][t] = TR::mfma(vf[t], dof[qt], f32x4{-di[qt], -di[qt], -di[qt], -di[qt]});
                 }
+            // The chunk's VALU work (exponentials, dS, the dBias sums) runs at a raised wave
+            // priority until its dQ MFMAs are issued: the other wave on the SIMD then gets the
+            // issue slots while this one waits on its S and dP MFMAs (2-3 us at N_res = 384).
+            __builtin_amdgcn_s_setprio(1);
             // x = log2(P) = logit * log2(e) - lse * log2(e), one FMA per score.
             float x[2][8];
 #pragma unroll
@@ -783,6 +787,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
 #pragma unroll
                 for (int qt = 0; qt < 2; ++qt) dqa[qt][dt] = TR::mfma(kt, dsf[qt], dqa[qt][dt]);
             }
+            __builtin_amdgcn_s_setprio(0);
         }
 
 #pragma unroll
