@@ -483,8 +483,8 @@ __device__ void transpose_bias_tile(const typename TR::elem* __restrict__ bias,
 // accumulator input), dS, and dQ^T += K^T.dS^T. The four key-quarter waves of a query group
 // then add their dQ partials through LDS in a fixed order. Also writes lse*log2(e) and -D_i
 // per query for the column-owner pass.
-template <typename TR, int D, int KCW, bool VEC>
-__global__ __launch_bounds__(512) void attn_bwd_dq2(
+template <typename TR, int D, int KCW, bool VEC, int QG, int QTW>
+__global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
     const typename TR::elem* __restrict__ q, const typename TR::elem* __restrict__ k,
     const typename TR::elem* __restrict__ v, const typename TR::elem* __restrict__ bias,
     const uint8_t* __restrict__ kmask, const typename TR::elem* __restrict__ out,
@@ -499,7 +499,8 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
     using V8 = typename TR::vec8;
     using T = SwzTile<D>;
     static_assert(D <= 32, "row-owner kernel holds one 32-dim k-slot group");
-    constexpr int KQ = 4, BQ = 64, DT = AttnGeom<D>::DT;
+    constexpr int KQ = 4, BQ = 16 * QTW * QG, DT = AttnGeom<D>::DT;
+    constexpr int NWV = KQ * QG, NT = 64 * NWV;  // waves, threads
     constexpr int RK = KQ * KCW * 32;
     constexpr int KVB = RK * T::ROWB;
     constexpr int QB = BQ * T::ROWB;
@@ -513,7 +514,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
     constexpr int XB = VEC ? 512 : 0;
     __shared__ __attribute__((aligned(16))) char qd0[3 * QB + XB];
     __shared__ __attribute__((aligned(16))) char qd1[3 * QB + XB];
-    __shared__ __attribute__((aligned(16))) char xch_raw[8 * 2 * DT * 64 * 16];
+    __shared__ __attribute__((aligned(16))) char xch_raw[NWV * QTW * DT * 64 * 16];
     f32x4* const xch = reinterpret_cast<f32x4*>(xch_raw);
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -528,19 +529,19 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
     const int range = zr % nranges, chunk = zr / nranges;
     const int kbeg = range * RK, kend = min(Sk, kbeg + RK);
     const int n0 = chunk * NB, n1 = min(N, n0 + NB);
-    int qrow[2];
+    int qrow[QTW];
 #pragma unroll
-    for (int qt = 0; qt < 2; ++qt) qrow[qt] = q0 + 32 * qg + 16 * qt + r16;
+    for (int qt = 0; qt < QTW; ++qt) qrow[qt] = q0 + 16 * QTW * qg + 16 * qt + r16;
 
     // Resident bias in the logit form's units (bias * lf.bscale, float32), laid out as the
     // accumulator input of S^T: chunk i, sub-tile qt, half t -> keys kbeg + 32j + 8g + 4t + 0..3
     // of query qrow[qt] (j = i*KQ + kq). The S^T product then yields the logit up to the factor
     // lf.cexp, and no per-row instruction touches the bias.
-    f32x4 bacc[KCW][2][2];
+    f32x4 bacc[KCW][QTW][2];
 #pragma unroll
     for (int i = 0; i < KCW; ++i)
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
+        for (int qt = 0; qt < QTW; ++qt) {
             const int kk = kbeg + 32 * (i * KQ + kq) + 8 * g;
             const E* brow = bias + ((size_t)h * Sq + min(qrow[qt], Sq - 1)) * Sk;
             float b[8];
@@ -564,22 +565,22 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
         cabs |= (lim >= 8 ? 0u : lim <= 0 ? 0xffu : (0xffu << lim) & 0xffu) << (8 * i);
     }
 
-    f32x4 dbias[KCW][2][2];
+    f32x4 dbias[KCW][QTW][2];
 #pragma unroll
     for (int i = 0; i < KCW; ++i)
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt)
+        for (int qt = 0; qt < QTW; ++qt)
 #pragma unroll
             for (int t = 0; t < 2; ++t) dbias[i][qt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     auto stage = [&](int n, char* kv, char* qd) {
         const size_t nh = (size_t)n * H + h;
         const uint32_t kb = (uint32_t)Sk * D * 2, qb = (uint32_t)Sq * D * 2;
-        stage_rows<D, RK, 512>(buffer_rsrc(k + nh * Sk * D, kb), kbeg, kv);
-        stage_rows<D, RK, 512>(buffer_rsrc(v + nh * Sk * D, kb), kbeg, kv + KVB);
-        stage_rows<D, BQ, 512>(buffer_rsrc(q + nh * Sq * D, qb), q0, qd);
-        stage_rows<D, BQ, 512>(buffer_rsrc(dout + nh * Sq * D, qb), q0, qd + QB);
-        stage_rows<D, BQ, 512>(buffer_rsrc(out + nh * Sq * D, qb), q0, qd + 2 * QB);
+        stage_rows<D, RK, NT>(buffer_rsrc(k + nh * Sk * D, kb), kbeg, kv);
+        stage_rows<D, RK, NT>(buffer_rsrc(v + nh * Sk * D, kb), kbeg, kv + KVB);
+        stage_rows<D, BQ, NT>(buffer_rsrc(q + nh * Sq * D, qb), q0, qd);
+        stage_rows<D, BQ, NT>(buffer_rsrc(dout + nh * Sq * D, qb), q0, qd + QB);
+        stage_rows<D, BQ, NT>(buffer_rsrc(out + nh * Sq * D, qb), q0, qd + 2 * QB);
         if constexpr (VEC) {
             // Queries past Sq and keys past Sk read zeros. Mask rows are 8-byte aligned (VEC).
             char* ex = qd + 3 * QB;
@@ -595,13 +596,13 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
     // Per-row values kept in registers one row ahead when they are not staged (not VEC), raw:
     // anything computed from them right after the load would wait for the row's direct-to-LDS
     // loads too.
-    float lse_nx[VEC ? 1 : 2], ml_nx = kMaskedLogit;
+    float lse_nx[VEC ? 1 : QTW], ml_nx = kMaskedLogit;
     u32x2 mask_nx[VEC ? 1 : KCW];
     auto prefetch = [&](int n) {
         if constexpr (!VEC) {
             const size_t nh = (size_t)n * H + h;
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt) lse_nx[qt] = lse[nh * Sq + min(qrow[qt], Sq - 1)];
+            for (int qt = 0; qt < QTW; ++qt) lse_nx[qt] = lse[nh * Sq + min(qrow[qt], Sq - 1)];
             const uint8_t* mrow = kmask ? kmask + (size_t)n * Sk : nullptr;
 #pragma unroll
             for (int i = 0; i < KCW; ++i)
@@ -615,7 +616,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
     int pend_n = -1;
     auto flush_dq = [&]() {
         if (pend_n < 0) return;
-        const int qt = kq / DT, dt = kq % DT;
+        const int qt = min(kq / DT, QTW - 1), dt = kq % DT;  // pend_n >= 0: kq < QTW * DT
         const int d = 16 * dt + 4 * g;
         if (qrow[qt] < Sq && d < D) {
             const size_t pnh = (size_t)pend_n * H + h;
@@ -642,16 +643,16 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
         const size_t nh = (size_t)n * H + h;
         async_wait();
         __syncthreads();  // row n in (kvc, qdc); every wave is done with row n-1
-        float lse2c[2];
+        float lse2c[QTW];
         const float mlc = ml_nx;
         // Presence bits of this wave's keys: chunk i in bits 8i .. 8i+7 (one register).
         unsigned vbits = 0;
         if constexpr (VEC) {
             const char* ex = qdc + 3 * QB;
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt)
+            for (int qt = 0; qt < QTW; ++qt)
                 lse2c[qt] = qrow[qt] < Sq
-                                ? reinterpret_cast<const float*>(ex)[32 * qg + 16 * qt + r16] * kLog2e
+                                ? reinterpret_cast<const float*>(ex)[16 * QTW * qg + 16 * qt + r16] * kLog2e
                                 : INFINITY;
             if (kmask) {
                 // Chunk i's 32 keys start at bit rel % 64 of staged word rel / 64 (rel = key
@@ -669,17 +670,17 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
             }
         } else {
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt)
+            for (int qt = 0; qt < QTW; ++qt)
                 lse2c[qt] = qrow[qt] < Sq ? lse_nx[qt] * kLog2e : INFINITY;
 #pragma unroll
             for (int i = 0; i < KCW; ++i) vbits |= nonzero_bits8(mask_nx[i]) << (8 * i);
         }
 
-        V8 qf[2], dof[2];
-        float di[2];
+        V8 qf[QTW], dof[QTW];
+        float di[QTW];
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
-            const int row = 32 * qg + 16 * qt + r16;
+        for (int qt = 0; qt < QTW; ++qt) {
+            const int row = 16 * QTW * qg + 16 * qt + r16;
             qf[qt] = swz_row_operand<V8, D>(qdc, row, 0, g);
             if (lf.qzero) qf[qt] = V8{};
             dof[qt] = swz_row_operand<V8, D>(qdc + QB, row, 0, g);
@@ -695,7 +696,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
         }
         if (range == 0 && kq == 0 && g == 0) {
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt)
+            for (int qt = 0; qt < QTW; ++qt)
                 if (qrow[qt] < Sq) {
                     lse2_out[nh * Sq + qrow[qt]] = lse2c[qt];
                     ndi_out[nh * Sq + qrow[qt]] = -di[qt];
@@ -709,16 +710,16 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
             prefetch(n + 1);
         }
 
-        f32x4 dqa[2][DT];
+        f32x4 dqa[QTW][DT];
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt)
+        for (int qt = 0; qt < QTW; ++qt)
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) dqa[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
         // An absent key's log2(P) (MASKED): its row's masked logit, in the same units.
-        float mx[2];
+        float mx[QTW];
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) mx[qt] = fmaf(mlc, kLog2e, -lse2c[qt]);
+        for (int qt = 0; qt < QTW; ++qt) mx[qt] = fmaf(mlc, kLog2e, -lse2c[qt]);
         // The wave's 32-key chunks: S^T and dP^T - D by MFMA, P, dS, the dBias sums, and
         // dQ^T += K^T.dS^T.
 #pragma unroll
@@ -732,11 +733,11 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
                 kf[t] = swz_row_operand<V8, D>(kvc, row, 0, g);
                 vf[t] = swz_row_operand<V8, D>(kvc + KVB, row, 0, g);
             }
-            f32x4 s[2][2], dp[2][2];
+            f32x4 s[QTW][2], dp[QTW][2];
 #pragma unroll
             for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int qt = 0; qt < 2; ++qt) {
+                for (int qt = 0; qt < QTW; ++qt) {
                     s[qt][t] = TR::mfma(kf[t], qf[qt], bacc[i][qt][t]);
                     dp[qt][t] = TR::mfma(vf[t], dof[qt], f32x4{-di[qt], -di[qt], -di[qt], -di[qt]});
                 }
@@ -745,9 +746,9 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
             // issue slots while this one waits on its S and dP MFMAs (2-3 us at N_res = 384).
             __builtin_amdgcn_s_setprio(1);
             // x = log2(P) = logit * log2(e) - lse * log2(e), one FMA per score.
-            float x[2][8];
+            float x[QTW][8];
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt)
+            for (int qt = 0; qt < QTW; ++qt)
 #pragma unroll
                 for (int j = 0; j < 8; ++j) x[qt][j] = fmaf(s[qt][j >> 2][j & 3], lf.cexp, -lse2c[qt]);
             if constexpr (MASKED) {
@@ -765,15 +766,15 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
                     for (int j = 0; j < 8; ++j) {
                         const int sel = __builtin_amdgcn_sbfe((int)valid, j, 1);
 #pragma unroll
-                        for (int qt = 0; qt < 2; ++qt)
+                        for (int qt = 0; qt < QTW; ++qt)
                             x[qt][j] = __int_as_float((sel & __float_as_int(x[qt][j])) |
                                                       (~sel & __float_as_int(mx[qt])));
                     }
                 }
             }
-            V8 dsf[2];
+            V8 dsf[QTW];
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt)
+            for (int qt = 0; qt < QTW; ++qt)
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const float p = fast_exp2(x[qt][j]);
@@ -785,21 +786,22 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
             for (int dt = 0; dt < DT; ++dt) {
                 const V8 kt = swz_tr_operand<V8, D>(kvc, c0, dt, r16, g);
 #pragma unroll
-                for (int qt = 0; qt < 2; ++qt) dqa[qt][dt] = TR::mfma(kt, dsf[qt], dqa[qt][dt]);
+                for (int qt = 0; qt < QTW; ++qt) dqa[qt][dt] = TR::mfma(kt, dsf[qt], dqa[qt][dt]);
             }
             __builtin_amdgcn_s_setprio(0);
         }
 
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt)
+        for (int qt = 0; qt < QTW; ++qt)
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) xch[((wave * 2 + qt) * DT + dt) * 64 + lane] = dqa[qt][dt];
+            for (int dt = 0; dt < DT; ++dt) xch[((wave * QTW + qt) * DT + dt) * 64 + lane] = dqa[qt][dt];
         lds_barrier();  // the exchange is LDS only
-        if (kq < 2 * DT) {
+        if (kq < QTW * DT) {
             const int qt = kq / DT, dt = kq % DT;
-            f32x4 acc = xch[(((qg * 4) * 2 + qt) * DT + dt) * 64 + lane];
+            f32x4 acc = xch[(((qg * 4) * QTW + qt) * DT + dt) * 64 + lane];
 #pragma unroll
-            for (int w = 1; w < 4; ++w) acc += xch[(((qg * 4 + w) * 2 + qt) * DT + dt) * 64 + lane];
+            for (int w = 1; w < 4; ++w)
+                acc += xch[(((qg * 4 + w) * QTW + qt) * DT + dt) * 64 + lane];
             pend_dq = acc * scale;
             pend_n = n;
         }
@@ -818,7 +820,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
         for (int t = blockIdx.x; t < ttiles; t += gridDim.x) {
             static_assert(sizeof(xch_raw) >= 64 * 72 * sizeof(E), "transpose tile fits");
             transpose_bias_tile<TR>(bias, bias_t, reinterpret_cast<E(*)[72]>(xch_raw), t, Sq, Sk,
-                                    SqP, tiles_q, tiles_k, threadIdx.x, 512);
+                                    SqP, tiles_q, tiles_k, threadIdx.x, NT);
             __syncthreads();
         }
         if (kmask) {
@@ -828,7 +830,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
             const int words = (Sk + 63) >> 6;
             unsigned long long seen = 0ull, always = ~0ull;
             bool empty_row = false;
-            for (int nr = n0 + wave; nr < n1; nr += 8) {
+            for (int nr = n0 + wave; nr < n1; nr += NWV) {
                 const uint8_t* m = kmask + (size_t)nr * Sk;
                 bool any = false;
                 if constexpr (VEC) {
@@ -857,9 +859,9 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
                 // per-score selects).
                 constexpr int NWD = RK / 64;
                 unsigned long long* orw = reinterpret_cast<unsigned long long*>(qd1);
-                unsigned long long* andw = orw + 8 * NWD;
-                int* emptyw = reinterpret_cast<int*>(andw + 8 * NWD);
-                static_assert(sizeof(qd1) >= 16 * NWD * 8 + 8 * 4, "presence words fit");
+                unsigned long long* andw = orw + NWV * NWD;
+                int* emptyw = reinterpret_cast<int*>(andw + NWV * NWD);
+                static_assert(sizeof(qd1) >= 2 * NWV * NWD * 8 + NWV * 4, "presence words fit");
                 if (lane < NWD) {
                     orw[wave * NWD + lane] = seen;
                     andw[wave * NWD + lane] = always;
@@ -871,7 +873,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
                     const int rel = 32 * (i * KQ + kq);
                     unsigned long long w = 0ull;
 #pragma unroll
-                    for (int ww = 0; ww < 8; ++ww) w |= orw[ww * NWD + (rel >> 6)];
+                    for (int ww = 0; ww < NWV; ++ww) w |= orw[ww * NWD + (rel >> 6)];
                     const unsigned bits = (unsigned)(w >> ((rel & 32) + 8 * g)) & 0xffu;
                     cabs |= (~bits & 0xffu) << (8 * i);
                 }
@@ -879,7 +881,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
                 if (lane < NWD) {
                     unsigned long long o = 0ull, a = ~0ull;
 #pragma unroll
-                    for (int ww = 0; ww < 8; ++ww) {
+                    for (int ww = 0; ww < NWV; ++ww) {
                         o |= orw[ww * NWD + lane];
                         a &= andw[ww * NWD + lane];
                     }
@@ -890,7 +892,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
                 }
                 bool empty = false;
 #pragma unroll
-                for (int ww = 0; ww < 8; ++ww) empty |= emptyw[ww] != 0;
+                for (int ww = 0; ww < NWV; ++ww) empty |= emptyw[ww] != 0;
                 block_masked = empty || __any(mixed);
             } else {
                 block_masked = true;
@@ -904,7 +906,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
         for (int j = 0; j < 8; ++j) {
             const int sel = __builtin_amdgcn_sbfe((int)cabs, 8 * i + j, 1);
 #pragma unroll
-            for (int qt = 0; qt < 2; ++qt) {
+            for (int qt = 0; qt < QTW; ++qt) {
                 const float b = bacc[i][qt][j >> 2][j & 3];
                 bacc[i][qt][j >> 2][j & 3] =
                     __int_as_float((~sel & __float_as_int(b)) | (sel & __float_as_int(-INFINITY)));
@@ -932,7 +934,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dq2(
         const int kk = kbeg + 32 * (i * KQ + kq) + 8 * g;
         if (kbeg + 32 * (i * KQ + kq) >= kend) continue;
 #pragma unroll
-        for (int qt = 0; qt < 2; ++qt) {
+        for (int qt = 0; qt < QTW; ++qt) {
             if (qrow[qt] >= Sq) continue;
             float* drow = dbias_dst + (((size_t)chunk * H + h) * Sq + qrow[qt]) * Sk;
             if (VEC) {
@@ -1198,7 +1200,18 @@ int grid_for(size_t count) {
 // Work decomposition of the backward pass; a pure function of the sizes, so the workspace size
 // and the launches always agree and the reduction order is fixed. Head dims up to 32 take the
 // prep / dq2 / dkv2 path (v2); D = 64 takes dot / dq / dkv.
-constexpr int kTargetBlocks = 256;  // one 8-wave row-owner block per CU of an MI355X
+constexpr int kTargetBlocks = 256;  // one row-owner block per CU of an MI355X
+// Row-owner block shape for head dim D: QG query groups of four waves, each wave QTW 16-query
+// sub-tiles (BQ = 16*QG*QTW queries per block). Two groups of two sub-tiles (8 waves, two per
+// SIMD, 255 VGPRs at D = 32): three groups of one sub-tile (12 waves, three per SIMD, 161
+// VGPRs) measured only 1 us faster at N_res = 384, with a third more LDS reads per MFMA, and its
+// 48-query tiles leave an eighth of the work empty at Sq = 256.
+template <int D>
+struct DqShape {
+    static constexpr int QG = 2, QTW = 2;
+    static constexpr int BQ = 16 * QG * QTW;
+};
+inline int dq_block_queries(int64_t) { return DqShape<32>::BQ; }
 
 struct BwdPlan {
     bool v2 = false;
@@ -1232,7 +1245,7 @@ BwdPlan plan_bwd(int64_t N, int64_t H, int64_t Sq, int64_t Sk, int64_t D) {
             p.KNW = 4;
         }
         p.SqP = (int)((Sq + 63) / 64 * 64);
-        qtiles = (Sq + 63) / 64;
+        qtiles = (Sq + dq_block_queries(D) - 1) / dq_block_queries(D);
     } else {
         const int64_t ktiles = (Sk + 63) / 64;
         p.KT = ktiles <= 2 ? 2 : ktiles <= 4 ? 4 : ktiles <= 6 ? 6 : 8;
@@ -1356,9 +1369,10 @@ void launch_dq2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, 
                 void* dq, float* dq_part, float* dbias_dst, void* bias_t, int N, int H, int Sq,
                 int Sk, float scale) {
     using E = typename TR::elem;
-    const dim3 grid(ceil_div(Sq, 64) * H * p.nchunks * p.nranges);
+    using S = DqShape<D>;
+    const dim3 grid(ceil_div(Sq, S::BQ) * H * p.nchunks * p.nranges);
     KernelTimer timer("attn_bwd_dq", st);
-    attn_bwd_dq2<TR, D, KCW, VEC><<<grid, 512, 0, st>>>(
+    attn_bwd_dq2<TR, D, KCW, VEC, S::QG, S::QTW><<<grid, 64 * 4 * S::QG, 0, st>>>(
         (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (const E*)out,
         (const E*)dout, lse, rowl, mbits, lse2, ndi, (E*)dq, dq_part, dbias_dst, N, H, Sq, Sk, p.NB,
         p.nranges, scale, LogitForm::make(scale), (E*)bias_t, p.SqP, ceil_div(p.SqP, 64),
