@@ -159,16 +159,16 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
     using V8 = typename TR::vec8;
     using G = AttnGeom<D>;
     using T = SwzTile<D>;
-    // PATCH (bfloat16 with the bias tile in LDS): a key tile with an absent key (or keys past
-    // Sk) has its bias changed in LDS before use -- -1e9, the masked logit, for an absent key
-    // (P = 0 after the exponential once the row's max comes from a present key), 0 for every key
-    // in range in a row without any present key (whose Q^T is zero, so every logit is that
-    // row's masked logit 0) -- and the scores need no per-key select, so the tile's MFMAs and
-    // exponentials stay one straight-line block. (-1e9 is beyond float16's range: float16
-    // keeps the selects. A larger magnitude would not do: the exponent's FMA against the
-    // running max leaves a rounding residue of about 2^-24 of the logit, which must stay far
-    // below float32's exponent range.)
-    constexpr bool PATCH = VEC && std::is_same<TR, BF16>::value;
+    // PATCH (the bias tile in LDS): a key tile with an absent key (or keys past Sk) has its bias
+    // changed in LDS before use -- a large negative bias for an absent key (P = 0 after the
+    // exponential once the row's max comes from a present key): the masked logit -1e9 in
+    // bfloat16, float16's lowest value -65504 in float16 (the reference's own masked logit is
+    // -1e4); 0 for every key in range in a row without any present key (whose Q^T is zero, so
+    // every logit is that row's masked logit 0) -- and the scores need no per-key select, so the
+    // tile's MFMAs and exponentials stay one straight-line block. (No larger magnitude: the
+    // exponent's FMA against the running max leaves a rounding residue of about 2^-24 of the
+    // logit, which must stay far below float32's exponent range.)
+    constexpr bool PATCH = VEC;
     using PF = TilePrefetch<TR, QT, VEC, BM>;
     constexpr int BQ = 4 * 16 * QT;
     constexpr int BK = G::BK;
@@ -297,7 +297,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
     // written back in one round.
     auto patch = [&](const char* kvc, int kt) {
         char* const bt = const_cast<char*>(kvc) + 2 * TILE;
-        const uint32_t neg = (uint32_t)__builtin_bit_cast(uint16_t, TR::from_f(kMaskedLogit)) * 0x10001u;
+        const float fill_bias = std::is_same<TR, BF16>::value ? kMaskedLogit : -65504.f;
+        const uint32_t neg = (uint32_t)__builtin_bit_cast(uint16_t, TR::from_f(fill_bias)) * 0x10001u;
         u32x4* at[2][QT];
         u32x4 v[2][QT];
 #pragma unroll
@@ -311,7 +312,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             const int kk = kt * BK + 32 * c + 8 * g;
-            // A key past Sk gets the masked logit in every row.
+            // A key past Sk gets the fill value in every row.
             const uint32_t fill = kk < Sk && row_empty ? 0u : neg;
             const uint32_t bits = reinterpret_cast<const uint32_t*>(pres)[2 * kt + c] >> (8 * g);
             // Dword i holds keys 2i, 2i+1 (low, high half): keep the bias of present keys.
@@ -626,10 +627,10 @@ void launch_fwd_qt(hipStream_t st, const void* q, const void* k, const void* v, 
                    float scale, GateArgs<typename TR::elem> ga) {
     using E = typename TR::elem;
     const dim3 grid(ceil_div(Sq, 64 * QT) * H * N);
-    // The bias tile through LDS: whole 8-key pieces and 8-byte aligned mask rows; for bfloat16
-    // (which patches masked bias tiles in LDS) at most kPresWords key tiles.
+    // The bias tile through LDS: whole 8-key pieces, 8-byte aligned mask rows and at most
+    // kPresWords key tiles (masked bias tiles are changed in LDS from presence words kept there).
     const bool vec = Sk % 8 == 0 && (reinterpret_cast<uintptr_t>(kmask) & 7u) == 0 &&
-                     (!std::is_same<TR, BF16>::value || Sk <= kPresWords * 64);
+                     Sk <= kPresWords * 64;
     BiasMfma bm{};
     if (vec && bias_mfma_for<TR>(scale, &bm))
         attn_fwd_kernel<TR, D, QT, true, GATE, true><<<grid, 256, 0, st>>>(
