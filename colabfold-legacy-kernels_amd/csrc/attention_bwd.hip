@@ -27,6 +27,11 @@
 namespace clk {
 namespace {
 
+// How a row-owner block's rows are masked, and the chunk code a row step runs.
+constexpr int kRowsClean = 0, kRowsEmpty = 1, kRowsMixed = 2;
+constexpr int kChunksClean = 0, kChunksSelect = 1, kChunksEmpty = 2;
+
+
 template <typename TR, int D>
 __global__ __launch_bounds__(256) void attn_bwd_dot(const typename TR::elem* __restrict__ out,
                                                     const typename TR::elem* __restrict__ dout,
@@ -631,15 +636,11 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
         pend_n = -1;
     };
 
-    // One row step. MASKED (the block has a row with no present key, or a key present in some
-    // of its rows and absent in others): absent keys take the row's masked logit by per-score
-    // selects. Otherwise every row's absent keys are the block's common ones, whose resident
-    // bias is -inf, and the chunks need no select. Either way the chunks are straight-line code:
-    // a branch between the MFMAs and the exponentials of a chunk, or between chunks, keeps the
-    // scheduler from overlapping them.
+    // One row step; `rows_tag` says how the block's rows are masked (kRowsClean, kRowsEmpty,
+    // kRowsMixed, below).
     auto step = [&](int n, const char* kvc, const char* qdc, char* kvn, char* qdn,
-                    auto masked_tag) __attribute__((always_inline)) {
-        constexpr bool MASKED = decltype(masked_tag)::value;
+                    auto rows_tag) __attribute__((always_inline)) {
+        constexpr int ROWS = decltype(rows_tag)::value;
         const size_t nh = (size_t)n * H + h;
         async_wait();
         __syncthreads();  // row n in (kvc, qdc); every wave is done with row n-1
@@ -716,79 +717,109 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
 #pragma unroll
             for (int dt = 0; dt < DT; ++dt) dqa[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-        // An absent key's log2(P) (MASKED): its row's masked logit, in the same units.
-        float mx[QTW];
-#pragma unroll
-        for (int qt = 0; qt < QTW; ++qt) mx[qt] = fmaf(mlc, kLog2e, -lse2c[qt]);
         // The wave's 32-key chunks: S^T and dP^T - D by MFMA, P, dS, the dBias sums, and
-        // dQ^T += K^T.dS^T.
+        // dQ^T += K^T.dS^T. CHUNKS: kChunksClean (every key present, or absent from every row of
+        // the block: resident bias -inf, so P = 0 there without any per-score instruction),
+        // kChunksSelect (absent keys take the row's masked logit by per-score selects, in the
+        // chunks that have one), kChunksEmpty (a row without any present key: every logit is the
+        // masked logit 0, so P = exp2(-lse*log2e) for every key and no S is needed). Each
+        // version's chunks are straight-line code apart from kChunksSelect's test: a branch
+        // between the MFMAs and the exponentials of a chunk, or between chunks, keeps the
+        // scheduler from overlapping them.
+        auto chunks = [&](auto chunks_tag) __attribute__((always_inline)) {
+            constexpr int CHUNKS = decltype(chunks_tag)::value;
+            // An absent key's log2(P): its row's masked logit, in the same units.
+            float mx[QTW];
 #pragma unroll
-        for (int i = 0; i < KCW; ++i) {
-            const int c0 = 32 * (i * KQ + kq);  // chunk's first key, relative to kbeg
-            if (kbeg + c0 >= kend) continue;   // block-uniform, the same for every row
-            V8 kf[2], vf[2];
+            for (int qt = 0; qt < QTW; ++qt) mx[qt] = fmaf(mlc, kLog2e, -lse2c[qt]);
+            float pe[QTW];  // kChunksEmpty: the one P of the row's queries
+            if constexpr (CHUNKS == kChunksEmpty) {
 #pragma unroll
-            for (int t = 0; t < 2; ++t) {
-                const int row = c0 + 8 * (r16 >> 2) + 4 * t + (r16 & 3);
-                kf[t] = swz_row_operand<V8, D>(kvc, row, 0, g);
-                vf[t] = swz_row_operand<V8, D>(kvc + KVB, row, 0, g);
+                for (int qt = 0; qt < QTW; ++qt) pe[qt] = fast_exp2(mx[qt]);
             }
-            f32x4 s[QTW][2], dp[QTW][2];
 #pragma unroll
-            for (int t = 0; t < 2; ++t)
+            for (int i = 0; i < KCW; ++i) {
+                const int c0 = 32 * (i * KQ + kq);  // chunk's first key, relative to kbeg
+                if (kbeg + c0 >= kend) continue;   // block-uniform, the same for every row
+                V8 kf[2], vf[2];
 #pragma unroll
-                for (int qt = 0; qt < QTW; ++qt) {
-                    s[qt][t] = TR::mfma(kf[t], qf[qt], bacc[i][qt][t]);
-                    dp[qt][t] = TR::mfma(vf[t], dof[qt], f32x4{-di[qt], -di[qt], -di[qt], -di[qt]});
+                for (int t = 0; t < 2; ++t) {
+                    const int row = c0 + 8 * (r16 >> 2) + 4 * t + (r16 & 3);
+                    if constexpr (CHUNKS != kChunksEmpty) kf[t] = swz_row_operand<V8, D>(kvc, row, 0, g);
+                    vf[t] = swz_row_operand<V8, D>(kvc + KVB, row, 0, g);
                 }
-            // The chunk's VALU work (exponentials, dS, the dBias sums) runs at a raised wave
-            // priority until its dQ MFMAs are issued: the other wave on the SIMD then gets the
-            // issue slots while this one waits on its S and dP MFMAs (2-3 us at N_res = 384).
-            __builtin_amdgcn_s_setprio(1);
-            // x = log2(P) = logit * log2(e) - lse * log2(e), one FMA per score.
-            float x[QTW][8];
+                f32x4 s[QTW][2], dp[QTW][2];
 #pragma unroll
-            for (int qt = 0; qt < QTW; ++qt)
+                for (int t = 0; t < 2; ++t)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) x[qt][j] = fmaf(s[qt][j >> 2][j & 3], lf.cexp, -lse2c[qt]);
-            if constexpr (MASKED) {
-                // The selects, for a chunk with a key absent in this row but present in another
-                // row of the block, or in a row with no present key (wave-uniform). Bit j of
-                // `valid` spread over a word (0 or ~0) selects x or mx bitwise. Keys past Sk have
-                // no valid bit: in a row with a present key their P is 0; in a row without one,
-                // P = exp2(-lse2) as for the absent keys in range, which is harmless: their K
-                // rows are staged as zeros and their dBias is never stored.
-                const unsigned valid = (vbits >> (8 * i)) & 0xffu;
-                if (mlc == 0.f || __any((valid | ((cabs >> (8 * i)) & 0xffu)) != 0xffu)) {
-                    // Opaque to speculation: nothing of it is hoisted onto the unmasked path.
-                    asm volatile("");
+                    for (int qt = 0; qt < QTW; ++qt) {
+                        if constexpr (CHUNKS != kChunksEmpty)
+                            s[qt][t] = TR::mfma(kf[t], qf[qt], bacc[i][qt][t]);
+                        dp[qt][t] = TR::mfma(vf[t], dof[qt], f32x4{-di[qt], -di[qt], -di[qt], -di[qt]});
+                    }
+                // The chunk's VALU work (exponentials, dS, the dBias sums) runs at a raised wave
+                // priority until its dQ MFMAs are issued: the other wave on the SIMD then gets
+                // the issue slots while this one waits on its S and dP MFMAs.
+                __builtin_amdgcn_s_setprio(1);
+                // x = log2(P) = logit * log2(e) - lse * log2(e), one FMA per score.
+                float x[QTW][8];
+                if constexpr (CHUNKS != kChunksEmpty) {
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const int sel = __builtin_amdgcn_sbfe((int)valid, j, 1);
+                    for (int qt = 0; qt < QTW; ++qt)
 #pragma unroll
-                        for (int qt = 0; qt < QTW; ++qt)
-                            x[qt][j] = __int_as_float((sel & __float_as_int(x[qt][j])) |
-                                                      (~sel & __float_as_int(mx[qt])));
+                        for (int j = 0; j < 8; ++j)
+                            x[qt][j] = fmaf(s[qt][j >> 2][j & 3], lf.cexp, -lse2c[qt]);
+                }
+                if constexpr (CHUNKS == kChunksSelect) {
+                    // The selects, for a chunk with a key absent in this row but present in
+                    // another row of the block, or in a row with no present key (wave-uniform).
+                    // Bit j of `valid` spread over a word (0 or ~0) selects x or mx bitwise. Keys
+                    // past Sk have no valid bit: in a row with a present key their P is 0; in a
+                    // row without one, P = exp2(-lse2) as for the absent keys in range, which is
+                    // harmless: their K rows are staged as zeros and their dBias is never stored.
+                    const unsigned valid = (vbits >> (8 * i)) & 0xffu;
+                    if (mlc == 0.f || __any((valid | ((cabs >> (8 * i)) & 0xffu)) != 0xffu)) {
+                        // Opaque to speculation: nothing of it is hoisted onto the unmasked path.
+                        asm volatile("");
+#pragma unroll
+                        for (int j = 0; j < 8; ++j) {
+                            const int sel = __builtin_amdgcn_sbfe((int)valid, j, 1);
+#pragma unroll
+                            for (int qt = 0; qt < QTW; ++qt)
+                                x[qt][j] = __int_as_float((sel & __float_as_int(x[qt][j])) |
+                                                          (~sel & __float_as_int(mx[qt])));
+                        }
                     }
                 }
-            }
-            V8 dsf[QTW];
+                V8 dsf[QTW];
 #pragma unroll
-            for (int qt = 0; qt < QTW; ++qt)
+                for (int qt = 0; qt < QTW; ++qt)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const float p = fast_exp2(x[qt][j]);
-                    const float ds = p * dp[qt][j >> 2][j & 3];
-                    dbias[i][qt][j >> 2][j & 3] += ds;
-                    dsf[qt][j] = TR::from_f(ds);
+                    for (int j = 0; j < 8; ++j) {
+                        // (Keys past Sk get pe too in kChunksEmpty, harmless as above.)
+                        const float p = CHUNKS == kChunksEmpty ? pe[qt] : fast_exp2(x[qt][j]);
+                        const float ds = p * dp[qt][j >> 2][j & 3];
+                        dbias[i][qt][j >> 2][j & 3] += ds;
+                        dsf[qt][j] = TR::from_f(ds);
+                    }
+#pragma unroll
+                for (int dt = 0; dt < DT; ++dt) {
+                    const V8 kt = swz_tr_operand<V8, D>(kvc, c0, dt, r16, g);
+#pragma unroll
+                    for (int qt = 0; qt < QTW; ++qt) dqa[qt][dt] = TR::mfma(kt, dsf[qt], dqa[qt][dt]);
                 }
-#pragma unroll
-            for (int dt = 0; dt < DT; ++dt) {
-                const V8 kt = swz_tr_operand<V8, D>(kvc, c0, dt, r16, g);
-#pragma unroll
-                for (int qt = 0; qt < QTW; ++qt) dqa[qt][dt] = TR::mfma(kt, dsf[qt], dqa[qt][dt]);
+                __builtin_amdgcn_s_setprio(0);
             }
-            __builtin_amdgcn_s_setprio(0);
+        };
+        if constexpr (ROWS == kRowsMixed) {
+            chunks(std::integral_constant<int, kChunksSelect>{});
+        } else if constexpr (ROWS == kRowsEmpty) {
+            if (mlc == 0.f)  // block-uniform: the row has no present key
+                chunks(std::integral_constant<int, kChunksEmpty>{});
+            else
+                chunks(std::integral_constant<int, kChunksClean>{});
+        } else {
+            chunks(std::integral_constant<int, kChunksClean>{});
         }
 
 #pragma unroll
@@ -807,8 +838,10 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
         }
     };
 
-    // Whether the rows need per-score selects (set below when a mask is given).
-    bool block_masked = false;
+    // How the block's rows are masked (set below when a mask is given): kRowsClean (every key
+    // is present in all rows or in none), kRowsEmpty (that, apart from rows with no present key),
+    // kRowsMixed (some key present in some rows with a present key and absent in others).
+    int block_rows = kRowsClean;
 
     // Work of the column-owner pass that would otherwise take a kernel of its own: the
     // transposed bias (one 64 x 64 tile per block, through the dQ exchange buffer, which is
@@ -834,15 +867,17 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
                 const uint8_t* m = kmask + (size_t)nr * Sk;
                 bool any = false;
                 if constexpr (VEC) {
+                    unsigned long long mine = 0ull;  // this lane's word of the row
                     for (int i = 0; i < words; ++i) {
                         const int kk = 64 * i + lane;
                         const unsigned long long b = __ballot(kk < Sk && m[kk] != 0);
                         any |= b != 0ull;
                         if (lane == 0) mbits[(size_t)nr * words + i] = b;
-                        if (lane == i - (kbeg >> 6)) {
-                            seen |= b;
-                            always &= b;
-                        }
+                        if (lane == i - (kbeg >> 6)) mine = b;
+                    }
+                    if (any) {  // rows with a present key only
+                        seen |= mine;
+                        always &= mine;
                     }
                 } else {
                     for (int i = lane; i < Sk; i += 64) any |= m[i] != 0;
@@ -852,11 +887,10 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
                 if (lane == 0) row_logit[nr] = any ? kMaskedLogit : 0.f;
             }
             if constexpr (VEC) {
-                // The eight waves' words combined through the second Q/dO/O buffer (idle until
-                // the first row step stages row n0 + 1): the keys present in no row of the block
-                // (their bias becomes -inf), and whether every key of the range is present in
-                // all rows or in none and every row has a present key (then no row needs
-                // per-score selects).
+                // The waves' words combined through the second Q/dO/O buffer (idle until the
+                // first row step stages row n0 + 1): the keys present in no row of the block
+                // (their bias becomes -inf), whether every key of the range is present in all
+                // rows that have a present key or in none of them, and whether a row has none.
                 constexpr int NWD = RK / 64;
                 unsigned long long* orw = reinterpret_cast<unsigned long long*>(qd1);
                 unsigned long long* andw = orw + NWV * NWD;
@@ -893,9 +927,9 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
                 bool empty = false;
 #pragma unroll
                 for (int ww = 0; ww < NWV; ++ww) empty |= emptyw[ww] != 0;
-                block_masked = empty || __any(mixed);
+                block_rows = __any(mixed) ? kRowsMixed : empty ? kRowsEmpty : kRowsClean;
             } else {
-                block_masked = true;
+                block_rows = kRowsMixed;
             }
             __syncthreads();  // this block's prefetches read them; the combined words are read
         }
@@ -923,10 +957,12 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
             if (n + 1 < n1) step(n + 1, kv1, qd1, kv0, qd0, masked_tag);
         }
     };
-    if (block_masked)
-        rows(std::true_type{});
+    if (block_rows == kRowsMixed)
+        rows(std::integral_constant<int, kRowsMixed>{});
+    else if (block_rows == kRowsEmpty)
+        rows(std::integral_constant<int, kRowsEmpty>{});
     else
-        rows(std::false_type{});
+        rows(std::integral_constant<int, kRowsClean>{});
     flush_dq();
 
 #pragma unroll
@@ -995,7 +1031,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkv2(
     // row without any present key needs the masked logit in place of the logit.
     const float ml = kmask ? row_logit[n] : kMaskedLogit;
     V8 kf[KSUB], vf[KSUB];
-    bool present[KSUB], clean[KSUB], none_present = true;
+    bool present[KSUB], none_present = true;
     float absent_logit[KSUB];
 #pragma unroll
     for (int s = 0; s < KSUB; ++s) {
@@ -1010,8 +1046,6 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkv2(
         vf[s] = bits_as<V8>(rv);
         present[s] = kin && (kmask == nullptr || kmask[(size_t)n * Sk + key] != 0);
         absent_logit[s] = kin ? ml : -INFINITY;
-        // Wave-uniform: no key of the sub-tile needs a select.
-        clean[s] = ml != 0.f || __all(present[s]);
         none_present = none_present && !__any(present[s]);
     }
     // Wave-uniform: every key of the wave is past Sk, or absent in a row with a present key.
@@ -1053,7 +1087,12 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkv2(
         }
     };
 
-    auto compute = [&](const char* qd, const char* bt, const float* st) {
+    // EMPTY: the row has no present key, so every logit in range is the masked logit 0 and no
+    // S is needed. Otherwise absent keys' lanes compute without selects (and store zeros).
+    // Either version is straight-line code.
+    auto compute = [&](const char* qd, const char* bt, const float* st, auto empty_tag)
+                       __attribute__((always_inline)) {
+        constexpr bool EMPTY = decltype(empty_tag)::value;
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
             V8 qa[2], da[2];
@@ -1077,22 +1116,21 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkv2(
                 f32x4 S[2], dP[2];
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
-                    S[t] = TR::mfma(qa[t], kf[s], f32x4{0.f, 0.f, 0.f, 0.f});
+                    if constexpr (!EMPTY) S[t] = TR::mfma(qa[t], kf[s], f32x4{0.f, 0.f, 0.f, 0.f});
                     dP[t] = TR::mfma(da[t], vf[s], n4[t]);
                 }
-                const int row = wave * KW + 16 * s + r16;
-                float b[8];
-                unpack8<TR>(*reinterpret_cast<const u32x4*>(
-                                bt + row * 128 + 16 * ((4 * c + g) ^ (row & 7))),
-                            b);
                 float x[8];
+                if constexpr (EMPTY) {
 #pragma unroll
-                for (int j = 0; j < 8; ++j) x[j] = fmaf(S[j >> 2][j & 3], scale, b[j]);
-                if (!clean[s]) {
-                    // Opaque to speculation: keeps the selects out of the common path.
-                    asm volatile("");
+                    for (int j = 0; j < 8; ++j) x[j] = absent_logit[s];
+                } else {
+                    const int row = wave * KW + 16 * s + r16;
+                    float b[8];
+                    unpack8<TR>(*reinterpret_cast<const u32x4*>(
+                                    bt + row * 128 + 16 * ((4 * c + g) ^ (row & 7))),
+                                b);
 #pragma unroll
-                    for (int j = 0; j < 8; ++j) x[j] = present[s] ? x[j] : absent_logit[s];
+                    for (int j = 0; j < 8; ++j) x[j] = fmaf(S[j >> 2][j & 3], scale, b[j]);
                 }
                 V8 pf, dsf;
 #pragma unroll
@@ -1114,18 +1152,24 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkv2(
 
     const int ntq = (Sq + 63) / 64;
     if (ntq > 0) stage(0, qd0, bt0, st0);
-    for (int it = 0; it < ntq; it += 2) {
-        async_wait();
-        __syncthreads();
-        if (it + 1 < ntq) stage(64 * (it + 1), qd1, bt1, st1);
-        if (active) compute(qd0, bt0, st0);
-        if (it + 1 < ntq) {
+    auto tiles = [&](auto empty_tag) __attribute__((always_inline)) {
+        for (int it = 0; it < ntq; it += 2) {
             async_wait();
             __syncthreads();
-            if (it + 2 < ntq) stage(64 * (it + 2), qd0, bt0, st0);
-            if (active) compute(qd1, bt1, st1);
+            if (it + 1 < ntq) stage(64 * (it + 1), qd1, bt1, st1);
+            if (active) compute(qd0, bt0, st0, empty_tag);
+            if (it + 1 < ntq) {
+                async_wait();
+                __syncthreads();
+                if (it + 2 < ntq) stage(64 * (it + 2), qd0, bt0, st0);
+                if (active) compute(qd1, bt1, st1, empty_tag);
+            }
         }
-    }
+    };
+    if (ml == 0.f)  // block-uniform: the row has no present key
+        tiles(std::true_type{});
+    else
+        tiles(std::false_type{});
 
 #pragma unroll
     for (int s = 0; s < KSUB; ++s) {
