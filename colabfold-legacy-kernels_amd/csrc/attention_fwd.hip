@@ -520,9 +520,60 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
                 for (int c = 0; c < 2; ++c) acc[qt][dt] = TR::mfma(vf[dt][c], pf[c], acc[qt][dt]);
         }
     };
-    for (int kt = 0; kt < ntiles; kt += 2) {
-        tile(kt, kv0, kv1, ca, cb);
-        if (kt + 1 < ntiles) tile(kt + 1, kv1, kv0, cb, ca);
+    // PATCH, a row without any present key: every logit in range is the masked logit 0, so
+    // P = 1 there (and 0 past Sk) with the running max at 0 -- the values the tiles above
+    // compute for such a row -- and a tile needs only its V rows: no S, no exponential.
+    auto tile_empty = [&](int kt, const char* kvc, char* kvn, PF& cur, PF& nxt) {
+        const int k0 = kt * BK;
+        async_wait();
+        __syncthreads();  // tile kt visible; every wave is done with the other buffer
+        if (kt + 1 < ntiles) {
+            stage(k0 + BK, kvn);
+            nxt.load(brow, mp, k0 + BK, g, Sk);
+        } else if constexpr (GATE) {
+            int t = threadIdx.x;
+            asm volatile("" : "+v"(t));
+            stage_rows_ld<D, kGateChannels, 256>(rw, 0, ga.HD, kvn, t);
+        }
+        V8 vf[G::DT][2];
+#pragma unroll
+        for (int dt = 0; dt < G::DT; ++dt)
+#pragma unroll
+            for (int c = 0; c < 2; ++c)
+                vf[dt][c] = BM ? swz_tr_operand_split<V8, D>(kvc + TILE, 32 * c, dt, r16, g)
+                               : swz_tr_operand<V8, D>(kvc + TILE, 32 * c, dt, r16, g);
+        // Slot j of chunk c is key k0 + 32c + 8g + j, or in the bias-MFMA order
+        // k0 + 32c + 4g + j (j < 4) and k0 + 32c + 12 + 4g + j (j >= 4).
+        V8 pf[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+            const int lim = Sk - (k0 + 32 * c + (BM ? 4 : 8) * g);
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+                pf[c][j] = TR::from_f((BM && j >= 4 ? j + 12 : j) < lim ? 1.f : 0.f);
+        }
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
+#pragma unroll
+            for (int c = 0; c < 2; ++c) lsum[qt] = TR::mfma(ones, pf[c], lsum[qt]);
+#pragma unroll
+            for (int dt = 0; dt < G::DT; ++dt)
+#pragma unroll
+                for (int c = 0; c < 2; ++c) acc[qt][dt] = TR::mfma(vf[dt][c], pf[c], acc[qt][dt]);
+        }
+    };
+    if (PATCH && row_empty) {  // block-uniform
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) m_run[qt] = 0.f;
+        for (int kt = 0; kt < ntiles; kt += 2) {
+            tile_empty(kt, kv0, kv1, ca, cb);
+            if (kt + 1 < ntiles) tile_empty(kt + 1, kv1, kv0, cb, ca);
+        }
+    } else {
+        for (int kt = 0; kt < ntiles; kt += 2) {
+            tile(kt, kv0, kv1, ca, cb);
+            if (kt + 1 < ntiles) tile(kt + 1, kv1, kv0, cb, ca);
+        }
     }
 
     // Gate pre-activations in O^T's accumulator layout (lane: rows 16*dt + 4*g + i of head h's
