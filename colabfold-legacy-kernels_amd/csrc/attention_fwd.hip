@@ -256,35 +256,40 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
     // reads the same facts from the presence words instead).
     const RowFlags rf = PATCH ? RowFlags{0ull, kMaskedLogit} : row_flags<VEC>(mp, Sk);
     // PATCH: the row's presence bits, one 64-bit word per key tile (bit j: key 64t + j is
-    // present and below Sk; the launch keeps ntiles <= kPresWords), and per wave whether its
-    // tiles hold a present key.
+    // present and below Sk; the launch keeps ntiles <= kPresWords), and per wave 1 + the last
+    // of its tiles that holds a present key (0 if none).
     __shared__ unsigned long long pres[PATCH ? kPresWords : 1];
-    __shared__ int wave_any[PATCH ? 4 : 1];
+    __shared__ int wave_last[PATCH ? 4 : 1];
     if constexpr (PATCH) {
-        bool any = false;
+        int last = 0;
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
             const int t = wave + 4 * i;
             if (t < ntiles) {
                 const unsigned long long b = __ballot(mb[i] != 0u);
-                any |= b != 0ull;
+                if (b != 0ull) last = t + 1;
                 if (lane == 0) pres[t] = b;
             }
         }
         for (int t = wave + 8; t < ntiles; t += 4) {
             const int kk = t * BK + lane;
             const unsigned long long b = __ballot(kk < Sk && (mp == nullptr || mp[kk] != 0));
-            any |= b != 0ull;
+            if (b != 0ull) last = t + 1;
             if (lane == 0) pres[t] = b;
         }
-        if (lane == 0) wave_any[wave] = any ? 1 : 0;
+        if (lane == 0) wave_last[wave] = last;
     }
     // PATCH: a row without any present key: every logit is its masked logit 0, so Q^T = 0 and
-    // the changed bias tiles hold 0 in range.
+    // the changed bias tiles hold 0 in range. Otherwise the key tiles after the row's last
+    // present key (a padding tail) add P = 0 to O and l and are not run at all: after the row's
+    // max is set their P underflows to 0.
     bool row_empty = false;
+    int nrun = ntiles;  // key tiles the loop runs
     if constexpr (PATCH) {
-        __syncthreads();  // the presence words and flags are visible
-        row_empty = mp && (wave_any[0] | wave_any[1] | wave_any[2] | wave_any[3]) == 0;
+        __syncthreads();  // the presence words and counts are visible
+        const int last = max(max(wave_last[0], wave_last[1]), max(wave_last[2], wave_last[3]));
+        row_empty = mp && last == 0;
+        if (!row_empty) nrun = last;
         if (row_empty) {
 #pragma unroll
             for (int qt = 0; qt < QT; ++qt)
@@ -376,7 +381,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
         } else {
             need_mask = kt >= 64 || ((rf.bits >> kt) & 1ull) != 0ull;
         }
-        if (kt + 1 < ntiles) {
+        if (kt + 1 < nrun) {
             stage(k0 + BK, kvn);
             nxt.load(brow, mp, k0 + BK, g, Sk);
         } else if constexpr (GATE) {
@@ -527,7 +532,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
         const int k0 = kt * BK;
         async_wait();
         __syncthreads();  // tile kt visible; every wave is done with the other buffer
-        if (kt + 1 < ntiles) {
+        if (kt + 1 < nrun) {
             stage(k0 + BK, kvn);
             nxt.load(brow, mp, k0 + BK, g, Sk);
         } else if constexpr (GATE) {
@@ -565,14 +570,14 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
     if (PATCH && row_empty) {  // block-uniform
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) m_run[qt] = 0.f;
-        for (int kt = 0; kt < ntiles; kt += 2) {
+        for (int kt = 0; kt < nrun; kt += 2) {
             tile_empty(kt, kv0, kv1, ca, cb);
-            if (kt + 1 < ntiles) tile_empty(kt + 1, kv1, kv0, cb, ca);
+            if (kt + 1 < nrun) tile_empty(kt + 1, kv1, kv0, cb, ca);
         }
     } else {
-        for (int kt = 0; kt < ntiles; kt += 2) {
+        for (int kt = 0; kt < nrun; kt += 2) {
             tile(kt, kv0, kv1, ca, cb);
-            if (kt + 1 < ntiles) tile(kt + 1, kv1, kv0, cb, ca);
+            if (kt + 1 < nrun) tile(kt + 1, kv1, kv0, cb, ca);
         }
     }
 
@@ -604,8 +609,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
         }
         constexpr int GC = kGateChannels, NX = 2 * GC / 32;
         static_assert(GC * T::ROWB <= 2 * TILE, "a K/V buffer holds kGateChannels wg rows");
-        char* const kfree = (ntiles & 1) ? kv1 : kv0;  // not read by the last key tile
-        char* const klast = (ntiles & 1) ? kv0 : kv1;
+        char* const kfree = (nrun & 1) ? kv1 : kv0;  // not read by the last key tile
+        char* const klast = (nrun & 1) ? kv0 : kv1;
         for (int c0 = 0; c0 < C; c0 += 2 * GC) {
             V8 xo[QT][NX];
 #pragma unroll
@@ -621,7 +626,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
                 }
             }
             __syncthreads();  // every wave is done with both buffers
-            if (c0 > 0 || ntiles == 0) stage_rows_ld<D, GC, 256>(rw, c0, HD, kfree, tid);
+            if (c0 > 0 || nrun == 0) stage_rows_ld<D, GC, 256>(rw, c0, HD, kfree, tid);
             if (c0 + GC < C) stage_rows_ld<D, GC, 256>(rw, c0 + GC, HD, klast, tid);
             async_wait();
             __syncthreads();  // this round's wg rows are visible

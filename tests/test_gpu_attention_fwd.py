@@ -21,7 +21,8 @@ CASES = [
     (2, 3, 257, 129, 32, 0.05, 1),
     (2, 2, 33, 300, 64, 0.0, 0),
     (1, 1, 16, 4100, 32, 0.1, 0),  # more than 64 key tiles, ragged last tile
-    (1, 1, 16, 16400, 32, 0.1, 0),  # more key tiles than bfloat16's masked-bias patching covers
+    (1, 1, 16, 16400, 32, 0.1, 0),  # more key tiles than the masked-bias patching covers
+    (3, 2, 64, 320, 32, 0.6, 1),    # a padding tail of whole key tiles
 ]
 
 

@@ -26,6 +26,8 @@ CASES = [
     (2, 3, 129, 77, 32, 96, 0.05, 1),
     (1, 2, 200, 64, 16, 32, 0.0, 0),
     (2, 1, 1, 1, 32, 160, 0.0, 0),
+    (2, 4, 70, 300, 32, 128, 0.5, 1),  # the last two key tiles hold no present key
+    (2, 2, 40, 256, 16, 64, 0.7, 0),   # ... the last three
 ]
 
 
