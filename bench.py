@@ -27,8 +27,8 @@ rocprofv3 FETCH_SIZE/WRITE_SIZE summaries in profiles/*hbm_traffic*.md (lines
 scale each counter by what it reads for a plain device copy of known size, which
 "--copy-calibration MIB" performs (and nothing else). roofline.issue is the same kernel's
 instruction-issue floor -- its VALU, transcendental and MFMA wave instructions per launch, from
-the committed profiles/*instruction_mix*.md, at 4, 16 and 16 cycles each over the 1024 SIMDs at
-2.4 GHz -- and frac = floor / measured duration.
+the committed profiles/*instruction_mix*.md, at 4, 8 and 16 cycles each over the 1024 SIMDs at
+2.4 GHz (the costs "--issue-calibration" measures) -- and frac = floor / measured duration.
 cpu_baseline times the same math in torch float32 on the host cores (oracle/cpu_baseline.py) on
 all 384 rows by default (--cpu-rows for fewer), repeated for about --cpu-seconds (10 s) and
 reported as the median run in the same unit.
@@ -55,11 +55,14 @@ HBM_PEAK = 8000.0        # GB/s
 N_ROWS, HEADS, NRES, HEAD_DIM = 384, 4, 384, 32
 ROTATE = 3
 
-# Issue rates of one MI355X (256 CUs x 4 SIMDs at 2.4 GHz): a wave64 VALU instruction occupies a
+# Issue costs of one MI355X (256 CUs x 4 SIMDs at 2.4 GHz): a wave64 VALU instruction occupies a
 # 16-lane SIMD for 4 cycles (the published 157.3 TFLOP/s vector fp32 counts two lanes per packed
-# instruction); a 16x16x32 bf16 MFMA (16384 flops) takes 16 cycles at the 2516.6 TFLOP/s peak.
+# instruction); a float32 transcendental (v_exp_f32) 8 cycles; a 16x16x32 bf16 MFMA (16384 flops)
+# 16 cycles at the 2516.6 TFLOP/s peak. "--issue-calibration" measures them: 4.3, 8.6 and 17.4
+# cycles at three waves per SIMD; FMAs and exponentials share the issue slots, while half to
+# three quarters of the MFMAs' time hides under them.
 SIMDS, CLOCK_HZ = 1024, 2.4e9
-VALU_CYCLES, MFMA_CYCLES = 4, 16
+VALU_CYCLES, TRANS_CYCLES, MFMA_CYCLES = 4, 8, 16
 
 
 def _cores():
@@ -511,23 +514,31 @@ def recorded_instructions(kernel):
     return found if len(found) == 3 else None
 
 
+def issue_cycles(valu, trans, mfma):
+    """(VALU + transcendental, MFMA) SIMD cycles of that many wave instructions."""
+    return valu * VALU_CYCLES + trans * TRANS_CYCLES, mfma * MFMA_CYCLES
+
+
 def issue_bound(kernel, avg_ms, scores):
-    """The kernel's instruction-issue floor: its recorded wave instructions at one per SIMD every
-    VALU_CYCLES cycles (transcendentals at a quarter of that rate, MFMA every MFMA_CYCLES) over
-    all SIMDs at CLOCK_HZ, added, since a wave issues one instruction at a time.
-    frac = floor / measured duration."""
+    """The kernel's instruction-issue floor: its recorded wave instructions at VALU_CYCLES,
+    TRANS_CYCLES and MFMA_CYCLES SIMD cycles each over all SIMDs at CLOCK_HZ. bound_ms adds
+    them all (a wave issues one instruction at a time; the calibration finds FMAs and
+    exponentials sharing the issue slots); bound_ms_mfma_hidden counts the VALU and
+    transcendental part only, the floor if every MFMA hid under other waves' work (half to three
+    quarters does in the calibration). frac = bound_ms / measured duration."""
     rec = recorded_instructions(kernel)
     if rec is None:
         return None
     cyc = SIMDS * CLOCK_HZ / 1e3
-    valu_ms = (rec["valu"] * VALU_CYCLES + rec["trans"] * 4 * VALU_CYCLES) / cyc
-    mfma_ms = rec["mfma"] * MFMA_CYCLES / cyc
+    v, m = issue_cycles(rec["valu"], rec["trans"], rec["mfma"])
+    valu_ms, mfma_ms = v / cyc, m / cyc
     lane_ops = (rec["valu"] + rec["trans"]) * 64
     return {"valu_instructions": rec["valu"], "trans_instructions": rec["trans"],
             "mfma_instructions": rec["mfma"], "scores": scores,
             "valu_lane_ops_per_score": lane_ops / scores if scores else None,
+            "cycles": {"valu": VALU_CYCLES, "trans": TRANS_CYCLES, "mfma": MFMA_CYCLES},
             "valu_ms": valu_ms, "mfma_ms": mfma_ms, "bound_ms": valu_ms + mfma_ms,
-            "frac": (valu_ms + mfma_ms) / avg_ms}
+            "bound_ms_mfma_hidden": valu_ms, "frac": (valu_ms + mfma_ms) / avg_ms}
 
 
 def _kernel_key(r):
@@ -588,6 +599,29 @@ def counter_summary(paths):
             cols.append("%.4g" % statistics.median(vals) if vals else "-")
         disp = len({disp for (disp, _) in d})
         print("| `%s` | %d | %d | %s |" % (name, wgs, disp, " | ".join(cols)))
+    mix = ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_VALU_TRANS_F32",
+           "SQ_VALU_MFMA_BUSY_CYCLES", "GRBM_GUI_ACTIVE")
+    if all(c in counters for c in mix):
+        # Derived per-dispatch medians: VALU = SQ_INSTS_VALU less MFMA and transcendentals; the
+        # SIMDs' cycles in a launch = SIMDS * GRBM_GUI_ACTIVE / 8 (that counter sums the XCDs).
+        print()
+        print("| kernel | workgroups | MFMA busy | MFMA instr | VALU instr | trans instr | "
+              "(VALU+trans) per MFMA | issue |")
+        print("|---|---|---|---|---|---|---|---|")
+        for (name, wgs), d in sorted(per.items()):
+            if name.startswith(("at::", "rocprim::")):
+                continue
+            med = {c: statistics.median([v for (disp, cn), v in d.items() if cn == c] or [0.0])
+                   for c in mix}
+            mf, tr = med["SQ_INSTS_MFMA"], med["SQ_INSTS_VALU_TRANS_F32"]
+            plain = med["SQ_INSTS_VALU"] - mf - tr
+            simd = SIMDS * med["GRBM_GUI_ACTIVE"] / 8
+            if simd <= 0:
+                continue
+            v, m = issue_cycles(plain, tr, mf)
+            print("| `%s` | %d | %.1f%% | %.3g | %.3g | %.3g | %s | %.0f%% |" % (
+                name, wgs, 100 * med["SQ_VALU_MFMA_BUSY_CYCLES"] / simd, mf, plain, tr,
+                "%.1f" % ((plain + tr) / mf) if mf else "-", 100 * (v + m) / simd))
     return 0
 
 
@@ -604,6 +638,54 @@ def copy_calibration(mib, reps=5):
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes_read": n * 4, "copy_bytes_written": n * 4, "reps": reps}),
           flush=True)
+    return 0
+
+
+def issue_calibration(iters=20000):
+    """What one wave instruction costs a SIMD on this device, from the library's
+    clk_issue_calibration mixes: each kind on 256 blocks of 256, 512 and 768 threads (one, two
+    and three waves per SIMD, the blocks one per CU), timed with HIP events on the launch stream,
+    in SIMD cycles at CLOCK_HZ. Per wave count, one JSON line: the cycles of an FMA, an
+    exponential and a 16x16x32 bf16 MFMA alone; the share of the MFMAs' own time that a mix with
+    FMAs, exponentials or both hides; and the share of the shorter of FMAs and exponentials that
+    overlaps the other (0: they share the issue slots)."""
+    import torch
+    from colabfold_legacy_kernels import _native as native
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib = native.lib()
+    st = torch.cuda.current_stream(dev)
+    blocks = 256
+    sink = torch.empty(blocks * 1024, device=dev)
+    names = ["fma", "exp", "mfma", "fma+exp", "fma+mfma", "exp+mfma", "fma+exp+mfma"]
+    per_round = {0: 64, 1: 64, 2: 8}  # instructions of the kind in one round (two copies)
+    for threads in (256, 512, 768):
+        waves_per_simd = blocks * threads // 64 / SIMDS
+
+        def run(kind, n):
+            if lib.clk_issue_calibration(st.cuda_stream, kind, blocks, threads, n,
+                                         sink.data_ptr()) != native.OK:
+                raise RuntimeError(native.last_error())
+
+        cyc = {}
+        for kind in range(7):
+            run(kind, 10)
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            run(kind, iters)
+            e1.record(st)
+            e1.synchronize()
+            # SIMD cycles per wave and round
+            cyc[kind] = e0.elapsed_time(e1) * 1e-3 * CLOCK_HZ / iters / waves_per_simd
+        print(json.dumps({
+            "waves_per_simd": waves_per_simd,
+            "cycles_per_instruction": {names[k]: cyc[k] / per_round[k] for k in (0, 1, 2)},
+            "round_cycles": {names[k]: round(cyc[k], 1) for k in range(7)},
+            "mfma_hidden": {"under fma": (cyc[0] + cyc[2] - cyc[4]) / cyc[2],
+                            "under exp": (cyc[1] + cyc[2] - cyc[5]) / cyc[2],
+                            "under fma+exp": (cyc[3] + cyc[2] - cyc[6]) / cyc[2]},
+            "fma_exp_overlap": (cyc[0] + cyc[1] - cyc[3]) / min(cyc[0], cyc[1])}), flush=True)
     return 0
 
 
@@ -633,6 +715,8 @@ def main(argv=None):
     ap.add_argument("--no-secondary", action="store_true")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (counter calibration)")
+    ap.add_argument("--issue-calibration", action="store_true",
+                    help="only measure the per-instruction issue costs (FMA, exponential, MFMA)")
     ap.add_argument("--counter-summary", nargs="+", metavar="CSV",
                     help="only summarise rocprofv3 --pmc (or one --kernel-trace) csv files per "
                          "kernel (no GPU)")
@@ -641,6 +725,8 @@ def main(argv=None):
         return counter_summary(args.counter_summary)
     if args.copy_calibration:
         return copy_calibration(args.copy_calibration)
+    if args.issue_calibration:
+        return issue_calibration()
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (the attention rows "
               "would shard across GPUs with one dBias all-reduce; not built). Use --gpus 1.",

@@ -44,6 +44,7 @@ PROTOTYPES = {
                                           c_void_p, c_void_p, c_void_p, c_void_p, c_i64, c_i64,
                                           c_i64, c_i64, c_i64, c_f32]),
     "clk_stream_copy": (c_int, [c_void_p, c_void_p, c_void_p, c_size]),
+    "clk_issue_calibration": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_void_p]),
     "clk_layer_norm_fwd": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                                    c_i64, c_i64, c_f32]),
     "clk_layer_norm_bwd_workspace_size": (c_size, [c_i64, c_i64]),

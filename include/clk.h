@@ -138,6 +138,19 @@ clk_status clk_attention_bwd_noalloc(hipStream_t stream, clk_dtype dtype, const 
 clk_status clk_stream_copy(hipStream_t stream, const void* src, void* dst, size_t bytes);
 
 /*
+ * Instruction-issue calibration: `blocks` x `threads` threads (threads a multiple of 64, at most
+ * 1024) each run `iters` rounds of one instruction mix and write one float to `sink` (blocks *
+ * threads floats). A round is two copies of: kind 0, 32 float32 FMAs; 1, 32 float32
+ * exponentials (v_exp_f32); 2, four 16x16x32 bf16 MFMAs; 3, kinds 0 and 1; 4, kinds 0 and 2;
+ * 5, kinds 1 and 2; 6, kinds 0, 1 and 2 -- every instruction independent of the others in its
+ * round. Timing the kinds gives each instruction's cost on a SIMD and how far MFMAs hide under
+ * the other kinds. No reference counterpart: it measures the per-instruction costs of the
+ * benchmark's instruction-issue floor.
+ */
+clk_status clk_issue_calibration(hipStream_t stream, int kind, int blocks, int threads,
+                                 int iters, float* sink);
+
+/*
  * LayerNorm forward over the last axis. Replaces VoltaLayerNorm (cuda/volta_ops.cu:62-95):
  * x and y of dtype CLK_F16, CLK_BF16 or CLK_F32; scale and offset float32; attribute eps.
  */

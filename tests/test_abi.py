@@ -117,6 +117,18 @@ def test_stream_copy_validation():
     assert lib.clk_stream_copy(None, None, FAKE, 64) == INVALID
 
 
+def test_issue_calibration_validation():
+    lib = _native.lib()
+    assert lib.clk_issue_calibration(None, 7, 256, 256, 10, FAKE) == INVALID   # no such kind
+    assert lib.clk_issue_calibration(None, -1, 256, 256, 10, FAKE) == INVALID
+    assert lib.clk_issue_calibration(None, 0, 0, 256, 10, FAKE) == INVALID     # no blocks
+    assert lib.clk_issue_calibration(None, 0, 256, 96, 10, FAKE) == INVALID    # not whole waves
+    assert lib.clk_issue_calibration(None, 0, 256, 2048, 10, FAKE) == INVALID  # too many threads
+    assert lib.clk_issue_calibration(None, 0, 256, 256, 0, FAKE) == INVALID    # no rounds
+    assert lib.clk_issue_calibration(None, 0, 256, 256, 10, None) == INVALID
+    assert "issue_calibration" in _native.last_error()
+
+
 def test_workspace_sizes_are_deterministic():
     lib = _native.lib()
     a = lib.clk_attention_bwd_workspace_size(384, 4, 384, 384, 32)

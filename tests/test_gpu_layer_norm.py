@@ -108,3 +108,17 @@ def test_stream_copy(cuda, nbytes):
     assert st == _native.OK, _native.last_error()
     torch.cuda.synchronize()
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("kind", range(7))
+def test_issue_calibration_mixes_run(cuda, kind):
+    """Every instruction mix of the issue calibration runs and writes one finite float per
+    thread (a short launch: 4 blocks of 128 threads, 3 rounds)."""
+    from colabfold_legacy_kernels import _native
+    sink = torch.full((4 * 128,), float("nan"), device=cuda)
+    lib = _native.lib()
+    st = lib.clk_issue_calibration(torch.cuda.current_stream(cuda).cuda_stream, kind, 4, 128, 3,
+                                   sink.data_ptr())
+    assert st == _native.OK, _native.last_error()
+    torch.cuda.synchronize()
+    assert torch.isfinite(sink).all()
