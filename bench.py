@@ -445,6 +445,57 @@ def bench_gated_attention(torch, workloads, native, dev, stream, steps, warmup):
     return res
 
 
+def bench_attention_nshd(torch, workloads, native, dev, stream, steps, warmup):
+    """MSA row attention's forward (bf16) with q, k, v and O in AlphaFold's [N,S,H,D] layout:
+    clk_attention_fwd_nshd on them directly, against transposing q, k, v to [N,H,S,D] (torch
+    copies), clk_attention_fwd, and transposing O back -- what a caller of the [N,H,S,D] entry
+    does -- and against clk_attention_fwd alone. Two rotating sets."""
+    lib = native.lib()
+    sets = []
+    for r in range(2):
+        inp = workloads.attention_workload("msa_row_attn", torch.bfloat16, device=dev,
+                                           with_dout=False)
+        t = {key: inp[key].transpose(1, 2).contiguous() for key in ("q", "k", "v")}
+        inp.update(qs=t["q"], ks=t["k"], vs=t["v"], outs=torch.empty_like(t["q"]),
+                   out=torch.empty_like(inp["q"]))
+        sets.append(inp)
+    n, h, sq, d = sets[0]["q"].shape
+    sk = sets[0]["k"].shape[2]
+
+    def run(st):
+        if st != 0:
+            raise RuntimeError(native.last_error())
+
+    def nshd(i):
+        s = sets[i % 2]
+        run(lib.clk_attention_fwd_nshd(stream, native.BF16, s["qs"].data_ptr(),
+                                       s["ks"].data_ptr(), s["vs"].data_ptr(),
+                                       s["bias"].data_ptr(), s["kmask"].data_ptr(),
+                                       s["outs"].data_ptr(), None, n, h, sq, sk, d, s["scale"]))
+
+    def nhsd(s, q, k, v):
+        run(lib.clk_attention_fwd(stream, native.BF16, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                  s["bias"].data_ptr(), s["kmask"].data_ptr(), s["out"].data_ptr(),
+                                  None, n, h, sq, sk, d, s["scale"], 64, 64))
+
+    def plain(i):
+        s = sets[i % 2]
+        nhsd(s, s["q"], s["k"], s["v"])
+
+    def transposed(i):
+        s = sets[i % 2]
+        q, k, v = (s[key].transpose(1, 2).contiguous() for key in ("qs", "ks", "vs"))
+        nhsd(s, q, k, v)
+        s["outs"].copy_(s["out"].transpose(1, 2))
+
+    so = torch.cuda.current_stream(dev)
+    res = {"attn_nshd_msa_ms": timed(torch, nshd, steps, warmup, so),
+           "attn_nhsd_msa_ms": timed(torch, plain, steps, warmup, so),
+           "attn_nhsd_transposed_msa_ms": timed(torch, transposed, steps, warmup, so)}
+    del sets
+    return res
+
+
 def bench_triangle(torch, native, dev, stream, steps, warmup):
     """Triangle multiplication (outgoing and incoming) on z [512,512,128] bf16 ~N(0,1), mask
     Bernoulli(0.95), six 128x128 weights ~N(0,1/128), biases 0, LayerNorm scales 1 + N(0,0.1)
@@ -811,6 +862,9 @@ def main(argv=None):
         print("bench: timing gated attention, fused and separate", file=sys.stderr, flush=True)
         sec.update(bench_gated_attention(torch, workloads, native, dev, stream, args.steps,
                                          args.warmup))
+        print("bench: timing the forward on the [N,S,H,D] layout", file=sys.stderr, flush=True)
+        sec.update(bench_attention_nshd(torch, workloads, native, dev, stream, args.steps,
+                                        args.warmup))
         print("bench: timing the triangle multiplication", file=sys.stderr, flush=True)
         sec.update(bench_triangle(torch, native, dev, stream, args.steps, args.warmup))
         result["secondary"] = sec

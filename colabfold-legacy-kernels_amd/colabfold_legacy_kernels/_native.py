@@ -29,6 +29,9 @@ PROTOTYPES = {
     "clk_attention_fwd": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                                   c_void_p, c_void_p, c_void_p, c_i64, c_i64, c_i64, c_i64,
                                   c_i64, c_f32, c_i64, c_i64]),
+    "clk_attention_fwd_nshd": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                                       c_void_p, c_void_p, c_void_p, c_i64, c_i64, c_i64, c_i64,
+                                       c_i64, c_f32]),
     "clk_attention_fwd_gated": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p,
                                         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                         c_void_p, c_void_p, c_void_p, c_i64, c_i64, c_i64,

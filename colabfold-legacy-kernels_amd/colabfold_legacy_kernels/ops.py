@@ -145,6 +145,28 @@ def attention_fwd(q, k, v, bias, kmask=None, scale=None):
     return _attention_call(q, k, v, bias, kmask, scale, 64, 64, True, "attention_fwd")
 
 
+def attention_nshd(q, k, v, bias, kmask=None, scale=None, want_lse=False):
+    """The forward on AlphaFold's [N,S,H,D] layout: q [N,Sq,H,D], k/v [N,Sk,H,D], bias
+    [H,Sq,Sk], kmask uint8 [N,Sk]; returns (out [N,Sq,H,D], lse [N,H,Sq] or None), bit-identical
+    to attention_fwd on the [N,H,S,D] transposes."""
+    what = "attention_nshd"
+    dev = _require([("q", q), ("k", k), ("v", v), ("bias", bias), ("kmask", kmask)], what)
+    _shape_check(q.dim() == 4 and k.dim() == 4, what, "q and k must be [N,S,H,D]")
+    n, h, sq, sk, d = _attn_dims(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), bias,
+                                 kmask, what)
+    code = _dtype_code(q, (_native.F16, _native.BF16), what)
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    out = torch.empty_like(q)
+    lse = torch.empty((n, h, sq), device=dev, dtype=torch.float32) if want_lse else None
+    lib = _native.lib()
+    with torch.cuda.device(dev):
+        _check(lib.clk_attention_fwd_nshd(_stream(dev), code, _ptr(q), _ptr(k), _ptr(v),
+                                          _ptr(bias), _ptr(kmask), _ptr(out), _ptr(lse), n, h, sq,
+                                          sk, d, float(scale)))
+    return out, lse
+
+
 def attention_bwd(q, k, v, bias, kmask, out, dout, lse, scale=None):
     """(dq, dk, dv, dbias) with dbias [H,Sq,Sk] float32 summed over the N rows."""
     what = "attention_bwd"

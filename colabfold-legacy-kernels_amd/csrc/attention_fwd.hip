@@ -147,7 +147,7 @@ struct GateArgs {
     int C, HD;
 };
 
-template <typename TR, int D, int QT, bool VEC, bool GATE, bool BM>
+template <typename TR, int D, int QT, bool VEC, bool GATE, bool BM, bool NSHD>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && VEC ? 3 : 1))) void attn_fwd_kernel(
     const typename TR::elem* __restrict__ q, const typename TR::elem* __restrict__ k,
     const typename TR::elem* __restrict__ v, const typename TR::elem* __restrict__ bias,
@@ -155,6 +155,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
     float* __restrict__ lse, int H, int Sq, int Sk, float scale,
     GateArgs<typename TR::elem> ga, BiasMfma bm) {
     static_assert(!BM || VEC, "the bias MFMA reads the bias tile from LDS");
+    static_assert(!(NSHD && GATE), "the gated entry takes the [N, H, S, D] layout");
     using E = typename TR::elem;
     using V8 = typename TR::vec8;
     using G = AttnGeom<D>;
@@ -188,24 +189,36 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
     const int item = xcd_contiguous(blockIdx.x, gridDim.x);
     const int q0 = (item % qtiles) * BQ, h = (item / qtiles) % H, n = item / (qtiles * H);
     const size_t nh = (size_t)n * H + h;
-    const E* qp = q + nh * Sq * D;
-    const E* kp = k + nh * Sk * D;
-    const E* vp = v + nh * Sk * D;
+    // Rows of one (n, h) in q, k, v and out: [N, H, S, D] (rows D apart), or with NSHD
+    // [N, S, H, D] (rows H*D apart, head h at column block h).
+    const int ld = NSHD ? H * D : D;
+    const E* qp = q + (NSHD ? ((size_t)n * Sq * H + h) * D : nh * Sq * D);
+    const E* kp = k + (NSHD ? ((size_t)n * Sk * H + h) * D : nh * Sk * D);
+    const E* vp = v + (NSHD ? ((size_t)n * Sk * H + h) * D : nh * Sk * D);
+    E* const op = out ? out + (NSHD ? ((size_t)n * Sq * H + h) * D : nh * Sq * D) : nullptr;
     const E* bp = bias + (size_t)h * Sq * Sk;
     const uint8_t* mp = kmask ? kmask + (size_t)n * Sk : nullptr;
     const int qbase = q0 + wave * 16 * QT;
     const int ntiles = (Sk + BK - 1) / BK;
 
-    const Rsrc rk = buffer_rsrc(kp, (uint32_t)Sk * D * 2);
-    const Rsrc rv = buffer_rsrc(vp, (uint32_t)Sk * D * 2);
+    // The Sk rows of (n, h): rows past Sk read zeros.
+    const uint32_t kvbytes = NSHD ? (Sk > 0 ? (uint32_t)(((size_t)(Sk - 1) * ld + D) * 2) : 0u)
+                                  : (uint32_t)Sk * D * 2;
+    const Rsrc rk = buffer_rsrc(kp, kvbytes);
+    const Rsrc rv = buffer_rsrc(vp, kvbytes);
     // The block's bias rows (queries q0 .. q0+BQ-1 that exist).
     const Rsrc rb = buffer_rsrc(bp + (size_t)q0 * Sk, (uint32_t)(min(BQ, Sq - q0) * Sk * 2));
     // Head h's D columns of the gate weight: row c (channel) starts HD elements after row c-1.
     const Rsrc rw = GATE ? buffer_rsrc(ga.wg + h * D, (uint32_t)((ga.C - 1) * ga.HD + D) * 2)
                          : rb;
     auto stage = [&](int k0, char* kv) {
-        stage_rows<D, BK, 256>(rk, k0, kv);
-        stage_rows<D, BK, 256>(rv, k0, kv + TILE);
+        if constexpr (NSHD) {
+            stage_rows_ld<D, BK, 256>(rk, k0, ld, kv, threadIdx.x);
+            stage_rows_ld<D, BK, 256>(rv, k0, ld, kv + TILE, threadIdx.x);
+        } else {
+            stage_rows<D, BK, 256>(rk, k0, kv);
+            stage_rows<D, BK, 256>(rv, k0, kv + TILE);
+        }
         if constexpr (VEC) {
             // Bias rows q0 .. q0+BQ-1, keys k0 .. k0+63 as eight 16-byte pieces per row; piece
             // p of row r sits at position p ^ (r & 7), so a 16-row operand read is conflict-free.
@@ -241,7 +254,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
         for (int ks = 0; ks < G::KS; ++ks) {
             const int d0 = ks * 32 + g * 8;
             u32x4 raw = {0u, 0u, 0u, 0u};
-            if (row < Sq && d0 < D) raw = ld16(qp + (size_t)row * D + d0);
+            if (row < Sq && d0 < D) raw = ld16(qp + (size_t)row * ld + d0);
             qf[qt][ks] = bits_as<V8>(raw);
         }
     }
@@ -664,7 +677,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
             const int d = 16 * dt + 4 * eg;
             if (d >= D) continue;
             const f32x4 o = acc[qt][dt] * inv;
-            if (!GATE || out) store4<TR>(out + (nh * Sq + row) * D + d, o);
+            if (!GATE || out) store4<TR>(op + (size_t)row * ld + d, o);
             if constexpr (GATE) {
                 f32x4 r;
 #pragma unroll
@@ -677,7 +690,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
     }
 }
 
-template <typename TR, int D, int QT, bool GATE>
+template <typename TR, int D, int QT, bool GATE, bool NSHD>
 void launch_fwd_qt(hipStream_t st, const void* q, const void* k, const void* v, const void* bias,
                    const uint8_t* kmask, void* out, float* lse, int N, int H, int Sq, int Sk,
                    float scale, GateArgs<typename TR::elem> ga) {
@@ -689,15 +702,15 @@ void launch_fwd_qt(hipStream_t st, const void* q, const void* k, const void* v, 
                      Sk <= kPresWords * 64;
     BiasMfma bm{};
     if (vec && bias_mfma_for<TR>(scale, &bm))
-        attn_fwd_kernel<TR, D, QT, true, GATE, true><<<grid, 256, 0, st>>>(
+        attn_fwd_kernel<TR, D, QT, true, GATE, true, NSHD><<<grid, 256, 0, st>>>(
             (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (E*)out, lse, H, Sq, Sk,
             scale, ga, bm);
     else if (vec)
-        attn_fwd_kernel<TR, D, QT, true, GATE, false><<<grid, 256, 0, st>>>(
+        attn_fwd_kernel<TR, D, QT, true, GATE, false, NSHD><<<grid, 256, 0, st>>>(
             (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (E*)out, lse, H, Sq, Sk,
             scale, ga, bm);
     else
-        attn_fwd_kernel<TR, D, QT, false, GATE, false><<<grid, 256, 0, st>>>(
+        attn_fwd_kernel<TR, D, QT, false, GATE, false, NSHD><<<grid, 256, 0, st>>>(
             (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (E*)out, lse, H, Sq, Sk,
             scale, ga, bm);
 }
@@ -705,30 +718,43 @@ void launch_fwd_qt(hipStream_t st, const void* q, const void* k, const void* v, 
 template <typename TR, int D, bool GATE>
 void launch_fwd(hipStream_t st, const void* q, const void* k, const void* v, const void* bias,
                 const uint8_t* kmask, void* out, float* lse, int N, int H, int Sq, int Sk,
-                float scale, GateArgs<typename TR::elem> ga) {
+                float scale, GateArgs<typename TR::elem> ga, int nshd) {
     KernelTimer timer(GATE ? "attn_fwd_gated" : "attn_fwd", st);
+    // The [N, S, H, D] layout only for the ungated forward.
+    if constexpr (!GATE) {
+        if (nshd) {
+            if (Sq <= 64)
+                launch_fwd_qt<TR, D, 1, GATE, true>(st, q, k, v, bias, kmask, out, lse, N, H, Sq,
+                                                    Sk, scale, ga);
+            else
+                launch_fwd_qt<TR, D, 2, GATE, true>(st, q, k, v, bias, kmask, out, lse, N, H, Sq,
+                                                    Sk, scale, ga);
+            return;
+        }
+    }
     if (Sq <= 64)
-        launch_fwd_qt<TR, D, 1, GATE>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk, scale, ga);
+        launch_fwd_qt<TR, D, 1, GATE, false>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk,
+                                             scale, ga);
     else
-        launch_fwd_qt<TR, D, 2, GATE>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk, scale, ga);
+        launch_fwd_qt<TR, D, 2, GATE, false>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk,
+                                             scale, ga);
 }
 
 template <typename TR, bool GATE>
 void dispatch_fwd(hipStream_t st, int64_t D, const void* q, const void* k, const void* v,
                   const void* bias, const uint8_t* kmask, void* out, float* lse, int N, int H,
-                  int Sq, int Sk, float scale, GateArgs<typename TR::elem> ga) {
+                  int Sq, int Sk, float scale, GateArgs<typename TR::elem> ga, int nshd = 0) {
     switch (D) {
-        case 8:
-            launch_fwd<TR, 8, GATE>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk, scale, ga);
-            break;
-        case 16:
-            launch_fwd<TR, 16, GATE>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk, scale, ga);
-            break;
-        case 32:
-            launch_fwd<TR, 32, GATE>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk, scale, ga);
-            break;
+#define CLK_FWD_D(DV)                                                                           \
+    case DV:                                                                                    \
+        launch_fwd<TR, DV, GATE>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk, scale, ga,   \
+                                 nshd);                                                         \
+        break;
+        CLK_FWD_D(8) CLK_FWD_D(16) CLK_FWD_D(32)
+#undef CLK_FWD_D
         default:
-            launch_fwd<TR, 64, GATE>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk, scale, ga);
+            launch_fwd<TR, 64, GATE>(st, q, k, v, bias, kmask, out, lse, N, H, Sq, Sk, scale, ga,
+                                     nshd);
             break;
     }
 }
@@ -766,6 +792,31 @@ extern "C" clk_status clk_attention_fwd(hipStream_t stream, clk_dtype dtype, con
         dispatch_fwd<F16, false>(stream, D, q, k, v, bias, kmask, out, lse, (int)N, (int)H,
                                  (int)Sq, (int)Sk, scale, {});
     return check_launch("attention");
+}
+
+extern "C" clk_status clk_attention_fwd_nshd(hipStream_t stream, clk_dtype dtype, const void* q,
+                                             const void* k, const void* v, const void* bias,
+                                             const uint8_t* kmask, void* out, float* lse,
+                                             int64_t N, int64_t H, int64_t Sq, int64_t Sk,
+                                             int64_t D, float scale) {
+    const char* who = "attention_nshd";
+    clk_status s = validate_attention(who, dtype, N, H, Sq, Sk, D);
+    if (s != CLK_OK) return s;
+    // Byte offsets within the rows of one (n, h) are 32-bit: S*H*D*2 below 2^31.
+    if ((Sq > Sk ? Sq : Sk) * H * D * 2 >= ((int64_t)1 << 31))
+        return fail(CLK_INVALID_ARGUMENT, "%s: S*H*D too large for the [N,S,H,D] layout", who);
+    if (N * H * Sq == 0) return ok();
+    if (!q || !k || !v || !bias || !out)
+        return fail(CLK_INVALID_ARGUMENT, "%s: null operand pointer", who);
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(bias) || !aligned16(out))
+        return fail(CLK_INVALID_ARGUMENT, "%s: q, k, v, bias, out must be 16-byte aligned", who);
+    if (dtype == CLK_BF16)
+        dispatch_fwd<BF16, false>(stream, D, q, k, v, bias, kmask, out, lse, (int)N, (int)H,
+                                  (int)Sq, (int)Sk, scale, {}, 1);
+    else
+        dispatch_fwd<F16, false>(stream, D, q, k, v, bias, kmask, out, lse, (int)N, (int)H,
+                                 (int)Sq, (int)Sk, scale, {}, 1);
+    return check_launch(who);
 }
 
 extern "C" clk_status clk_attention_fwd_gated(hipStream_t stream, clk_dtype dtype, const void* q,

@@ -12,8 +12,9 @@
  * the XLA FFI handlers pass them through unchanged.
  *
  * Layouts (all row-major, contiguous):
- *   attention  q, out [N,H,Sq,D]; k, v [N,H,Sk,D]; bias [H,Sq,Sk] shared by the N rows;
- *              kmask [N,Sk] uint8 (0 = key absent); lse [N,H,Sq] float32 (natural log)
+ *   attention  q, out [N,H,Sq,D]; k, v [N,H,Sk,D] (clk_attention_fwd_nshd: [N,Sq,H,D],
+ *              [N,Sk,H,D]); bias [H,Sq,Sk] shared by the N rows; kmask [N,Sk] uint8
+ *              (0 = key absent); lse [N,H,Sq] float32 (natural log)
  *   layer norm x, y [M,C]; scale, offset [C] float32
  *   gdp        x [M,K]; wp, wg [K,N]; bp, bg [N]; mask [M]; out [M,N]
  */
@@ -73,6 +74,20 @@ clk_status clk_attention_fwd(hipStream_t stream, clk_dtype dtype, const void* q,
                              const void* v, const void* bias, const uint8_t* kmask, void* out,
                              float* lse, int64_t N, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
                              float scale, int64_t block_q, int64_t block_k);
+
+/*
+ * Attention forward on AlphaFold's own [N, S, H, D] layout: q [N, Sq, H, D], k and v
+ * [N, Sk, H, D], out [N, Sq, H, D] (contiguous), so a caller need not transpose them to the
+ * [N, H, S, D] layout of VoltaMma first (the jnp caller does, around
+ * cuda/volta_mma_attn.cu:304-351; four passes over the operands). bias [H, Sq, Sk], kmask
+ * [N, Sk], lse [N, H, Sq] (may be NULL), dtype, D and scale as in clk_attention_fwd, and the
+ * same kernel, so O and lse are bit-identical to clk_attention_fwd on the transposed operands.
+ * S*H*D*2 must stay below 2^31 bytes.
+ */
+clk_status clk_attention_fwd_nshd(hipStream_t stream, clk_dtype dtype, const void* q,
+                                  const void* k, const void* v, const void* bias,
+                                  const uint8_t* kmask, void* out, float* lse, int64_t N,
+                                  int64_t H, int64_t Sq, int64_t Sk, int64_t D, float scale);
 
 /*
  * Attention forward with the output gate fused into its epilogue: the reference's epilogue

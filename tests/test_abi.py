@@ -76,6 +76,25 @@ def test_attention_fwd_validation(kw, msg):
     assert msg in _native.last_error()
 
 
+def attn_fwd_nshd(**kw):
+    a = dict(stream=None, dtype=BF16, q=FAKE, k=FAKE, v=FAKE, bias=FAKE, kmask=FAKE, out=FAKE,
+             lse=None, N=2, H=2, Sq=16, Sk=16, D=32, scale=0.17)
+    a.update(kw)
+    return _native.lib().clk_attention_fwd_nshd(*a.values())
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(D=24), "head dim"), (dict(dtype=F32), "dtype"), (dict(N=-1), "negative"),
+    (dict(q=None), "null"), (dict(v=FAKE + 8), "aligned"),
+    # [N,S,H,D] rows of one (n, h) lie H*D apart: S*H*D*2 must fit 31 bits.
+    (dict(H=4096, Sq=8192, Sk=8192, D=64), "[N,S,H,D]"),
+])
+def test_attention_fwd_nshd_validation(kw, msg):
+    assert attn_fwd_nshd(**kw) == INVALID
+    assert msg in _native.last_error()
+    assert attn_fwd_nshd(N=0) == _native.OK
+
+
 def test_attention_fwd_empty_is_ok():
     assert attn_fwd(N=0) == _native.OK
     assert attn_fwd(Sq=0) == _native.OK

@@ -54,6 +54,35 @@ def test_attention_fwd_parity(cuda, case, dtype):
     assert torch.equal(out, out2)
 
 
+# (N, H, Sq, Sk, D, masked_tail, masked_rows): every head dim, one- and two-sub-tile query
+# blocks, the bias-tile and element-wise paths (Sk % 8), a padding tail, rows with no key, H = 1.
+NSHD_CASES = [(3, 4, 100, 77, 32, 0.1, 1), (2, 2, 64, 384, 32, 0.2, 1),
+              (2, 3, 130, 200, 64, 0.0, 0), (2, 4, 48, 40, 8, 0.1, 0), (2, 2, 33, 136, 16, 0.0, 1),
+              (4, 1, 70, 96, 32, 0.5, 0)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=dname)
+@pytest.mark.parametrize("case", NSHD_CASES, ids=lambda c: "x".join(map(str, c[:5])))
+def test_attention_fwd_nshd_layout(cuda, case, dtype):
+    """The [N,S,H,D] entry runs the same kernel with rows H*D apart: O (in [N,S,H,D]) and lse
+    are bit-identical to the [N,H,S,D] entry on the transposed operands, and match the oracle."""
+    n, h, sq, sk, d, tail, rows = case
+    inp = attention_inputs(n, h, sq, sk, d, dtype, seed=sq * 5 + sk + d, bias_var=1.0,
+                           masked_tail=tail, masked_rows=rows, with_dout=False)
+    g = {k: (v.to(cuda) if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    out, lse = ops.attention_fwd(g["q"], g["k"], g["v"], g["bias"], g["kmask"], g["scale"])
+    t = lambda x: x.transpose(1, 2).contiguous()  # [N,H,S,D] <-> [N,S,H,D]
+    out_s, lse_s = ops.attention_nshd(t(g["q"]), t(g["k"]), t(g["v"]), g["bias"], g["kmask"],
+                                      g["scale"], want_lse=True)
+    assert out_s.shape == (n, sq, h, d)
+    assert torch.equal(t(out_s), out)
+    assert torch.equal(lse_s, lse)
+    assert_close("O", t(out_s), _oracle(inp)[0], TOL[dname(dtype)]["o"])
+    out_n, lse_n = ops.attention_nshd(t(g["q"]), t(g["k"]), t(g["v"]), g["bias"], g["kmask"],
+                                      g["scale"])
+    assert lse_n is None and torch.equal(out_n, out_s)
+
+
 # (N, H, Sq, Sk, D): whole and ragged key tiles, the element-wise mask path (Sk % 8 != 0).
 MIXED_MASK_SHAPES = [(8, 2, 70, 200, 32), (6, 2, 64, 77, 32), (6, 2, 40, 456, 16),
                      (4, 1, 130, 384, 64), (5, 2, 64, 136, 8)]
