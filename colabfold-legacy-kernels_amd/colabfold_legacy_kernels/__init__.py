@@ -44,6 +44,7 @@ _TABLE = {
     "ln_gated_dual_proj": ((_ARCH, _LIB, "ClkLnGdp"),),
     "attention_gate": ((_ARCH, _LIB, "ClkAttentionGate"),),
     "attention_gated": ((_ARCH, _LIB, "ClkAttentionGated"),),
+    "attention_nshd": ((_ARCH, _LIB, "ClkAttentionNshd"),),
     "ln_pair_bias": ((_ARCH, _LIB, "ClkLnPairBias"),),
     "gated_dual_proj_bwd": ((_ARCH, _LIB, "ClkGdpBwd"),),
     "triangle_multiply": ((_ARCH, _LIB, "ClkTriangleMultiply"),),

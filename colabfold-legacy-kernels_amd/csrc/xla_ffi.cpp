@@ -13,6 +13,8 @@
 //       x, wp, bp, wg, bg, mask -> out
 // and accept bf16 as well as f16. Targets without a reference counterpart:
 //   ClkAttentionFwd   q, k, v, bias, kmask -> out, lse (f32 [N,H,Sq]); attribute scale
+//   ClkAttentionNshd  q [N,Sq,H,D], k, v [N,Sk,H,D], bias, kmask -> out [N,Sq,H,D] (AlphaFold's
+//                     layout, no transposes); attribute scale
 //   ClkAttentionGated q, k, v, bias, kmask, x [N,Sq,C], wg [C,H*D], bg [H*D] -> gated
 //                     [N,Sq,H*D] (attention with the output gate fused in); attribute scale
 //   ClkAttentionBwd   q, k, v, bias, kmask, out, dout, lse -> dq, dk, dv, dbias (f32 [H,Sq,Sk]),
@@ -212,6 +214,32 @@ clk_status attention_fwd(const char* who, const Frame& f, bool with_lse) {
                              f.arg(1)->data, f.arg(2)->data, f.arg(3)->data,
                              static_cast<const uint8_t*>(f.arg(4)->data), out->data, lse, d.N,
                              d.H, d.Sq, d.Sk, d.D, scale, bq, bk);
+}
+
+clk_status attention_nshd(const Frame& f) {
+    const char* who = "ClkAttentionNshd";
+    if (f.nargs() != 5 || f.nrets() != 1)
+        return bad(who, "expects 5 operands (q, k, v, bias, kmask) and 1 result");
+    const Buffer *q = f.arg(0), *k = f.arg(1), *v = f.arg(2), *bias = f.arg(3), *km = f.arg(4);
+    const Buffer* out = f.ret(0);
+    if (!q || !k || !v || !bias || !km || !out) return bad(who, "operands must be buffers");
+    if (q->rank != 4 || k->rank != 4) return bad(who, "q and k must be [N,S,H,D]");
+    const int64_t N = q->dims[0], Sq = q->dims[1], H = q->dims[2], D = q->dims[3];
+    const int64_t Sk = k->dims[1];
+    if (!dims_are(k, {N, Sk, H, D}) || !dims_are(v, {N, Sk, H, D}))
+        return bad(who, "k and v must be [N,Sk,H,D] matching q");
+    if (!dims_are(bias, {H, Sq, Sk})) return bad(who, "bias must be [H,Sq,Sk]");
+    if (!dims_are(km, {N, Sk}) || km->dtype != kU8) return bad(who, "kmask must be u8 [N,Sk]");
+    if (!half_type(q->dtype) || k->dtype != q->dtype || v->dtype != q->dtype ||
+        bias->dtype != q->dtype)
+        return bad(who, "q, k, v and bias must all be f16 or all bf16");
+    if (!dims_are(out, {N, Sq, H, D}) || out->dtype != q->dtype)
+        return bad(who, "result must be [N,Sq,H,D] of the input dtype");
+    float scale = 0.f;
+    if (!f.attr_f32("scale", &scale)) return bad(who, "missing f32 attribute 'scale'");
+    return clk_attention_fwd_nshd(f.stream(), static_cast<clk_dtype>(q->dtype), q->data, k->data,
+                                  v->data, bias->data, static_cast<const uint8_t*>(km->data),
+                                  out->data, nullptr, N, H, Sq, Sk, D, scale);
 }
 
 clk_status attention_gated(const Frame& f) {
@@ -494,6 +522,9 @@ CLK_FFI_EXPORT Error* VoltaWmma(CallFrame* frame) {
 }
 CLK_FFI_EXPORT Error* ClkAttentionFwd(CallFrame* frame) {
     return run(frame, [](const Frame& f) { return attention_fwd("ClkAttentionFwd", f, true); });
+}
+CLK_FFI_EXPORT Error* ClkAttentionNshd(CallFrame* frame) {
+    return run(frame, [](const Frame& f) { return attention_nshd(f); });
 }
 CLK_FFI_EXPORT Error* ClkAttentionGated(CallFrame* frame) {
     return run(frame, [](const Frame& f) { return attention_gated(f); });

@@ -13,7 +13,8 @@ pytestmark = pytest.mark.skipif(not clk.available("gfx950"), reason="library not
 
 TARGETS = ["VoltaMma", "VoltaWmma", "ClkAttentionFwd", "ClkAttentionBwd", "VoltaLayerNorm",
            "ClkLayerNormBwd", "VoltaGdp", "VoltaGdpWmma", "ClkLnGdp", "ClkAttentionGate",
-           "ClkAttentionGated", "ClkLnPairBias", "ClkGdpBwd", "ClkTriangleMultiply"]
+           "ClkAttentionGated", "ClkAttentionNshd", "ClkLnPairBias", "ClkGdpBwd",
+           "ClkTriangleMultiply"]
 FAKE = 0x100000
 
 
@@ -183,3 +184,29 @@ def test_stream_get_failure_fails_the_call(lib, name):
     err = x.call(lib, name, fr)
     assert err == 0xE5
     assert x.stream_gets == 1 and x.errors == []
+
+
+def test_attention_nshd_decode_errors(lib):
+    """ClkAttentionNshd: q, k, v and the result in [N,S,H,D]; every shape and dtype checked on the
+    host before the C ABI is called."""
+    x = FakeXla()
+    q = x.buffer(BF16, (2, 16, 8, 32), FAKE)      # [N, Sq, H, D]
+    kv = x.buffer(BF16, (2, 24, 8, 32), FAKE)     # [N, Sk, H, D]
+    bias, km = x.buffer(BF16, (8, 16, 24), FAKE), x.buffer(U8, (2, 24), FAKE)
+    res = [x.buffer(BF16, (2, 16, 8, 32), FAKE)]
+    scale = [("scale", F32, 0.17)]
+    cases = [
+        ([q, kv, kv, bias], res, scale, "5 operands"),
+        ([q, x.buffer(BF16, (2, 24, 4, 32), FAKE), kv, bias, km], res, scale, "[N,Sk,H,D]"),
+        ([q, kv, kv, x.buffer(BF16, (8, 24, 16), FAKE), km], res, scale, "bias"),
+        ([q, kv, kv, bias, x.buffer(BF16, (2, 24), FAKE)], res, scale, "kmask"),
+        ([q, kv, kv, bias, km], [x.buffer(BF16, (2, 8, 16, 32), FAKE)], scale, "result"),
+        ([q, kv, kv, bias, km], res, [], "scale"),
+        ([x.buffer(F32, (2, 16, 8, 32), FAKE), kv, kv, bias, km], res, scale, "f16 or all bf16"),
+        ([x.buffer(BF16, (2, 16, 8, 24), FAKE), x.buffer(BF16, (2, 24, 8, 24), FAKE),
+          x.buffer(BF16, (2, 24, 8, 24), FAKE), bias, km], [x.buffer(BF16, (2, 16, 8, 24), FAKE)],
+         scale, "head dim"),
+    ]
+    for args, rets, attrs, msg in cases:
+        assert x.call(lib, "ClkAttentionNshd", x.frame(args, rets, attrs)) is not None, msg
+        assert msg in x.errors[-1][1], (msg, x.errors[-1][1])

@@ -129,8 +129,8 @@ def test_layer_norm_and_gdp_targets(cuda):
 
 
 def test_new_targets_match_the_c_abi(cuda):
-    """ClkAttentionGate, ClkAttentionGated, ClkLnPairBias, ClkGdpBwd and ClkTriangleMultiply on
-    device buffers."""
+    """ClkAttentionGate, ClkAttentionGated, ClkAttentionNshd, ClkLnPairBias, ClkGdpBwd and
+    ClkTriangleMultiply on device buffers."""
     lib, x = lib_and_runtime(cuda)
     g = torch.Generator().manual_seed(21)
     bf = lambda *s, std=1.0: (torch.randn(s, generator=g) * std).to(torch.bfloat16).to(cuda)  # noqa
@@ -151,6 +151,15 @@ def test_new_targets_match_the_c_abi(cuda):
     assert x.call(lib, "ClkAttentionGated", fr) is None, x.errors
     torch.cuda.synchronize()
     assert torch.equal(gated, ops.attention_gated(q, k, v, ab, km, xin, wgt, bgt, 0.17))
+
+    qs, ks, vs = (t.transpose(1, 2).contiguous() for t in (q, k, v))  # [N, S, H, D]
+    outs = torch.empty_like(qs)
+    fr = x.frame([buf(x, t) for t in (qs, ks, vs, ab, km)], [buf(x, outs)],
+                 [("scale", F32, 0.17)])
+    assert x.call(lib, "ClkAttentionNshd", fr) is None, x.errors
+    torch.cuda.synchronize()
+    assert torch.equal(outs, ops.attention_nshd(qs, ks, vs, ab, km, 0.17)[0])
+    assert torch.equal(outs.transpose(1, 2), ops.attention(q, k, v, ab, km, 0.17))
 
     z, sc, of, w = bf(16, 24, 128), f32(128, base=1.0), f32(128), bf(128, 4, std=1 / 11.3)
     bias = torch.empty((4, 16, 24), dtype=torch.bfloat16, device=cuda)
