@@ -8,7 +8,8 @@ import pytest
 import torch
 
 from colabfold_legacy_kernels import ops
-from colabfold_legacy_kernels.workloads import attention_inputs, gdp_weights, layer_norm_inputs
+from colabfold_legacy_kernels.workloads import (attention_inputs, gate_inputs, gdp_weights,
+                                                layer_norm_inputs)
 from test_gpu_triangle import module_case
 
 pytestmark = pytest.mark.gpu
@@ -47,6 +48,29 @@ def test_attention_fwd_bwd_graph(cuda):
     def step():
         out, lse = ops.attention_fwd(q, k, v, bias, km, s)
         return out, lse, ops.attention_bwd(q, k, v, bias, km, out, dout, lse, s)
+
+    _check_replays(step)
+
+
+def test_attention_layouts_gates_and_pair_bias_graph(cuda):
+    """The [N,S,H,D] forward, the forward with the gate fused, the separate gate and the
+    pair-bias projection."""
+    inp = attention_inputs(2, 4, 70, 96, 32, torch.bfloat16, seed=23, device=cuda,
+                           masked_tail=0.1, masked_rows=1, with_dout=False)
+    q, k, v, bias, km, s = (inp[n] for n in ("q", "k", "v", "bias", "kmask", "scale"))
+    qs, ks, vs = (t.transpose(1, 2).contiguous() for t in (q, k, v))
+    x, wg, bg = gate_inputs(2, 70, 128, 4 * 32, torch.bfloat16, seed=24, device=cuda)
+    g = torch.Generator().manual_seed(25)
+    z = torch.randn((16, 24, 128), generator=g).to(torch.bfloat16).to(cuda)
+    sc = (1.0 + 0.1 * torch.randn(128, generator=g)).to(cuda)
+    of = (0.1 * torch.randn(128, generator=g)).to(cuda)
+    w = (torch.randn((128, 4), generator=g) / 11.3).to(torch.bfloat16).to(cuda)
+
+    def step():
+        o = ops.attention(q, k, v, bias, km, s)
+        return (ops.attention_nshd(qs, ks, vs, bias, km, s, want_lse=True),
+                ops.attention_gated(q, k, v, bias, km, x, wg, bg, s),
+                ops.attention_gate(o, x, wg, bg), ops.ln_pair_bias(z, sc, of, w))
 
     _check_replays(step)
 
