@@ -589,7 +589,8 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
         if constexpr (VEC) {
             // Queries past Sq and keys past Sk read zeros. Mask rows are 8-byte aligned (VEC).
             char* ex = qd + 3 * QB;
-            if (wave == 0) buf_dma4(buffer_rsrc(lse + nh * Sq, (uint32_t)Sq * 4), lane * 4, q0 * 4, ex);
+            if (wave == 0)
+                buf_dma4(buffer_rsrc(lse + nh * Sq, (uint32_t)Sq * 4), lane * 4, q0 * 4, ex);
             // Words kbeg/64 .. of the row's presence bits (kbeg % 64 == 0); words past the row
             // read zeros.
             const int words = (Sk + 63) >> 6;
@@ -652,14 +653,16 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
             const char* ex = qdc + 3 * QB;
 #pragma unroll
             for (int qt = 0; qt < QTW; ++qt)
-                lse2c[qt] = qrow[qt] < Sq
-                                ? reinterpret_cast<const float*>(ex)[16 * QTW * qg + 16 * qt + r16] * kLog2e
-                                : INFINITY;
+                lse2c[qt] =
+                    qrow[qt] < Sq
+                        ? reinterpret_cast<const float*>(ex)[16 * QTW * qg + 16 * qt + r16] * kLog2e
+                        : INFINITY;
             if (kmask) {
                 // Chunk i's 32 keys start at bit rel % 64 of staged word rel / 64 (rel = key
                 // offset in the range, a multiple of 32); the lane's 8 keys are bits 8g .. 8g+7
                 // of that. The word's address is the same in every lane (an LDS broadcast).
-                const unsigned long long* wd = reinterpret_cast<const unsigned long long*>(ex + 256);
+                const unsigned long long* wd =
+                    reinterpret_cast<const unsigned long long*>(ex + 256);
 #pragma unroll
                 for (int i = 0; i < KCW; ++i) {
                     const int rel = 32 * (i * KQ + kq);
@@ -745,7 +748,8 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
                     const int row = c0 + 8 * (r16 >> 2) + 4 * t + (r16 & 3);
-                    if constexpr (CHUNKS != kChunksEmpty) kf[t] = swz_row_operand<V8, D>(kvc, row, 0, g);
+                    if constexpr (CHUNKS != kChunksEmpty)
+                        kf[t] = swz_row_operand<V8, D>(kvc, row, 0, g);
                     vf[t] = swz_row_operand<V8, D>(kvc + KVB, row, 0, g);
                 }
                 f32x4 s[QTW][2], dp[QTW][2];
@@ -755,7 +759,8 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
                     for (int qt = 0; qt < QTW; ++qt) {
                         if constexpr (CHUNKS != kChunksEmpty)
                             s[qt][t] = TR::mfma(kf[t], qf[qt], bacc[i][qt][t]);
-                        dp[qt][t] = TR::mfma(vf[t], dof[qt], f32x4{-di[qt], -di[qt], -di[qt], -di[qt]});
+                        dp[qt][t] =
+                            TR::mfma(vf[t], dof[qt], f32x4{-di[qt], -di[qt], -di[qt], -di[qt]});
                     }
                 // The chunk's VALU work (exponentials, dS, the dBias sums) runs at a raised wave
                 // priority until its dQ MFMAs are issued: the other wave on the SIMD then gets
@@ -806,7 +811,8 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
                 for (int dt = 0; dt < DT; ++dt) {
                     const V8 kt = swz_tr_operand<V8, D>(kvc, c0, dt, r16, g);
 #pragma unroll
-                    for (int qt = 0; qt < QTW; ++qt) dqa[qt][dt] = TR::mfma(kt, dsf[qt], dqa[qt][dt]);
+                    for (int qt = 0; qt < QTW; ++qt)
+                        dqa[qt][dt] = TR::mfma(kt, dsf[qt], dqa[qt][dt]);
                 }
                 __builtin_amdgcn_s_setprio(0);
             }
@@ -825,7 +831,8 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
 #pragma unroll
         for (int qt = 0; qt < QTW; ++qt)
 #pragma unroll
-            for (int dt = 0; dt < DT; ++dt) xch[((wave * QTW + qt) * DT + dt) * 64 + lane] = dqa[qt][dt];
+            for (int dt = 0; dt < DT; ++dt)
+                xch[((wave * QTW + qt) * DT + dt) * 64 + lane] = dqa[qt][dt];
         lds_barrier();  // the exchange is LDS only
         if (kq < QTW * DT) {
             const int qt = kq / DT, dt = kq % DT;
