@@ -41,6 +41,10 @@ PROTOTYPES = {
                                   c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                                   c_void_p, c_void_p, c_void_p, c_size, c_i64, c_i64, c_i64,
                                   c_i64, c_i64, c_f32]),
+    "clk_attention_bwd_nshd": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                                       c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                       c_void_p, c_void_p, c_void_p, c_void_p, c_size, c_i64,
+                                       c_i64, c_i64, c_i64, c_i64, c_f32]),
     "clk_attention_bwd_noalloc_limit": (c_size, []),
     "clk_attention_bwd_noalloc": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p,
                                           c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,

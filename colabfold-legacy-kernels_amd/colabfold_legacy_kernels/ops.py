@@ -195,6 +195,38 @@ def attention_bwd(q, k, v, bias, kmask, out, dout, lse, scale=None):
     return dq, dk, dv, dbias
 
 
+def attention_bwd_nshd(q, k, v, bias, kmask, out, dout, lse, scale=None):
+    """attention_bwd on AlphaFold's [N,S,H,D] layout: q, out, dout [N,Sq,H,D], k, v [N,Sk,H,D],
+    lse [N,H,Sq]; returns (dq, dk, dv) in the layout of q, k, v and dbias [H,Sq,Sk] float32,
+    bit-identical to attention_bwd on the [N,H,S,D] transposes."""
+    what = "attention_bwd_nshd"
+    dev = _require([("q", q), ("k", k), ("v", v), ("bias", bias), ("kmask", kmask),
+                    ("out", out), ("dout", dout), ("lse", lse)], what)
+    _shape_check(q.dim() == 4 and k.dim() == 4, what, "q and k must be [N,S,H,D]")
+    n, h, sq, sk, d = _attn_dims(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), bias,
+                                 kmask, what)
+    code = _dtype_code(q, (_native.F16, _native.BF16), what)
+    _shape_check(tuple(out.shape) == tuple(q.shape) and out.dtype == q.dtype, what,
+                 "out must match q")
+    _shape_check(tuple(dout.shape) == tuple(q.shape) and dout.dtype == q.dtype, what,
+                 "dout must match q")
+    _shape_check(tuple(lse.shape) == (n, h, sq) and lse.dtype == torch.float32, what,
+                 "lse must be float32 [N,H,Sq]")
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    lib = _native.lib()
+    ws_bytes = lib.clk_attention_bwd_workspace_size(n, h, sq, sk, d)
+    ws = torch.empty(max(ws_bytes, 1), device=dev, dtype=torch.uint8)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dbias = torch.empty((h, sq, sk), device=dev, dtype=torch.float32)
+    with torch.cuda.device(dev):
+        _check(lib.clk_attention_bwd_nshd(_stream(dev), code, _ptr(q), _ptr(k), _ptr(v),
+                                          _ptr(bias), _ptr(kmask), _ptr(out), _ptr(dout),
+                                          _ptr(lse), _ptr(dq), _ptr(dk), _ptr(dv), _ptr(dbias),
+                                          _ptr(ws), ws_bytes, n, h, sq, sk, d, float(scale)))
+    return dq, dk, dv, dbias
+
+
 def _ln_dims(x, scale, what):
     _shape_check(x.dim() >= 1, what, "x must have at least one axis")
     c = x.shape[-1]

@@ -32,10 +32,13 @@ constexpr int kRowsClean = 0, kRowsEmpty = 1, kRowsMixed = 2;
 constexpr int kChunksClean = 0, kChunksSelect = 1, kChunksEmpty = 2;
 
 
-template <typename TR, int D>
+// D_i = rowsum(dO * O) for every query row (rows in the operands' order; with NSHD the
+// [N, S, H] order, written to di in the [N, H, S] order).
+template <typename TR, int D, bool NSHD>
 __global__ __launch_bounds__(256) void attn_bwd_dot(const typename TR::elem* __restrict__ out,
                                                     const typename TR::elem* __restrict__ dout,
-                                                    float* __restrict__ di, int64_t rows) {
+                                                    float* __restrict__ di, int64_t rows, int H,
+                                                    int Sq) {
     constexpr int LPR = D / 8;
     const int64_t gid = (int64_t)blockIdx.x * 256 + threadIdx.x;
     const int64_t row = gid / LPR;
@@ -49,10 +52,17 @@ __global__ __launch_bounds__(256) void attn_bwd_dot(const typename TR::elem* __r
         for (int j = 0; j < 8; ++j) s += o[j] * d[j];
     }
     s = group_sum<LPR>(s);
-    if (row < rows && part == 0) di[row] = s;
+    if (row < rows && part == 0) {
+        int64_t at = row;
+        if constexpr (NSHD) {  // row = (n*Sq + q)*H + h
+            const int64_t hh = row % H, nq = row / H;
+            at = (nq / Sq * H + hh) * Sq + nq % Sq;
+        }
+        di[at] = s;
+    }
 }
 
-template <typename TR, int D, int KT>
+template <typename TR, int D, int KT, bool NSHD>
 __global__ __launch_bounds__(256) void attn_bwd_dq(
     const typename TR::elem* __restrict__ q, const typename TR::elem* __restrict__ k,
     const typename TR::elem* __restrict__ v, const typename TR::elem* __restrict__ bias,
@@ -93,10 +103,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dq(
     RowTileStager<E, D, 2> stage;
     E* const dst[2] = {k_lds, v_lds};
     const int lds_ld[2] = {LD, LD};
+    using HR = HeadRows<D, NSHD>;
     auto load_tile = [&](int n, int kstart) {
-        const size_t base = ((size_t)n * H + h) * Sk * D;
+        const size_t base = HR::at(n, h, 0, Sk, H);
         const E* src[2] = {k + base, v + base};
-        stage.load(src, kstart, kend);
+        stage.load(src, kstart, kend, HR::ld(H));
     };
     if (n0 < n1) load_tile(n0, kbeg);
 
@@ -108,8 +119,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq(
             const int d0 = ks * 32 + g * 8;
             u32x4 rq = {0u, 0u, 0u, 0u}, rd = {0u, 0u, 0u, 0u};
             if (qin && d0 < D) {
-                rq = ld16(q + (nh * Sq + qrow) * D + d0);
-                rd = ld16(dout + (nh * Sq + qrow) * D + d0);
+                rq = ld16(q + HR::at(n, h, qrow, Sq, H) + d0);
+                rd = ld16(dout + HR::at(n, h, qrow, Sq, H) + d0);
             }
             qf[ks] = bits_as<V8>(rq);
             dof[ks] = bits_as<V8>(rd);
@@ -196,10 +207,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dq(
                 const int d = 16 * dt + 4 * g;
                 if (d < D) {
                     if (nranges == 1) {
-                        store4<TR>(dq + (nh * Sq + qrow) * D + d, dq_acc[dt] * scale);
-                    } else {
-                        float* o = dq_part + (((size_t)range * N + n) * H + h) * Sq * D +
-                                   (size_t)qrow * D + d;
+                        store4<TR>(dq + HR::at(n, h, qrow, Sq, H) + d, dq_acc[dt] * scale);
+                    } else {  // range's partial, in dq's layout
+                        float* o = dq_part + (size_t)range * N * H * Sq * D +
+                                   HR::at(n, h, qrow, Sq, H) + d;
                         *reinterpret_cast<f32x4*>(o) = dq_acc[dt] * scale;
                     }
                 }
@@ -231,7 +242,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq(
     }
 }
 
-template <typename TR, int D>
+template <typename TR, int D, bool NSHD>
 __global__ __launch_bounds__(256) void attn_bwd_dkv(
     const typename TR::elem* __restrict__ q, const typename TR::elem* __restrict__ k,
     const typename TR::elem* __restrict__ v, const typename TR::elem* __restrict__ bias,
@@ -255,6 +266,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv(
     const int r16 = lane & 15, g = lane >> 4;
     const int k0 = blockIdx.x * 64, h = blockIdx.y, n = blockIdx.z;
     const size_t nh = (size_t)n * H + h;
+    using HR = HeadRows<D, NSHD>;
     const int key = k0 + wave * 16 + r16;
     const bool kin = key < Sk;
 
@@ -264,8 +276,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv(
         const int d0 = ks * 32 + g * 8;
         u32x4 rk = {0u, 0u, 0u, 0u}, rv = {0u, 0u, 0u, 0u};
         if (kin && d0 < D) {
-            rk = ld16(k + (nh * Sk + key) * D + d0);
-            rv = ld16(v + (nh * Sk + key) * D + d0);
+            rk = ld16(k + HR::at(n, h, key, Sk, H) + d0);
+            rv = ld16(v + HR::at(n, h, key, Sk, H) + d0);
         }
         kf[ks] = bits_as<V8>(rk);
         vf[ks] = bits_as<V8>(rv);
@@ -288,7 +300,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv(
     RowTileStager<E, D, 2> stage;
     E* const dst[2] = {q_lds, do_lds};
     const int lds_ld[2] = {LD, LD};
-    const E* src[2] = {q + nh * Sq * D, dout + nh * Sq * D};
+    const E* src[2] = {q + HR::at(n, h, 0, Sq, H), dout + HR::at(n, h, 0, Sq, H)};
 
     // Bias tile [64 queries][64 keys]: two 16-byte chunks per thread.
     u32x4 breg[2];
@@ -316,7 +328,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv(
 
     const int qtiles = (Sq + 63) / 64;
     if (qtiles > 0) {
-        stage.load(src, 0, Sq);
+        stage.load(src, 0, Sq, HR::ld(H));
         load_bias_tile(0);
     }
     for (int qt = 0; qt < qtiles; ++qt) {
@@ -335,7 +347,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv(
         }
         __syncthreads();
         if (qt + 1 < qtiles) {
-            stage.load(src, qs + 64, Sq);
+            stage.load(src, qs + 64, Sq, HR::ld(H));
             load_bias_tile(qs + 64);
         }
 
@@ -395,8 +407,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv(
     for (int dt = 0; dt < G::DT; ++dt) {
         const int d = 16 * dt + 4 * g;
         if (d < D) {
-            store4<TR>(dk + (nh * Sk + key) * D + d, dk_acc[dt] * scale);
-            store4<TR>(dv + (nh * Sk + key) * D + d, dv_acc[dt]);
+            store4<TR>(dk + HR::at(n, h, key, Sk, H) + d, dk_acc[dt] * scale);
+            store4<TR>(dv + HR::at(n, h, key, Sk, H) + d, dv_acc[dt]);
         }
     }
 }
@@ -488,7 +500,7 @@ __device__ void transpose_bias_tile(const typename TR::elem* __restrict__ bias,
 // accumulator input), dS, and dQ^T += K^T.dS^T. The four key-quarter waves of a query group
 // then add their dQ partials through LDS in a fixed order. Also writes lse*log2(e) and -D_i
 // per query for the column-owner pass.
-template <typename TR, int D, int KCW, bool VEC, int QG, int QTW>
+template <typename TR, int D, int KCW, bool VEC, int QG, int QTW, bool NSHD>
 __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
     const typename TR::elem* __restrict__ q, const typename TR::elem* __restrict__ k,
     const typename TR::elem* __restrict__ v, const typename TR::elem* __restrict__ bias,
@@ -580,12 +592,14 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
 
     auto stage = [&](int n, char* kv, char* qd) {
         const size_t nh = (size_t)n * H + h;
-        const uint32_t kb = (uint32_t)Sk * D * 2, qb = (uint32_t)Sq * D * 2;
-        stage_rows<D, RK, NT>(buffer_rsrc(k + nh * Sk * D, kb), kbeg, kv);
-        stage_rows<D, RK, NT>(buffer_rsrc(v + nh * Sk * D, kb), kbeg, kv + KVB);
-        stage_rows<D, BQ, NT>(buffer_rsrc(q + nh * Sq * D, qb), q0, qd);
-        stage_rows<D, BQ, NT>(buffer_rsrc(dout + nh * Sq * D, qb), q0, qd + QB);
-        stage_rows<D, BQ, NT>(buffer_rsrc(out + nh * Sq * D, qb), q0, qd + 2 * QB);
+        using HR = HeadRows<D, NSHD>;
+        const uint32_t kb = HR::bytes(Sk, H), qb = HR::bytes(Sq, H);
+        const size_t ko = HR::at(n, h, 0, Sk, H), qo = HR::at(n, h, 0, Sq, H);
+        stage_head_rows<D, RK, NT, NSHD>(buffer_rsrc(k + ko, kb), kbeg, H, kv);
+        stage_head_rows<D, RK, NT, NSHD>(buffer_rsrc(v + ko, kb), kbeg, H, kv + KVB);
+        stage_head_rows<D, BQ, NT, NSHD>(buffer_rsrc(q + qo, qb), q0, H, qd);
+        stage_head_rows<D, BQ, NT, NSHD>(buffer_rsrc(dout + qo, qb), q0, H, qd + QB);
+        stage_head_rows<D, BQ, NT, NSHD>(buffer_rsrc(out + qo, qb), q0, H, qd + 2 * QB);
         if constexpr (VEC) {
             // Queries past Sq and keys past Sk read zeros. Mask rows are 8-byte aligned (VEC).
             char* ex = qd + 3 * QB;
@@ -625,12 +639,11 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
         const int qt = min(kq / DT, QTW - 1), dt = kq % DT;  // pend_n >= 0: kq < QTW * DT
         const int d = 16 * dt + 4 * g;
         if (qrow[qt] < Sq && d < D) {
-            const size_t pnh = (size_t)pend_n * H + h;
+            const size_t at = HeadRows<D, NSHD>::at(pend_n, h, qrow[qt], Sq, H) + d;
             if (nranges == 1) {
-                store4<TR>(dq + (pnh * Sq + qrow[qt]) * D + d, pend_dq);
-            } else {
-                float* o = dq_part + (((size_t)range * N + pend_n) * H + h) * Sq * D +
-                           (size_t)qrow[qt] * D + d;
+                store4<TR>(dq + at, pend_dq);
+            } else {  // range's partial, in dq's layout
+                float* o = dq_part + (size_t)range * N * H * Sq * D + at;
                 *reinterpret_cast<f32x4*>(o) = pend_dq;
             }
         }
@@ -999,7 +1012,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
 // global->LDS loads into the other buffer while the current tile is computed (one barrier per
 // tile). Per 32-query chunk: S = Q.K^T and dP - D = dO.V^T with the queries permuted so that P
 // and dS are directly the B operands of dV^T += dO^T.P and dK^T += Q^T.dS.
-template <typename TR, int D, int KSUB, int NW, bool VEC>
+template <typename TR, int D, int KSUB, int NW, bool VEC, bool NSHD>
 __global__ __launch_bounds__(64 * NW) void attn_bwd_dkv2(
     const typename TR::elem* __restrict__ q, const typename TR::elem* __restrict__ k,
     const typename TR::elem* __restrict__ v, const typename TR::elem* __restrict__ bias_t,
@@ -1007,7 +1020,6 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkv2(
     const float* __restrict__ lse2, const float* __restrict__ ndi,
     const float* __restrict__ row_logit, typename TR::elem* __restrict__ dk,
     typename TR::elem* __restrict__ dv, int H, int Sq, int Sk, int SqP, float scale) {
-    using E = typename TR::elem;
     using V8 = typename TR::vec8;
     using T = SwzTile<D>;
     static_assert(D <= 32, "column-owner kernel holds one 32-dim k-slot group");
@@ -1031,6 +1043,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkv2(
     const int item = xcd_contiguous(blockIdx.x, gridDim.x);
     const int k0 = (item % kblocks) * KB, h = (item / kblocks) % H, n = item / (kblocks * H);
     const size_t nh = (size_t)n * H + h;
+    using HR = HeadRows<D, NSHD>;
     const int kw0 = k0 + wave * KW;
 
     // In a row with a present key an absent key's P is 0, so its dK and dV are 0: its lane (one
@@ -1046,8 +1059,8 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkv2(
         const bool kin = key < Sk;
         u32x4 rk = {0u, 0u, 0u, 0u}, rv = {0u, 0u, 0u, 0u};
         if (kin && 8 * g < D) {
-            rk = ld16(k + (nh * Sk + key) * D + 8 * g);
-            rv = ld16(v + (nh * Sk + key) * D + 8 * g);
+            rk = ld16(k + HR::at(n, h, key, Sk, H) + 8 * g);
+            rv = ld16(v + HR::at(n, h, key, Sk, H) + 8 * g);
         }
         kf[s] = bits_as<V8>(rk);
         vf[s] = bits_as<V8>(rv);
@@ -1067,9 +1080,9 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkv2(
             dva[s][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
 
-    const uint32_t qbytes = (uint32_t)Sq * D * 2;
-    const Rsrc rq = buffer_rsrc(q + nh * Sq * D, qbytes);
-    const Rsrc rdo = buffer_rsrc(dout + nh * Sq * D, qbytes);
+    const uint32_t qbytes = HR::bytes(Sq, H);
+    const Rsrc rq = buffer_rsrc(q + HR::at(n, h, 0, Sq, H), qbytes);
+    const Rsrc rdo = buffer_rsrc(dout + HR::at(n, h, 0, Sq, H), qbytes);
     // The block's transposed-bias rows (keys k0 .. k0+KB-1 that exist) and the two per-query
     // vectors of (n, h).
     const Rsrc rbt = buffer_rsrc(bias_t + ((size_t)h * Sk + k0) * SqP,
@@ -1077,8 +1090,8 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkv2(
     const Rsrc rl = buffer_rsrc(lse2 + nh * Sq, (uint32_t)Sq * 4);
     const Rsrc rn = buffer_rsrc(ndi + nh * Sq, (uint32_t)Sq * 4);
     auto stage = [&](int qs, char* qd, char* bt, float* st) {
-        stage_rows<D, 64, NT>(rq, qs, qd);
-        stage_rows<D, 64, NT>(rdo, qs, qd + QB);
+        stage_head_rows<D, 64, NT, NSHD>(rq, qs, H, qd);
+        stage_head_rows<D, 64, NT, NSHD>(rdo, qs, H, qd + QB);
         // bias^T rows k0 .. k0+KB-1, eight 16-byte pieces of 8 queries each, piece p of row r
         // at position p ^ (r & 7). Keys past Sk read zeros; SqP is a multiple of 64, so a tile
         // never runs past its row.
@@ -1188,8 +1201,8 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkv2(
             const int d = 16 * dt + 4 * g;
             if (d < D) {
                 const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                store4<TR>(dk + (nh * Sk + key) * D + d, zero ? z : dka[s][dt] * scale);
-                store4<TR>(dv + (nh * Sk + key) * D + d, zero ? z : dva[s][dt]);
+                store4<TR>(dk + HR::at(n, h, key, Sk, H) + d, zero ? z : dka[s][dt] * scale);
+                store4<TR>(dv + HR::at(n, h, key, Sk, H) + d, zero ? z : dva[s][dt]);
             }
         }
     }
@@ -1337,14 +1350,14 @@ BwdPlan plan_bwd(int64_t N, int64_t H, int64_t Sq, int64_t Sk, int64_t D) {
     return p;
 }
 
-template <typename TR, int D, int KT>
+template <typename TR, int D, int KT, bool NSHD>
 void launch_dq(hipStream_t st, dim3 grid, const void* q, const void* k, const void* v,
                const void* bias, const uint8_t* kmask, const void* dout, const float* lse,
                const float* di, void* dq, float* dq_part, float* dbias_dst, int N, int H, int Sq,
                int Sk, int NB, int nranges, float scale, int vec_ok) {
     using E = typename TR::elem;
     KernelTimer timer("attn_bwd_dq", st);
-    attn_bwd_dq<TR, D, KT><<<grid, 256, 0, st>>>(
+    attn_bwd_dq<TR, D, KT, NSHD><<<grid, 256, 0, st>>>(
         (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (const E*)dout, lse, di,
         (E*)dq, dq_part, dbias_dst, N, H, Sq, Sk, NB, nranges, scale, vec_ok);
 }
@@ -1371,7 +1384,7 @@ void finish_partials(hipStream_t st, const BwdPlan& p, float* dbias_part, float*
     }
 }
 
-template <typename TR, int D>
+template <typename TR, int D, bool NSHD>
 void run_bwd_v1(hipStream_t st, const BwdPlan& p, const void* q, const void* k, const void* v,
                 const void* bias, const uint8_t* kmask, const void* out, const void* dout,
                 const float* lse, void* dq, void* dk, void* dv, float* dbias, char* ws, int N,
@@ -1386,8 +1399,8 @@ void run_bwd_v1(hipStream_t st, const BwdPlan& p, const void* q, const void* k, 
     {
         const int64_t threads = rows * (D / 8);
         KernelTimer timer("attn_bwd_dot", st);
-        attn_bwd_dot<TR, D><<<(int)((threads + 255) / 256), 256, 0, st>>>(
-            (const E*)out, (const E*)dout, di, rows);
+        attn_bwd_dot<TR, D, NSHD><<<(int)((threads + 255) / 256), 256, 0, st>>>(
+            (const E*)out, (const E*)dout, di, rows, H, Sq);
     }
     {
         dim3 grid(ceil_div(Sq, 64), H, p.nchunks * p.nranges);
@@ -1395,7 +1408,7 @@ void run_bwd_v1(hipStream_t st, const BwdPlan& p, const void* q, const void* k, 
         switch (p.KT) {
 #define CLK_KT(KTV)                                                                              \
     case KTV:                                                                                    \
-        launch_dq<TR, D, KTV>(st, grid, q, k, v, bias, kmask, dout, lse, di, dq, dq_part,        \
+        launch_dq<TR, D, KTV, NSHD>(st, grid, q, k, v, bias, kmask, dout, lse, di, dq, dq_part,  \
                               dbias_dst, N, H, Sq, Sk, p.NB, p.nranges, scale, vec_ok);          \
         break;
             CLK_KT(2) CLK_KT(4) CLK_KT(6) CLK_KT(8)
@@ -1405,7 +1418,7 @@ void run_bwd_v1(hipStream_t st, const BwdPlan& p, const void* q, const void* k, 
     {
         dim3 grid(ceil_div(Sk, 64), H, N);
         KernelTimer timer("attn_bwd_dkv", st);
-        attn_bwd_dkv<TR, D><<<grid, 256, 0, st>>>((const E*)q, (const E*)k, (const E*)v,
+        attn_bwd_dkv<TR, D, NSHD><<<grid, 256, 0, st>>>((const E*)q, (const E*)k, (const E*)v,
                                                   (const E*)bias, kmask, (const E*)dout, lse, di,
                                                   (E*)dk, (E*)dv, H, Sq, Sk, scale, vec_ok);
     }
@@ -1413,7 +1426,7 @@ void run_bwd_v1(hipStream_t st, const BwdPlan& p, const void* q, const void* k, 
                         (size_t)rows * D);
 }
 
-template <typename TR, int D, int KCW, bool VEC>
+template <typename TR, int D, int KCW, bool VEC, bool NSHD>
 void launch_dq2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, const void* v,
                 const void* bias, const uint8_t* kmask, const void* out, const void* dout,
                 const float* lse, float* rowl, unsigned long long* mbits, float* lse2, float* ndi,
@@ -1423,14 +1436,14 @@ void launch_dq2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, 
     using S = DqShape<D>;
     const dim3 grid(ceil_div(Sq, S::BQ) * H * p.nchunks * p.nranges);
     KernelTimer timer("attn_bwd_dq", st);
-    attn_bwd_dq2<TR, D, KCW, VEC, S::QG, S::QTW><<<grid, 64 * 4 * S::QG, 0, st>>>(
+    attn_bwd_dq2<TR, D, KCW, VEC, S::QG, S::QTW, NSHD><<<grid, 64 * 4 * S::QG, 0, st>>>(
         (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (const E*)out,
         (const E*)dout, lse, rowl, mbits, lse2, ndi, (E*)dq, dq_part, dbias_dst, N, H, Sq, Sk, p.NB,
         p.nranges, scale, LogitForm::make(scale), (E*)bias_t, p.SqP, ceil_div(p.SqP, 64),
         ceil_div(Sk, 64));
 }
 
-template <typename TR, int D, int KSUB, int NW, bool VEC>
+template <typename TR, int D, int KSUB, int NW, bool VEC, bool NSHD>
 void launch_dkv2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, const void* v,
                  const void* bias_t, const uint8_t* kmask, const void* dout, const float* lse2,
                  const float* ndi, const float* rowl, void* dk, void* dv, int N, int H, int Sq,
@@ -1438,12 +1451,12 @@ void launch_dkv2(hipStream_t st, const BwdPlan& p, const void* q, const void* k,
     using E = typename TR::elem;
     const dim3 grid(ceil_div(Sk, 16 * KSUB * NW) * H * N);
     KernelTimer timer("attn_bwd_dkv", st);
-    attn_bwd_dkv2<TR, D, KSUB, NW, VEC><<<grid, 64 * NW, 0, st>>>(
+    attn_bwd_dkv2<TR, D, KSUB, NW, VEC, NSHD><<<grid, 64 * NW, 0, st>>>(
         (const E*)q, (const E*)k, (const E*)v, (const E*)bias_t, kmask, (const E*)dout, lse2,
         ndi, rowl, (E*)dk, (E*)dv, H, Sq, Sk, p.SqP, scale);
 }
 
-template <typename TR, int D, bool VEC>
+template <typename TR, int D, bool VEC, bool NSHD>
 void run_bwd_v2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, const void* v,
                 const void* bias, const uint8_t* kmask, const void* out, const void* dout,
                 const float* lse, void* dq, void* dk, void* dv, float* dbias, char* ws, int N,
@@ -1460,9 +1473,9 @@ void run_bwd_v2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, 
     switch (p.KCW) {
 #define CLK_KCW(V)                                                                               \
     case V:                                                                                      \
-        launch_dq2<TR, D, V, VEC>(st, p, q, k, v, bias, kmask, out, dout, lse, rowl, mbits,     \
-                                  lse2, ndi, dq, dq_part, dbias_dst, bias_t, N, H, Sq, Sk,       \
-                                  scale);                                                        \
+        launch_dq2<TR, D, V, VEC, NSHD>(st, p, q, k, v, bias, kmask, out, dout, lse, rowl,       \
+                                        mbits, lse2, ndi, dq, dq_part, dbias_dst, bias_t, N, H,  \
+                                        Sq, Sk, scale);                                          \
         break;
         CLK_KCW(1) CLK_KCW(2) CLK_KCW(3)
 #undef CLK_KCW
@@ -1470,8 +1483,8 @@ void run_bwd_v2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, 
     switch (p.KSUB * 100 + p.KNW) {
 #define CLK_KSUB(V, W)                                                                           \
     case V * 100 + W:                                                                            \
-        launch_dkv2<TR, D, V, W, VEC>(st, p, q, k, v, bias_t, kmask, dout, lse2, ndi, rowl, dk,  \
-                                      dv, N, H, Sq, Sk, scale);                                  \
+        launch_dkv2<TR, D, V, W, VEC, NSHD>(st, p, q, k, v, bias_t, kmask, dout, lse2, ndi,      \
+                                            rowl, dk, dv, N, H, Sq, Sk, scale);                  \
         break;
         CLK_KSUB(1, 8) CLK_KSUB(2, 4)
 #undef CLK_KSUB
@@ -1480,7 +1493,7 @@ void run_bwd_v2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, 
                         (size_t)N * H * Sq * D);
 }
 
-template <typename TR, int D>
+template <typename TR, int D, bool NSHD>
 void run_bwd(hipStream_t st, const BwdPlan& p, const void* q, const void* k, const void* v,
              const void* bias, const uint8_t* kmask, const void* out, const void* dout,
              const float* lse, void* dq, void* dk, void* dv, float* dbias, char* ws, int N,
@@ -1488,14 +1501,14 @@ void run_bwd(hipStream_t st, const BwdPlan& p, const void* q, const void* k, con
     if constexpr (D <= 32) {
         const bool vec = Sk % 8 == 0 && (reinterpret_cast<uintptr_t>(kmask) & 7u) == 0;
         if (vec)
-            run_bwd_v2<TR, D, true>(st, p, q, k, v, bias, kmask, out, dout, lse, dq, dk, dv,
-                                    dbias, ws, N, H, Sq, Sk, scale);
+            run_bwd_v2<TR, D, true, NSHD>(st, p, q, k, v, bias, kmask, out, dout, lse, dq, dk, dv,
+                                          dbias, ws, N, H, Sq, Sk, scale);
         else
-            run_bwd_v2<TR, D, false>(st, p, q, k, v, bias, kmask, out, dout, lse, dq, dk, dv,
-                                     dbias, ws, N, H, Sq, Sk, scale);
+            run_bwd_v2<TR, D, false, NSHD>(st, p, q, k, v, bias, kmask, out, dout, lse, dq, dk,
+                                           dv, dbias, ws, N, H, Sq, Sk, scale);
     } else {
-        run_bwd_v1<TR, D>(st, p, q, k, v, bias, kmask, out, dout, lse, dq, dk, dv, dbias, ws, N,
-                          H, Sq, Sk, scale);
+        run_bwd_v1<TR, D, NSHD>(st, p, q, k, v, bias, kmask, out, dout, lse, dq, dk, dv, dbias,
+                                ws, N, H, Sq, Sk, scale);
     }
 }
 
@@ -1519,12 +1532,17 @@ template <typename TR>
 void dispatch_bwd(hipStream_t st, int64_t D, const BwdPlan& p, const void* q, const void* k,
                   const void* v, const void* bias, const uint8_t* kmask, const void* out,
                   const void* dout, const float* lse, void* dq, void* dk, void* dv,
-                  float* dbias, char* ws, int N, int H, int Sq, int Sk, float scale) {
+                  float* dbias, char* ws, int N, int H, int Sq, int Sk, float scale,
+                  bool nshd = false) {
     switch (D) {
-#define CLK_D(DV)                                                                           \
-    case DV:                                                                                \
-        run_bwd<TR, DV>(st, p, q, k, v, bias, kmask, out, dout, lse, dq, dk, dv, dbias, ws, \
-                        N, H, Sq, Sk, scale);                                               \
+#define CLK_D(DV)                                                                               \
+    case DV:                                                                                    \
+        if (nshd)                                                                               \
+            run_bwd<TR, DV, true>(st, p, q, k, v, bias, kmask, out, dout, lse, dq, dk, dv,      \
+                                  dbias, ws, N, H, Sq, Sk, scale);                              \
+        else                                                                                    \
+            run_bwd<TR, DV, false>(st, p, q, k, v, bias, kmask, out, dout, lse, dq, dk, dv,     \
+                                   dbias, ws, N, H, Sq, Sk, scale);                             \
         break;
         CLK_D(8) CLK_D(16) CLK_D(32) CLK_D(64)
 #undef CLK_D
@@ -1542,6 +1560,53 @@ extern "C" size_t clk_attention_bwd_workspace_size(int64_t N, int64_t H, int64_t
     return plan_bwd(N, H, Sq, Sk, D).bytes;
 }
 
+namespace {
+
+// The backward entries share this body: nshd selects AlphaFold's [N, S, H, D] layout for q, k, v,
+// out, dout, dq, dk and dv (lse stays [N, H, Sq]).
+clk_status attention_bwd_entry(const char* who, hipStream_t stream, clk_dtype dtype,
+                               const void* q, const void* k, const void* v, const void* bias,
+                               const uint8_t* kmask, const void* out, const void* dout,
+                               const float* lse, void* dq, void* dk, void* dv, float* dbias,
+                               void* workspace, size_t workspace_bytes, int64_t N, int64_t H,
+                               int64_t Sq, int64_t Sk, int64_t D, float scale, bool nshd) {
+    clk_status s = validate_attention(who, dtype, N, H, Sq, Sk, D);
+    if (s != CLK_OK) return s;
+    // [N, S, H, D]: byte offsets within the rows of one (n, h) are 32-bit.
+    if (nshd && (Sq > Sk ? Sq : Sk) * H * D * 2 >= ((int64_t)1 << 31))
+        return fail(CLK_INVALID_ARGUMENT, "%s: S*H*D too large for the [N,S,H,D] layout", who);
+    const BwdPlan p = plan_bwd(N, H, Sq, Sk, D);
+    if (workspace_bytes < p.bytes)
+        return fail(CLK_INVALID_ARGUMENT, "%s: workspace %zu bytes, needs %zu", who,
+                    workspace_bytes, p.bytes);
+    if (N == 0 || H == 0 || Sq == 0 || Sk == 0) {
+        const bool need_b = H * Sq * Sk > 0, need_q = N * H * Sq > 0, need_k = N * H * Sk > 0;
+        if ((need_b && !dbias) || (need_q && !dq) || (need_k && (!dk || !dv)))
+            return fail(CLK_INVALID_ARGUMENT, "%s: null gradient pointer", who);
+        if (dtype == CLK_BF16) zero_grads<BF16>(stream, N, H, Sq, Sk, D, dq, dk, dv, dbias);
+        else zero_grads<F16>(stream, N, H, Sq, Sk, D, dq, dk, dv, dbias);
+        return check_launch(who);
+    }
+    if (!q || !k || !v || !bias || !out || !dout || !lse || !dq || !dk || !dv || !dbias ||
+        !workspace)
+        return fail(CLK_INVALID_ARGUMENT, "%s: null operand pointer", who);
+    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(bias) || !aligned16(out) ||
+        !aligned16(dout) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv) ||
+        !aligned16(dbias) || !aligned16(lse) || (reinterpret_cast<uintptr_t>(workspace) & 255u))
+        return fail(CLK_INVALID_ARGUMENT,
+                    "%s: operands must be 16-byte and workspace 256-byte aligned", who);
+    char* ws = static_cast<char*>(workspace);
+    if (dtype == CLK_BF16)
+        dispatch_bwd<BF16>(stream, D, p, q, k, v, bias, kmask, out, dout, lse, dq, dk, dv, dbias,
+                           ws, (int)N, (int)H, (int)Sq, (int)Sk, scale, nshd);
+    else
+        dispatch_bwd<F16>(stream, D, p, q, k, v, bias, kmask, out, dout, lse, dq, dk, dv, dbias,
+                          ws, (int)N, (int)H, (int)Sq, (int)Sk, scale, nshd);
+    return check_launch(who);
+}
+
+}  // namespace
+
 extern "C" clk_status clk_attention_bwd(hipStream_t stream, clk_dtype dtype, const void* q,
                                         const void* k, const void* v, const void* bias,
                                         const uint8_t* kmask, const void* out, const void* dout,
@@ -1549,34 +1614,19 @@ extern "C" clk_status clk_attention_bwd(hipStream_t stream, clk_dtype dtype, con
                                         float* dbias, void* workspace, size_t workspace_bytes,
                                         int64_t N, int64_t H, int64_t Sq, int64_t Sk, int64_t D,
                                         float scale) {
-    clk_status s = validate_attention("attention_bwd", dtype, N, H, Sq, Sk, D);
-    if (s != CLK_OK) return s;
-    const BwdPlan p = plan_bwd(N, H, Sq, Sk, D);
-    if (workspace_bytes < p.bytes)
-        return fail(CLK_INVALID_ARGUMENT, "attention_bwd: workspace %zu bytes, needs %zu",
-                    workspace_bytes, p.bytes);
-    if (N == 0 || H == 0 || Sq == 0 || Sk == 0) {
-        const bool need_b = H * Sq * Sk > 0, need_q = N * H * Sq > 0, need_k = N * H * Sk > 0;
-        if ((need_b && !dbias) || (need_q && !dq) || (need_k && (!dk || !dv)))
-            return fail(CLK_INVALID_ARGUMENT, "attention_bwd: null gradient pointer");
-        if (dtype == CLK_BF16) zero_grads<BF16>(stream, N, H, Sq, Sk, D, dq, dk, dv, dbias);
-        else zero_grads<F16>(stream, N, H, Sq, Sk, D, dq, dk, dv, dbias);
-        return check_launch("attention_bwd");
-    }
-    if (!q || !k || !v || !bias || !out || !dout || !lse || !dq || !dk || !dv || !dbias ||
-        !workspace)
-        return fail(CLK_INVALID_ARGUMENT, "attention_bwd: null operand pointer");
-    if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(bias) || !aligned16(out) ||
-        !aligned16(dout) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv) ||
-        !aligned16(dbias) || !aligned16(lse) || (reinterpret_cast<uintptr_t>(workspace) & 255u))
-        return fail(CLK_INVALID_ARGUMENT,
-                    "attention_bwd: operands must be 16-byte and workspace 256-byte aligned");
-    char* ws = static_cast<char*>(workspace);
-    if (dtype == CLK_BF16)
-        dispatch_bwd<BF16>(stream, D, p, q, k, v, bias, kmask, out, dout, lse, dq, dk, dv, dbias,
-                           ws, (int)N, (int)H, (int)Sq, (int)Sk, scale);
-    else
-        dispatch_bwd<F16>(stream, D, p, q, k, v, bias, kmask, out, dout, lse, dq, dk, dv, dbias,
-                          ws, (int)N, (int)H, (int)Sq, (int)Sk, scale);
-    return check_launch("attention_bwd");
+    return attention_bwd_entry("attention_bwd", stream, dtype, q, k, v, bias, kmask, out, dout,
+                               lse, dq, dk, dv, dbias, workspace, workspace_bytes, N, H, Sq, Sk,
+                               D, scale, false);
+}
+
+extern "C" clk_status clk_attention_bwd_nshd(hipStream_t stream, clk_dtype dtype, const void* q,
+                                             const void* k, const void* v, const void* bias,
+                                             const uint8_t* kmask, const void* out,
+                                             const void* dout, const float* lse, void* dq,
+                                             void* dk, void* dv, float* dbias, void* workspace,
+                                             size_t workspace_bytes, int64_t N, int64_t H,
+                                             int64_t Sq, int64_t Sk, int64_t D, float scale) {
+    return attention_bwd_entry("attention_bwd_nshd", stream, dtype, q, k, v, bias, kmask, out,
+                               dout, lse, dq, dk, dv, dbias, workspace, workspace_bytes, N, H, Sq,
+                               Sk, D, scale, true);
 }

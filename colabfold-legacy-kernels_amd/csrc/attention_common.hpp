@@ -64,7 +64,8 @@ struct RowTileStager {
     static constexpr int CPT = (CHUNKS + 255) / 256;
     u32x4 r[NOPS][CPT];
 
-    __device__ __forceinline__ void load(const E* const* src, int row0, int S) {
+    // Rows row0 .. row0+63 of each src (rows gld elements apart; rows past S read zeros).
+    __device__ __forceinline__ void load(const E* const* src, int row0, int S, int gld = D) {
 #pragma unroll
         for (int i = 0; i < CPT; ++i) {
             const int ch = threadIdx.x + 256 * i;
@@ -73,7 +74,7 @@ struct RowTileStager {
 #pragma unroll
             for (int o = 0; o < NOPS; ++o) {
                 r[o][i] = u32x4{0u, 0u, 0u, 0u};
-                if (in) r[o][i] = ld16(src[o] + (size_t)(row0 + row) * D + c8);
+                if (in) r[o][i] = ld16(src[o] + (size_t)(row0 + row) * gld + c8);
             }
         }
     }
@@ -231,6 +232,31 @@ __device__ __forceinline__ void stage_rows_ld(Rsrc r, int r0, int ld, char* lds,
     }
 }
 
+
+// The rows of one (n, h) of an attention operand: [N, H, S, D] (rows D apart), or with NSHD
+// AlphaFold's [N, S, H, D] (rows H*D apart, head h at column block h).
+template <int D, bool NSHD>
+struct HeadRows {
+    // Element offset of row s of head h of batch row n.
+    static __device__ __forceinline__ size_t at(int n, int h, int s, int S, int H) {
+        return NSHD ? (((size_t)n * S + s) * H + h) * D : (((size_t)n * H + h) * S + s) * D;
+    }
+    static __device__ __forceinline__ int ld(int H) { return NSHD ? H * D : D; }
+    // Bytes from row 0's start to row S-1's end: a buffer resource over exactly the S rows.
+    static __device__ __forceinline__ uint32_t bytes(int S, int H) {
+        if constexpr (NSHD) return S > 0 ? (uint32_t)(((size_t)(S - 1) * H * D + D) * 2) : 0u;
+        else return (uint32_t)S * D * 2;
+    }
+};
+
+// stage_rows over the rows of one (n, h) in either layout (`r` from HeadRows' offset and bytes).
+template <int D, int ROWS, int NTHREADS, bool NSHD>
+__device__ __forceinline__ void stage_head_rows(Rsrc r, int r0, int H, char* lds) {
+    if constexpr (NSHD)
+        stage_rows_ld<D, ROWS, NTHREADS>(r, r0, H * D, lds, threadIdx.x);
+    else
+        stage_rows<D, ROWS, NTHREADS>(r, r0, lds);
+}
 
 // Row operand from a swizzled tile: row `row`, head dims 32*ks + 8*g + 0..7 (zero beyond D).
 template <typename V8, int D>

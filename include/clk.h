@@ -12,7 +12,7 @@
  * the XLA FFI handlers pass them through unchanged.
  *
  * Layouts (all row-major, contiguous):
- *   attention  q, out [N,H,Sq,D]; k, v [N,H,Sk,D] (clk_attention_fwd_nshd: [N,Sq,H,D],
+ *   attention  q, out [N,H,Sq,D]; k, v [N,H,Sk,D] (the *_nshd entries: [N,Sq,H,D],
  *              [N,Sk,H,D]); bias [H,Sq,Sk] shared by the N rows; kmask [N,Sk] uint8
  *              (0 = key absent); lse [N,H,Sq] float32 (natural log)
  *   layer norm x, y [M,C]; scale, offset [C] float32
@@ -126,6 +126,20 @@ clk_status clk_attention_bwd(hipStream_t stream, clk_dtype dtype, const void* q,
                              void* dk, void* dv, float* dbias, void* workspace,
                              size_t workspace_bytes, int64_t N, int64_t H, int64_t Sq, int64_t Sk,
                              int64_t D, float scale);
+
+/*
+ * Attention backward on AlphaFold's [N, S, H, D] layout: q, out, dout, dq [N, Sq, H, D] and k, v,
+ * dk, dv [N, Sk, H, D]; bias, kmask, lse [N, H, Sq], dbias, workspace (the same
+ * clk_attention_bwd_workspace_size) and scale as in clk_attention_bwd, whose kernels it runs with
+ * rows H*D apart: the results are bit-identical to clk_attention_bwd on the transposed operands.
+ * S*H*D*2 must stay below 2^31 bytes. No reference counterpart (as clk_attention_bwd).
+ */
+clk_status clk_attention_bwd_nshd(hipStream_t stream, clk_dtype dtype, const void* q,
+                                  const void* k, const void* v, const void* bias,
+                                  const uint8_t* kmask, const void* out, const void* dout,
+                                  const float* lse, void* dq, void* dk, void* dv, float* dbias,
+                                  void* workspace, size_t workspace_bytes, int64_t N, int64_t H,
+                                  int64_t Sq, int64_t Sk, int64_t D, float scale);
 
 /*
  * Attention backward that allocates nothing. No counterpart in the reference: it is for callers

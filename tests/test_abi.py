@@ -114,6 +114,24 @@ def test_attention_bwd_validation():
     assert "head dim" in _native.last_error()
 
 
+def test_attention_bwd_nshd_validation():
+    lib = _native.lib()
+    dims = [384, 4, 384, 384, 32]
+    ws = lib.clk_attention_bwd_workspace_size(*dims)
+    args = [None, BF16] + [FAKE] * 12 + [FAKE, ws - 1] + dims + [0.17]
+    assert lib.clk_attention_bwd_nshd(*args) == INVALID
+    assert "workspace" in _native.last_error()
+    args[15] = ws
+    args[-2] = 12
+    assert lib.clk_attention_bwd_nshd(*args) == INVALID
+    assert "head dim" in _native.last_error()
+    # [N,S,H,D] rows of one (n, h) lie H*D apart: S*H*D*2 must fit 31 bits.
+    big = [1, 4096, 8192, 8192, 64]
+    args = [None, BF16] + [FAKE] * 12 + [FAKE, 1 << 40] + big + [0.17]
+    assert lib.clk_attention_bwd_nshd(*args) == INVALID
+    assert "[N,S,H,D]" in _native.last_error()
+
+
 def test_attention_bwd_noalloc_refuses_sizes_beyond_its_scratch():
     """Host-side check before any device call: the 1024-residue problem needs more workspace
     than the fixed scratch array holds."""

@@ -79,6 +79,31 @@ def test_attention_bwd_bias_past_float16_range(cuda, shape):
     assert_close("dBias", dbias, rb, tol)
 
 
+# (N, H, Sq, Sk, D, masked_tail, masked_rows): the mask-byte path (Sk % 8 != 0), two key ranges
+# (dQ partials), D = 8, 16 and 64 (the D = 64 kernels), rows with no present key.
+NSHD_CASES = [(3, 2, 100, 77, 32, 0.1, 1), (4, 2, 96, 600, 32, 0.1, 1),
+              (3, 2, 70, 456, 16, 0.1, 1), (2, 1, 130, 200, 64, 0.2, 0),
+              (2, 2, 48, 40, 8, 0.1, 0), (3, 4, 64, 128, 32, 0.3, 1)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=dname)
+@pytest.mark.parametrize("case", NSHD_CASES, ids=lambda c: "x".join(map(str, c[:5])))
+def test_attention_bwd_nshd_layout(cuda, case, dtype):
+    """The [N,S,H,D] backward runs the same kernels with rows H*D apart: dq, dk, dv (in
+    [N,S,H,D]) and dbias are bit-identical to the [N,H,S,D] entry on the transposed operands."""
+    n, h, sq, sk, d, tail, rows = case
+    inp = attention_inputs(n, h, sq, sk, d, dtype, seed=sq * 3 + sk + d, masked_tail=tail,
+                           masked_rows=rows)
+    g, out, lse, (dq, dk, dv, dbias) = _run(inp, cuda)
+    t = lambda x: x.transpose(1, 2).contiguous()  # [N,H,S,D] <-> [N,S,H,D]
+    gs = ops.attention_bwd_nshd(t(g["q"]), t(g["k"]), t(g["v"]), g["bias"], g["kmask"], t(out),
+                                t(g["dout"]), lse, g["scale"])
+    for name, a, b in zip(("dQ", "dK", "dV"), gs[:3], (dq, dk, dv)):
+        assert a.shape == (n, b.shape[2], h, d), name
+        assert torch.equal(t(a), b), name
+    assert torch.equal(gs[3], dbias)
+
+
 # (N, H, Sq, Sk, D): key counts that fill whole 32-key chunks and ones that end inside a chunk,
 # Sk % 8 == 0 (presence words) and not (mask bytes), one and two key ranges.
 MIXED_MASK_SHAPES = [(24, 2, 70, 200, 32), (20, 2, 64, 77, 32), (12, 2, 40, 456, 16),
