@@ -45,6 +45,7 @@ _TABLE = {
     "attention_gate": ((_ARCH, _LIB, "ClkAttentionGate"),),
     "attention_gated": ((_ARCH, _LIB, "ClkAttentionGated"),),
     "attention_nshd": ((_ARCH, _LIB, "ClkAttentionNshd"),),
+    "attention_bwd_nshd": ((_ARCH, _LIB, "ClkAttentionBwdNshd"),),
     "ln_pair_bias": ((_ARCH, _LIB, "ClkLnPairBias"),),
     "gated_dual_proj_bwd": ((_ARCH, _LIB, "ClkGdpBwd"),),
     "triangle_multiply": ((_ARCH, _LIB, "ClkTriangleMultiply"),),

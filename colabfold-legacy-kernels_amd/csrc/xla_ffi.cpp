@@ -14,7 +14,8 @@
 // and accept bf16 as well as f16. Targets without a reference counterpart:
 //   ClkAttentionFwd   q, k, v, bias, kmask -> out, lse (f32 [N,H,Sq]); attribute scale
 //   ClkAttentionNshd  q [N,Sq,H,D], k, v [N,Sk,H,D], bias, kmask -> out [N,Sq,H,D] (AlphaFold's
-//                     layout, no transposes); attribute scale
+//                     layout, no transposes) and optionally lse (f32 [N,H,Sq]); attribute scale
+//   ClkAttentionBwdNshd  ClkAttentionBwd with q, k, v, out, dout, dq, dk, dv in [N,S,H,D]
 //   ClkAttentionGated q, k, v, bias, kmask, x [N,Sq,C], wg [C,H*D], bg [H*D] -> gated
 //                     [N,Sq,H*D] (attention with the output gate fused in); attribute scale
 //   ClkAttentionBwd   q, k, v, bias, kmask, out, dout, lse -> dq, dk, dv, dbias (f32 [H,Sq,Sk]),
@@ -170,18 +171,24 @@ struct AttnDims {
 };
 
 // q [N,H,Sq,D], k, v [N,H,Sk,D], bias [H,Sq,Sk], kmask u8 [N,Sk], all half types alike.
-clk_status decode_attention(const char* who, const Frame& f, AttnDims* d) {
+// Whether b is an attention operand of S rows: [N, H, S, D], or [N, S, H, D] with nshd.
+bool rows_are(const Buffer* b, const AttnDims& d, int64_t S, bool nshd) {
+    return nshd ? dims_are(b, {d.N, S, d.H, d.D}) : dims_are(b, {d.N, d.H, S, d.D});
+}
+
+clk_status decode_attention(const char* who, const Frame& f, AttnDims* d, bool nshd = false) {
     const Buffer *q = f.arg(0), *k = f.arg(1), *v = f.arg(2), *bias = f.arg(3), *km = f.arg(4);
     if (!q || !k || !v || !bias || !km) return bad(who, "expects buffers q, k, v, bias, kmask");
-    if (q->rank != 4) return bad(who, "q must be [N,H,S,D]");
+    if (q->rank != 4) return bad(who, nshd ? "q must be [N,S,H,D]" : "q must be [N,H,S,D]");
     d->N = q->dims[0];
-    d->H = q->dims[1];
-    d->Sq = q->dims[2];
+    d->H = q->dims[nshd ? 2 : 1];
+    d->Sq = q->dims[nshd ? 1 : 2];
     d->D = q->dims[3];
-    if (k->rank != 4) return bad(who, "k must be [N,H,S,D]");
-    d->Sk = k->dims[2];
-    if (!dims_are(k, {d->N, d->H, d->Sk, d->D}) || !dims_are(v, {d->N, d->H, d->Sk, d->D}))
-        return bad(who, "k and v must be [N,H,Sk,D] matching q");
+    if (k->rank != 4) return bad(who, nshd ? "k must be [N,S,H,D]" : "k must be [N,H,S,D]");
+    d->Sk = k->dims[nshd ? 1 : 2];
+    if (!rows_are(k, *d, d->Sk, nshd) || !rows_are(v, *d, d->Sk, nshd))
+        return bad(who, nshd ? "k and v must be [N,Sk,H,D] matching q"
+                             : "k and v must be [N,H,Sk,D] matching q");
     if (!dims_are(bias, {d->H, d->Sq, d->Sk})) return bad(who, "bias must be [H,Sq,Sk]");
     if (!dims_are(km, {d->N, d->Sk}) || km->dtype != kU8) return bad(who, "kmask must be u8 [N,Sk]");
     if (!half_type(q->dtype) || k->dtype != q->dtype || v->dtype != q->dtype ||
@@ -218,28 +225,27 @@ clk_status attention_fwd(const char* who, const Frame& f, bool with_lse) {
 
 clk_status attention_nshd(const Frame& f) {
     const char* who = "ClkAttentionNshd";
-    if (f.nargs() != 5 || f.nrets() != 1)
-        return bad(who, "expects 5 operands (q, k, v, bias, kmask) and 1 result");
-    const Buffer *q = f.arg(0), *k = f.arg(1), *v = f.arg(2), *bias = f.arg(3), *km = f.arg(4);
+    if (f.nargs() != 5 || (f.nrets() != 1 && f.nrets() != 2))
+        return bad(who, "expects 5 operands (q, k, v, bias, kmask) and 1 or 2 results");
+    AttnDims d;
+    clk_status s = decode_attention(who, f, &d, true);
+    if (s != CLK_OK) return s;
     const Buffer* out = f.ret(0);
-    if (!q || !k || !v || !bias || !km || !out) return bad(who, "operands must be buffers");
-    if (q->rank != 4 || k->rank != 4) return bad(who, "q and k must be [N,S,H,D]");
-    const int64_t N = q->dims[0], Sq = q->dims[1], H = q->dims[2], D = q->dims[3];
-    const int64_t Sk = k->dims[1];
-    if (!dims_are(k, {N, Sk, H, D}) || !dims_are(v, {N, Sk, H, D}))
-        return bad(who, "k and v must be [N,Sk,H,D] matching q");
-    if (!dims_are(bias, {H, Sq, Sk})) return bad(who, "bias must be [H,Sq,Sk]");
-    if (!dims_are(km, {N, Sk}) || km->dtype != kU8) return bad(who, "kmask must be u8 [N,Sk]");
-    if (!half_type(q->dtype) || k->dtype != q->dtype || v->dtype != q->dtype ||
-        bias->dtype != q->dtype)
-        return bad(who, "q, k, v and bias must all be f16 or all bf16");
-    if (!dims_are(out, {N, Sq, H, D}) || out->dtype != q->dtype)
+    if (!rows_are(out, d, d.Sq, true) || out->dtype != f.arg(0)->dtype)
         return bad(who, "result must be [N,Sq,H,D] of the input dtype");
+    float* lse = nullptr;
+    if (f.nrets() == 2) {  // the logsumexp for a backward pass
+        const Buffer* l = f.ret(1);
+        if (!dims_are(l, {d.N, d.H, d.Sq}) || l->dtype != kF32)
+            return bad(who, "second result must be f32 [N,H,Sq]");
+        lse = static_cast<float*>(l->data);
+    }
     float scale = 0.f;
     if (!f.attr_f32("scale", &scale)) return bad(who, "missing f32 attribute 'scale'");
-    return clk_attention_fwd_nshd(f.stream(), static_cast<clk_dtype>(q->dtype), q->data, k->data,
-                                  v->data, bias->data, static_cast<const uint8_t*>(km->data),
-                                  out->data, nullptr, N, H, Sq, Sk, D, scale);
+    return clk_attention_fwd_nshd(f.stream(), static_cast<clk_dtype>(f.arg(0)->dtype),
+                                  f.arg(0)->data, f.arg(1)->data, f.arg(2)->data, f.arg(3)->data,
+                                  static_cast<const uint8_t*>(f.arg(4)->data), out->data, lse,
+                                  d.N, d.H, d.Sq, d.Sk, d.D, scale);
 }
 
 clk_status attention_gated(const Frame& f) {
@@ -268,34 +274,34 @@ clk_status attention_gated(const Frame& f) {
                                    d.Sq, d.Sk, d.D, C, scale);
 }
 
-clk_status attention_bwd(const Frame& f) {
-    const char* who = "ClkAttentionBwd";
+clk_status attention_bwd(const Frame& f, bool nshd) {
+    const char* who = nshd ? "ClkAttentionBwdNshd" : "ClkAttentionBwd";
     AttnDims d;
-    clk_status s = decode_attention(who, f, &d);
+    clk_status s = decode_attention(who, f, &d, nshd);
     if (s != CLK_OK) return s;
     const DataType t = f.arg(0)->dtype;
     const Buffer *out = f.arg(5), *dout = f.arg(6), *lse = f.arg(7);
-    if (!dims_are(out, {d.N, d.H, d.Sq, d.D}) || out->dtype != t ||
-        !dims_are(dout, {d.N, d.H, d.Sq, d.D}) || dout->dtype != t)
-        return bad(who, "out and dout must be [N,H,Sq,D] of the input dtype");
+    if (!rows_are(out, d, d.Sq, nshd) || out->dtype != t || !rows_are(dout, d, d.Sq, nshd) ||
+        dout->dtype != t)
+        return bad(who, nshd ? "out and dout must be [N,Sq,H,D] of the input dtype"
+                             : "out and dout must be [N,H,Sq,D] of the input dtype");
     if (!dims_are(lse, {d.N, d.H, d.Sq}) || lse->dtype != kF32)
         return bad(who, "lse must be f32 [N,H,Sq]");
     const Buffer *dq = f.ret(0), *dk = f.ret(1), *dv = f.ret(2), *db = f.ret(3), *ws = f.ret(4);
-    if (!dims_are(dq, {d.N, d.H, d.Sq, d.D}) || dq->dtype != t ||
-        !dims_are(dk, {d.N, d.H, d.Sk, d.D}) || dk->dtype != t ||
-        !dims_are(dv, {d.N, d.H, d.Sk, d.D}) || dv->dtype != t)
+    if (!rows_are(dq, d, d.Sq, nshd) || dq->dtype != t || !rows_are(dk, d, d.Sk, nshd) ||
+        dk->dtype != t || !rows_are(dv, d, d.Sk, nshd) || dv->dtype != t)
         return bad(who, "dq, dk, dv must match q, k, v");
     if (!dims_are(db, {d.H, d.Sq, d.Sk}) || db->dtype != kF32)
         return bad(who, "dbias must be f32 [H,Sq,Sk]");
     if (!ws || ws->dtype != kU8) return bad(who, "fifth result must be the u8 workspace");
     float scale;
     if (!f.attr_f32("scale", &scale)) return bad(who, "missing f32 attribute 'scale'");
-    return clk_attention_bwd(f.stream(), static_cast<clk_dtype>(t), f.arg(0)->data,
-                             f.arg(1)->data, f.arg(2)->data, f.arg(3)->data,
-                             static_cast<const uint8_t*>(f.arg(4)->data), out->data, dout->data,
-                             static_cast<const float*>(lse->data), dq->data, dk->data, dv->data,
-                             static_cast<float*>(db->data), ws->data, (size_t)numel(ws), d.N, d.H,
-                             d.Sq, d.Sk, d.D, scale);
+    return (nshd ? clk_attention_bwd_nshd : clk_attention_bwd)(
+        f.stream(), static_cast<clk_dtype>(t), f.arg(0)->data, f.arg(1)->data, f.arg(2)->data,
+        f.arg(3)->data, static_cast<const uint8_t*>(f.arg(4)->data), out->data, dout->data,
+        static_cast<const float*>(lse->data), dq->data, dk->data, dv->data,
+        static_cast<float*>(db->data), ws->data, (size_t)numel(ws), d.N, d.H, d.Sq, d.Sk, d.D,
+        scale);
 }
 
 clk_status layer_norm_fwd(const Frame& f) {
@@ -530,7 +536,10 @@ CLK_FFI_EXPORT Error* ClkAttentionGated(CallFrame* frame) {
     return run(frame, [](const Frame& f) { return attention_gated(f); });
 }
 CLK_FFI_EXPORT Error* ClkAttentionBwd(CallFrame* frame) {
-    return run(frame, [](const Frame& f) { return attention_bwd(f); });
+    return run(frame, [](const Frame& f) { return attention_bwd(f, false); });
+}
+CLK_FFI_EXPORT Error* ClkAttentionBwdNshd(CallFrame* frame) {
+    return run(frame, [](const Frame& f) { return attention_bwd(f, true); });
 }
 CLK_FFI_EXPORT Error* VoltaLayerNorm(CallFrame* frame) {
     return run(frame, [](const Frame& f) { return layer_norm_fwd(f); });

@@ -13,8 +13,8 @@ pytestmark = pytest.mark.skipif(not clk.available("gfx950"), reason="library not
 
 TARGETS = ["VoltaMma", "VoltaWmma", "ClkAttentionFwd", "ClkAttentionBwd", "VoltaLayerNorm",
            "ClkLayerNormBwd", "VoltaGdp", "VoltaGdpWmma", "ClkLnGdp", "ClkAttentionGate",
-           "ClkAttentionGated", "ClkAttentionNshd", "ClkLnPairBias", "ClkGdpBwd",
-           "ClkTriangleMultiply"]
+           "ClkAttentionGated", "ClkAttentionNshd", "ClkAttentionBwdNshd", "ClkLnPairBias",
+           "ClkGdpBwd", "ClkTriangleMultiply"]
 FAKE = 0x100000
 
 
@@ -111,6 +111,29 @@ def test_attention_bwd_rejects_small_workspace(lib):
     rets = [q(), q(), q(), x.buffer(F32, (h, s, s), FAKE), x.buffer(U8, (1,), FAKE)]
     assert x.call(lib, "ClkAttentionBwd", x.frame(args, rets, [("scale", F32, 0.17)])) is not None
     assert "workspace" in x.errors[-1][1]
+
+
+def test_attention_bwd_nshd_decode_errors(lib):
+    """ClkAttentionBwdNshd checks q, k, v, out, dout and the gradients in [N,S,H,D]."""
+    x = FakeXla()
+    n, h, sq, sk, d = 2, 4, 16, 24, 32
+    qs = lambda: x.buffer(BF16, (n, sq, h, d), FAKE)  # noqa: E731
+    ks = lambda: x.buffer(BF16, (n, sk, h, d), FAKE)  # noqa: E731
+    args = [qs(), ks(), ks(), x.buffer(BF16, (h, sq, sk), FAKE), x.buffer(U8, (n, sk), FAKE),
+            qs(), qs(), x.buffer(F32, (n, h, sq), FAKE)]
+    rets = [qs(), ks(), ks(), x.buffer(F32, (h, sq, sk), FAKE), x.buffer(U8, (1,), FAKE)]
+    scale = [("scale", F32, 0.17)]
+    assert x.call(lib, "ClkAttentionBwdNshd", x.frame(args, rets, scale)) is not None
+    assert "workspace" in x.errors[-1][1]  # every shape accepted, the 1-byte workspace is not
+    bad_out = args[:5] + [x.buffer(BF16, (n, h, sq, d), FAKE)] + args[6:]
+    assert x.call(lib, "ClkAttentionBwdNshd", x.frame(bad_out, rets, scale)) is not None
+    assert "[N,Sq,H,D]" in x.errors[-1][1]
+    bad_dk = rets[:1] + [x.buffer(BF16, (n, h, sk, d), FAKE)] + rets[2:]
+    assert x.call(lib, "ClkAttentionBwdNshd", x.frame(args, bad_dk, scale)) is not None
+    assert "dq, dk, dv" in x.errors[-1][1]
+    # The [N,H,S,D] target rejects the same operands.
+    assert x.call(lib, "ClkAttentionBwd", x.frame(args, rets, scale)) is not None
+    assert "[N,H," in x.errors[-1][1]
 
 
 def test_ln_gdp_operand_count(lib):

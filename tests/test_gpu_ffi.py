@@ -59,6 +59,24 @@ def test_volta_mma_and_attention_bwd_targets(cuda):
     for a, b in zip(grads, ref):
         assert torch.equal(a, b)
 
+    # The [N,S,H,D] targets: forward with lse, then the backward, on the transposed operands.
+    t = lambda x_: x_.transpose(1, 2).contiguous()  # noqa: E731
+    qs, ks, vs, outs_ref, douts = t(q), t(k), t(v), t(ref_out), t(dout)
+    outs, lses = torch.empty_like(qs), torch.empty_like(ref_lse)
+    fr = x.frame([buf(x, tt) for tt in (qs, ks, vs, bias, km)], [buf(x, outs), buf(x, lses)],
+                 [("scale", F32, inp["scale"])])
+    assert x.call(lib, "ClkAttentionNshd", fr) is None, x.errors
+    gs = [torch.empty_like(qs), torch.empty_like(ks), torch.empty_like(vs),
+          torch.empty((h, sq, sk), device=cuda, dtype=torch.float32)]
+    fr = x.frame([buf(x, tt) for tt in (qs, ks, vs, bias, km, outs_ref, douts, ref_lse)],
+                 [buf(x, tt) for tt in gs] + [buf(x, ws)], [("scale", F32, inp["scale"])])
+    assert x.call(lib, "ClkAttentionBwdNshd", fr) is None, x.errors
+    torch.cuda.synchronize()
+    assert torch.equal(outs, outs_ref) and torch.equal(lses, ref_lse)
+    for a, b in zip(gs[:3], ref[:3]):
+        assert torch.equal(t(a), b)
+    assert torch.equal(gs[3], ref[3])
+
 
 # The (D, block_q, block_k) sets each reference target dispatches (cuda/volta_mma_attn.cu:323-331,
 # cuda/volta_wmma_attn.cu:286-292), called with f16 buffers as the reference's callers do.
