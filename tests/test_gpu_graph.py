@@ -53,12 +53,12 @@ def test_attention_fwd_bwd_graph(cuda):
 
 
 def test_attention_layouts_gates_and_pair_bias_graph(cuda):
-    """The [N,S,H,D] forward, the forward with the gate fused, the separate gate and the
-    pair-bias projection."""
+    """The [N,S,H,D] forward and backward, the forward with the gate fused, the separate gate and
+    the pair-bias projection."""
     inp = attention_inputs(2, 4, 70, 96, 32, torch.bfloat16, seed=23, device=cuda,
-                           masked_tail=0.1, masked_rows=1, with_dout=False)
+                           masked_tail=0.1, masked_rows=1)
     q, k, v, bias, km, s = (inp[n] for n in ("q", "k", "v", "bias", "kmask", "scale"))
-    qs, ks, vs = (t.transpose(1, 2).contiguous() for t in (q, k, v))
+    qs, ks, vs, dos = (t.transpose(1, 2).contiguous() for t in (q, k, v, inp["dout"]))
     x, wg, bg = gate_inputs(2, 70, 128, 4 * 32, torch.bfloat16, seed=24, device=cuda)
     g = torch.Generator().manual_seed(25)
     z = torch.randn((16, 24, 128), generator=g).to(torch.bfloat16).to(cuda)
@@ -68,7 +68,8 @@ def test_attention_layouts_gates_and_pair_bias_graph(cuda):
 
     def step():
         o = ops.attention(q, k, v, bias, km, s)
-        return (ops.attention_nshd(qs, ks, vs, bias, km, s, want_lse=True),
+        os_, lse = ops.attention_nshd(qs, ks, vs, bias, km, s, want_lse=True)
+        return (os_, lse, ops.attention_bwd_nshd(qs, ks, vs, bias, km, os_, dos, lse, s),
                 ops.attention_gated(q, k, v, bias, km, x, wg, bg, s),
                 ops.attention_gate(o, x, wg, bg), ops.ln_pair_bias(z, sc, of, w))
 
