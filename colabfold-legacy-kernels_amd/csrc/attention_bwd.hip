@@ -22,6 +22,7 @@
 // P is recomputed in 2 and 3 from the saved lse; it is never stored.
 #include "attention_common.hpp"
 
+#include <algorithm>
 #include <type_traits>
 
 namespace clk {
@@ -1006,6 +1007,29 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
     }
 }
 
+// out[i] = part[i] + part[count4 + i] + ... over nparts slices of count4 16-byte vectors, added
+// in slice order 0, 1, 2, ... with four slices in flight; block blk of nblk, NT threads a block.
+__device__ __forceinline__ void sum_slices(const f32x4* __restrict__ part, size_t count4,
+                                           int nparts, f32x4* __restrict__ out, int blk, int nblk,
+                                           int tid, int NT) {
+    for (size_t i = (size_t)blk * NT + tid; i < count4; i += (size_t)nblk * NT) {
+        f32x4 a = {0.f, 0.f, 0.f, 0.f};
+        int p = 0;
+        for (; p + 4 <= nparts; p += 4) {
+            const f32x4 v0 = part[(size_t)p * count4 + i];
+            const f32x4 v1 = part[(size_t)(p + 1) * count4 + i];
+            const f32x4 v2 = part[(size_t)(p + 2) * count4 + i];
+            const f32x4 v3 = part[(size_t)(p + 3) * count4 + i];
+            a += v0;
+            a += v1;
+            a += v2;
+            a += v3;
+        }
+        for (; p < nparts; ++p) a += part[(size_t)p * count4 + i];
+        out[i] = a;
+    }
+}
+
 // Column owner. A block of NW waves owns (16*KSUB*NW keys, head h, row n); wave w owns keys
 // k0 + 16*KSUB*w + 0..16*KSUB-1 with K and V held as MFMA B operands. The queries stream in
 // 64-row tiles: Q, dO, the transposed bias tile and lse*log2(e), -D_i arrive by direct
@@ -1019,10 +1043,19 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkv2(
     const uint8_t* __restrict__ kmask, const typename TR::elem* __restrict__ dout,
     const float* __restrict__ lse2, const float* __restrict__ ndi,
     const float* __restrict__ row_logit, typename TR::elem* __restrict__ dk,
-    typename TR::elem* __restrict__ dv, int H, int Sq, int Sk, int SqP, float scale) {
+    typename TR::elem* __restrict__ dv, int H, int Sq, int Sk, int SqP, float scale,
+    int main_blocks, const f32x4* __restrict__ dbias_part, f32x4* __restrict__ dbias,
+    size_t dbias_count4, int dbias_parts) {
     using V8 = typename TR::vec8;
     using T = SwzTile<D>;
     static_assert(D <= 32, "column-owner kernel holds one 32-dim k-slot group");
+    if ((int)blockIdx.x >= main_blocks) {
+        // Blocks past the work items sum the row-owner pass's dBias slices (written by the
+        // kernel before this one): they start as the work items run out, in the grid's tail.
+        sum_slices(dbias_part, dbias_count4, dbias_parts, dbias, (int)blockIdx.x - main_blocks,
+                   (int)gridDim.x - main_blocks, threadIdx.x, 64 * NW);
+        return;
+    }
     constexpr int DT = AttnGeom<D>::DT;
     constexpr int KW = 16 * KSUB, KB = NW * KW, NT = 64 * NW;
     constexpr int QB = 64 * T::ROWB;
@@ -1040,7 +1073,7 @@ __global__ __launch_bounds__(64 * NW) void attn_bwd_dkv2(
     // 1-D grid of (key block, head, row) work items, key block fastest, placed so that the key
     // blocks of one (row, head) -- which stream the same Q and dO rows -- share an XCD's L2.
     const int kblocks = (Sk + KB - 1) / KB;
-    const int item = xcd_contiguous(blockIdx.x, gridDim.x);
+    const int item = xcd_contiguous(blockIdx.x, main_blocks);
     const int k0 = (item % kblocks) * KB, h = (item / kblocks) % H, n = item / (kblocks * H);
     const size_t nh = (size_t)n * H + h;
     using HR = HeadRows<D, NSHD>;
@@ -1220,28 +1253,11 @@ __global__ __launch_bounds__(256) void sum_partials_f32(const float* __restrict_
     }
 }
 
-// The same sum four elements at a time (count4 = count / 4, 16-byte aligned arrays), with four
-// partials in flight; the additions keep the order p = 0, 1, 2, ...
+// The same sum four elements at a time (count4 = count / 4, 16-byte aligned arrays).
 __global__ __launch_bounds__(256) void sum_partials_f32x4(const f32x4* __restrict__ part,
                                                           size_t count4, int nparts,
                                                           f32x4* __restrict__ out) {
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < count4;
-         i += (size_t)gridDim.x * 256) {
-        f32x4 a = {0.f, 0.f, 0.f, 0.f};
-        int p = 0;
-        for (; p + 4 <= nparts; p += 4) {
-            const f32x4 v0 = part[(size_t)p * count4 + i];
-            const f32x4 v1 = part[(size_t)(p + 1) * count4 + i];
-            const f32x4 v2 = part[(size_t)(p + 2) * count4 + i];
-            const f32x4 v3 = part[(size_t)(p + 3) * count4 + i];
-            a += v0;
-            a += v1;
-            a += v2;
-            a += v3;
-        }
-        for (; p < nparts; ++p) a += part[(size_t)p * count4 + i];
-        out[i] = a;
-    }
+    sum_slices(part, count4, nparts, out, blockIdx.x, gridDim.x, threadIdx.x, 256);
 }
 
 template <typename TR>
@@ -1286,6 +1302,12 @@ struct BwdPlan {
 };
 
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Whether the column-owner kernel's extra blocks sum the dBias slices of count elements (v2, more
+// than one slice, slices of whole 16-byte vectors) instead of a kernel of their own.
+bool dbias_folded(const BwdPlan& p, size_t count) {
+    return p.v2 && p.nchunks > 1 && count % 4 == 0;
+}
 
 BwdPlan plan_bwd(int64_t N, int64_t H, int64_t Sq, int64_t Sk, int64_t D) {
     BwdPlan p;
@@ -1367,7 +1389,7 @@ template <typename TR>
 void finish_partials(hipStream_t st, const BwdPlan& p, float* dbias_part, float* dq_part,
                      float* dbias, void* dq, size_t dbias_count, size_t dq_count) {
     using E = typename TR::elem;
-    if (p.nchunks > 1) {
+    if (p.nchunks > 1 && !dbias_folded(p, dbias_count)) {
         KernelTimer timer("attn_bwd_dbias_sum", st);
         if (dbias_count % 4 == 0)  // partial arrays are then 16-byte aligned
             sum_partials_f32x4<<<grid_for(dbias_count / 4), 256, 0, st>>>(
@@ -1446,14 +1468,21 @@ void launch_dq2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, 
 template <typename TR, int D, int KSUB, int NW, bool VEC, bool NSHD>
 void launch_dkv2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, const void* v,
                  const void* bias_t, const uint8_t* kmask, const void* dout, const float* lse2,
-                 const float* ndi, const float* rowl, void* dk, void* dv, int N, int H, int Sq,
-                 int Sk, float scale) {
+                 const float* ndi, const float* rowl, void* dk, void* dv, const float* dbias_part,
+                 float* dbias, int N, int H, int Sq, int Sk, float scale) {
     using E = typename TR::elem;
-    const dim3 grid(ceil_div(Sk, 16 * KSUB * NW) * H * N);
+    const int main_blocks = ceil_div(Sk, 16 * KSUB * NW) * H * N;
+    // The dBias slices are summed by extra blocks of this grid when they are 16-byte vectors.
+    const size_t count = (size_t)H * Sq * Sk;
+    const size_t per_block = 64 * NW, vecs = count / 4;
+    const int extra =
+        dbias_folded(p, count) ? (int)std::min<size_t>((vecs + per_block - 1) / per_block, 2048) : 0;
     KernelTimer timer("attn_bwd_dkv", st);
-    attn_bwd_dkv2<TR, D, KSUB, NW, VEC, NSHD><<<grid, 64 * NW, 0, st>>>(
+    attn_bwd_dkv2<TR, D, KSUB, NW, VEC, NSHD><<<dim3(main_blocks + extra), 64 * NW, 0, st>>>(
         (const E*)q, (const E*)k, (const E*)v, (const E*)bias_t, kmask, (const E*)dout, lse2,
-        ndi, rowl, (E*)dk, (E*)dv, H, Sq, Sk, p.SqP, scale);
+        ndi, rowl, (E*)dk, (E*)dv, H, Sq, Sk, p.SqP, scale, main_blocks,
+        reinterpret_cast<const f32x4*>(dbias_part), reinterpret_cast<f32x4*>(dbias), vecs,
+        p.nchunks);
 }
 
 template <typename TR, int D, bool VEC, bool NSHD>
@@ -1484,7 +1513,8 @@ void run_bwd_v2(hipStream_t st, const BwdPlan& p, const void* q, const void* k, 
 #define CLK_KSUB(V, W)                                                                           \
     case V * 100 + W:                                                                            \
         launch_dkv2<TR, D, V, W, VEC, NSHD>(st, p, q, k, v, bias_t, kmask, dout, lse2, ndi,      \
-                                            rowl, dk, dv, N, H, Sq, Sk, scale);                  \
+                                            rowl, dk, dv, dbias_part, dbias, N, H, Sq, Sk,       \
+                                            scale);                                              \
         break;
         CLK_KSUB(1, 8) CLK_KSUB(2, 4)
 #undef CLK_KSUB
