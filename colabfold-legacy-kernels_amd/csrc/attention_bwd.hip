@@ -491,6 +491,28 @@ __device__ void transpose_bias_tile(const typename TR::elem* __restrict__ bias,
     }
 }
 
+// One wave's share of a direct-to-LDS tile fill: wave instructions m = w, w + WSTRIDE, ... of a
+// tile of ROWS rows of D columns (rows `ld` elements apart, from row r0 of the resource) into a
+// swizzled LDS tile, as stage_rows; w is wave-uniform (a scalar), so the instruction count and
+// the LDS addresses are scalar too.
+template <int D, int ROWS, int WSTRIDE>
+__device__ __forceinline__ void stage_rows_wave(Rsrc r, int r0, int ld, char* lds, int w,
+                                                int lane) {
+    using T = SwzTile<D>;
+    constexpr int INSTR = ROWS * T::PL / 64;
+    static_assert(ROWS * T::PL % 64 == 0, "tile must be whole wave instructions");
+#pragma unroll
+    for (int i = 0; i < (INSTR + WSTRIDE - 1) / WSTRIDE; ++i) {
+        const int m = w + i * WSTRIDE;
+        if (INSTR % WSTRIDE != 0 && m >= INSTR) break;
+        const int slot = m * 64 + lane;
+        const int row = slot / T::PL;
+        const int piece = (slot % T::PL) ^ T::swz(row);
+        const int voff = piece < T::P ? (row * ld + piece * 8) * 2 : kPastEnd;
+        buf_dma16(r, voff, r0 * ld * 2, lds + m * 64 * 16);
+    }
+}
+
 // Row owner. A block of 8 waves owns (64 queries, head h, rows n0..n1, key range [kbeg, kend)
 // of up to 128*KCW keys). Wave w = 4*qg + kq owns queries 32*qg + 0..31 (two 16-query
 // sub-tiles) and the 32-key chunks j = 4*i + kq, i < KCW, of the range. The bias of those
@@ -538,6 +560,8 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r16 = lane & 15, g = lane >> 4;
     const int qg = wave >> 2, kq = wave & 3;
+    // The wave index as a scalar: per-wave choices below are scalar branches.
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
     // 1-D grid of (query tile, head, key range, row chunk) work items, query tile fastest,
     // placed so that the query tiles that stream the same K/V rows share an XCD's L2.
     const int qtiles = (Sq + BQ - 1) / BQ;
@@ -575,7 +599,8 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
 
     // Keys absent from every row of the block, or past Sk: bit 8i + j of the lane's keys
     // kbeg + 32(i*KQ + kq) + 8g + j (the rows' presence is ORed in below). Their resident bias
-    // becomes -inf, so S^T is -inf there and P is 0 without any per-score instruction.
+    // becomes an infinity of the sign of lf.cexp's inverse (-inf for a positive scale), so
+    // S^T * lf.cexp is -inf there and P is 0 without any per-score instruction.
     unsigned cabs = 0;
 #pragma unroll
     for (int i = 0; i < KCW; ++i) {
@@ -583,6 +608,15 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
         cabs |= (lim >= 8 ? 0u : lim <= 0 ? 0xffu : (0xffu << lim) & 0xffu) << (8 * i);
     }
 
+    // The two halves of the 16 x 32 identity [I | 0], [0 | I] as MFMA A operands: with dS^T as
+    // the B operand, the product adds dS of keys 16t + 0..15 (rows) of every query (column) to
+    // the accumulator, so the dBias sums run on the matrix core.
+    V8 eye[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) eye[t][j] = TR::from_f(8 * g + j == r16 + 16 * t ? 1.f : 0.f);
+    // dBias of chunk i, sub-tile qt, half t: keys kbeg + 32j + 16t + 4g + 0..3 of query qrow[qt].
     f32x4 dbias[KCW][QTW][2];
 #pragma unroll
     for (int i = 0; i < KCW; ++i)
@@ -591,27 +625,41 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
 #pragma unroll
             for (int t = 0; t < 2; ++t) dbias[i][qt][t] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    auto stage = [&](int n, char* kv, char* qd) {
-        const size_t nh = (size_t)n * H + h;
+    // Row n's operands into (kv, qd) by direct-to-LDS loads, in three parts issued between the
+    // chunks of the row before (so the vector memory path drains while the block computes):
+    // part 0 the K rows of the key range, part 1 the V rows (both over all waves), part 2 the
+    // Q and O rows (first half of the waves), the dO rows and the per-row extras (second half).
+    auto stage_part = [&](int part, int n, char* kv, char* qd) __attribute__((always_inline)) {
         using HR = HeadRows<D, NSHD>;
-        const uint32_t kb = HR::bytes(Sk, H), qb = HR::bytes(Sq, H);
-        const size_t ko = HR::at(n, h, 0, Sk, H), qo = HR::at(n, h, 0, Sq, H);
-        stage_head_rows<D, RK, NT, NSHD>(buffer_rsrc(k + ko, kb), kbeg, H, kv);
-        stage_head_rows<D, RK, NT, NSHD>(buffer_rsrc(v + ko, kb), kbeg, H, kv + KVB);
-        stage_head_rows<D, BQ, NT, NSHD>(buffer_rsrc(q + qo, qb), q0, H, qd);
-        stage_head_rows<D, BQ, NT, NSHD>(buffer_rsrc(dout + qo, qb), q0, H, qd + QB);
-        stage_head_rows<D, BQ, NT, NSHD>(buffer_rsrc(out + qo, qb), q0, H, qd + 2 * QB);
-        if constexpr (VEC) {
-            // Queries past Sq and keys past Sk read zeros. Mask rows are 8-byte aligned (VEC).
-            char* ex = qd + 3 * QB;
-            if (wave == 0)
-                buf_dma4(buffer_rsrc(lse + nh * Sq, (uint32_t)Sq * 4), lane * 4, q0 * 4, ex);
-            // Words kbeg/64 .. of the row's presence bits (kbeg % 64 == 0); words past the row
-            // read zeros.
-            const int words = (Sk + 63) >> 6;
-            if (kmask && wave == 1)
-                buf_dma4(buffer_rsrc(mbits + (size_t)n * words, (uint32_t)words * 8),
-                         lane * 4, (kbeg >> 6) * 8, ex + 256);
+        const int ld = HR::ld(H);
+        if (part < 2) {
+            const Rsrc r = buffer_rsrc((part == 0 ? k : v) + HR::at(n, h, 0, Sk, H),
+                                       HR::bytes(Sk, H));
+            stage_rows_wave<D, RK, NWV>(r, kbeg, ld, kv + part * KVB, wv, lane);
+            return;
+        }
+        const size_t qo = HR::at(n, h, 0, Sq, H);
+        const uint32_t qb = HR::bytes(Sq, H);
+        constexpr int HW = NWV / 2;
+        if (wv < HW) {
+            stage_rows_wave<D, BQ, HW>(buffer_rsrc(q + qo, qb), q0, ld, qd, wv, lane);
+            stage_rows_wave<D, BQ, HW>(buffer_rsrc(out + qo, qb), q0, ld, qd + 2 * QB, wv, lane);
+        } else {
+            stage_rows_wave<D, BQ, HW>(buffer_rsrc(dout + qo, qb), q0, ld, qd + QB, wv - HW,
+                                       lane);
+            if constexpr (VEC) {
+                // Queries past Sq and keys past Sk read zeros. Mask rows are 8-byte aligned.
+                char* ex = qd + 3 * QB;
+                const size_t nh = (size_t)n * H + h;
+                if (wv == HW)
+                    buf_dma4(buffer_rsrc(lse + nh * Sq, (uint32_t)Sq * 4), lane * 4, q0 * 4, ex);
+                // Words kbeg/64 .. of the row's presence bits (kbeg % 64 == 0); words past the
+                // row read zeros.
+                const int words = (Sk + 63) >> 6;
+                if (kmask && wv == HW + 1)
+                    buf_dma4(buffer_rsrc(mbits + (size_t)n * words, (uint32_t)words * 8),
+                             lane * 4, (kbeg >> 6) * 8, ex + 256);
+            }
         }
     };
     // Per-row values kept in registers one row ahead when they are not staged (not VEC), raw:
@@ -632,24 +680,36 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
         ml_nx = kmask ? row_logit[n] : kMaskedLogit;
     };
 
-    // dQ of the last row (this wave's slice), stored at the start of the next step.
+    // dQ of the last row (this wave's slice), stored at the start of the next step by the waves
+    // kq < QTW * DT: sub-tile dqt, head dims dd .. dd+3 of query qrow[dqt], at element offset
+    // dq_off of the (n, h) slice, by the lanes with dq_ok.
+    const int dqt = min(kq / DT, QTW - 1), dd = 16 * (kq % DT) + 4 * g;
+    const bool dq_ok = qrow[dqt] < Sq && dd < D;
+    const int dq_off = qrow[dqt] * HeadRows<D, NSHD>::ld(H) + dd;
     f32x4 pend_dq = {0.f, 0.f, 0.f, 0.f};
-    int pend_n = -1;
-    auto flush_dq = [&]() {
-        if (pend_n < 0) return;
-        const int qt = min(kq / DT, QTW - 1), dt = kq % DT;  // pend_n >= 0: kq < QTW * DT
-        const int d = 16 * dt + 4 * g;
-        if (qrow[qt] < Sq && d < D) {
-            const size_t at = HeadRows<D, NSHD>::at(pend_n, h, qrow[qt], Sq, H) + d;
-            if (nranges == 1) {
-                store4<TR>(dq + at, pend_dq);
-            } else {  // range's partial, in dq's layout
-                float* o = dq_part + (size_t)range * N * H * Sq * D + at;
-                *reinterpret_cast<f32x4*>(o) = pend_dq;
-            }
+    auto flush_dq = [&](int pn) __attribute__((always_inline)) {
+        if (pn < 0 || wv % KQ >= QTW * DT || !dq_ok) return;
+        using HR = HeadRows<D, NSHD>;
+        const size_t at = HR::at(pn, h, 0, Sq, H);
+        if (nranges == 1) {
+            const Rsrc r = buffer_rsrc(dq + at, HR::bytes(Sq, H));
+            E e[4] = {TR::from_f(pend_dq[0]), TR::from_f(pend_dq[1]), TR::from_f(pend_dq[2]),
+                      TR::from_f(pend_dq[3])};
+            u32x2 w;
+            __builtin_memcpy(&w, e, 8);
+            __builtin_amdgcn_raw_buffer_store_b64(w, r, dq_off * 2, 0, 0);
+        } else {  // range's partial, in dq's layout
+            const Rsrc r = buffer_rsrc(dq_part + (size_t)range * N * H * Sq * D + at,
+                                       HR::bytes(Sq, H) * 2);
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, pend_dq), r,
+                                                   dq_off * 4, 0, 0);
         }
-        pend_n = -1;
     };
+    // lse2_out / ndi_out: stored by the lanes g == 0 of the waves kq == 0 of key range 0.
+    int ls_off[QTW];
+#pragma unroll
+    for (int qt = 0; qt < QTW; ++qt)
+        ls_off[qt] = range == 0 && g == 0 && qrow[qt] < Sq ? qrow[qt] * 4 : kPastEnd;
 
     // One row step; `rows_tag` says how the block's rows are masked (kRowsClean, kRowsEmpty,
     // kRowsMixed, below).
@@ -657,6 +717,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
                     auto rows_tag) __attribute__((always_inline)) {
         constexpr int ROWS = decltype(rows_tag)::value;
         const size_t nh = (size_t)n * H + h;
+        const bool more = n + 1 < n1;  // block-uniform: stage row n+1 during this step
         async_wait();
         __syncthreads();  // row n in (kvc, qdc); every wave is done with row n-1
         float lse2c[QTW];
@@ -666,11 +727,11 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
         if constexpr (VEC) {
             const char* ex = qdc + 3 * QB;
 #pragma unroll
-            for (int qt = 0; qt < QTW; ++qt)
-                lse2c[qt] =
-                    qrow[qt] < Sq
-                        ? reinterpret_cast<const float*>(ex)[16 * QTW * qg + 16 * qt + r16] * kLog2e
-                        : INFINITY;
+            for (int qt = 0; qt < QTW; ++qt) {
+                // Read in every lane (queries past Sq read the staged zeros), then selected.
+                const float l = reinterpret_cast<const float*>(ex)[16 * QTW * qg + 16 * qt + r16];
+                lse2c[qt] = qrow[qt] < Sq ? l * kLog2e : INFINITY;
+            }
             if (kmask) {
                 // Chunk i's 32 keys start at bit rel % 64 of staged word rel / 64 (rel = key
                 // offset in the range, a multiple of 32); the lane's 8 keys are bits 8g .. 8g+7
@@ -712,22 +773,24 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
             for (int j = 0; j < 4; ++j) part = dot2<TR>(dw[j], ow[j], part);
             di[qt] = xgroup_sum(part);
         }
-        if (range == 0 && kq == 0 && g == 0) {
+        if (wv % KQ == 0) {
+            const Rsrc rl = buffer_rsrc(lse2_out + nh * Sq, (uint32_t)Sq * 4);
+            const Rsrc rn = buffer_rsrc(ndi_out + nh * Sq, (uint32_t)Sq * 4);
 #pragma unroll
-            for (int qt = 0; qt < QTW; ++qt)
-                if (qrow[qt] < Sq) {
-                    lse2_out[nh * Sq + qrow[qt]] = lse2c[qt];
-                    ndi_out[nh * Sq + qrow[qt]] = -di[qt];
-                }
+            for (int qt = 0; qt < QTW; ++qt) {
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(lse2c[qt]), rl, ls_off[qt],
+                                                      0, 0);
+                __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(-di[qt]), rn, ls_off[qt],
+                                                      0, 0);
+            }
         }
         // The stores of this row and the last go out before row n+1's loads are issued, so the
         // next barrier's wait for those loads finds them long written.
-        flush_dq();
-        if (n + 1 < n1) {
-            stage(n + 1, kvn, qdn);
-            prefetch(n + 1);
-        }
+        flush_dq(n > n0 ? n - 1 : -1);
 
+        f32x4 ndi4[QTW];
+#pragma unroll
+        for (int qt = 0; qt < QTW; ++qt) ndi4[qt] = f32x4{-di[qt], -di[qt], -di[qt], -di[qt]};
         f32x4 dqa[QTW][DT];
 #pragma unroll
         for (int qt = 0; qt < QTW; ++qt)
@@ -757,7 +820,6 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
 #pragma unroll
             for (int i = 0; i < KCW; ++i) {
                 const int c0 = 32 * (i * KQ + kq);  // chunk's first key, relative to kbeg
-                if (kbeg + c0 >= kend) continue;   // block-uniform, the same for every row
                 V8 kf[2], vf[2];
 #pragma unroll
                 for (int t = 0; t < 2; ++t) {
@@ -773,9 +835,15 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
                     for (int qt = 0; qt < QTW; ++qt) {
                         if constexpr (CHUNKS != kChunksEmpty)
                             s[qt][t] = TR::mfma(kf[t], qf[qt], bacc[i][qt][t]);
-                        dp[qt][t] =
-                            TR::mfma(vf[t], dof[qt], f32x4{-di[qt], -di[qt], -di[qt], -di[qt]});
+                        dp[qt][t] = TR::mfma(vf[t], dof[qt], ndi4[qt]);
                     }
+                // Row n+1's loads, a third after each chunk's first MFMAs.
+                if (more) {
+#pragma unroll
+                    for (int part = i * 3 / KCW; part < (i + 1) * 3 / KCW; ++part)
+                        stage_part(part, n + 1, kvn, qdn);
+                    if (i == KCW - 1) prefetch(n + 1);
+                }
                 // The chunk's VALU work (exponentials, dS, the dBias sums) runs at a raised wave
                 // priority until its dQ MFMAs are issued: the other wave on the SIMD then gets
                 // the issue slots while this one waits on its S and dP MFMAs.
@@ -817,9 +885,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
                     for (int j = 0; j < 8; ++j) {
                         // (Keys past Sk get pe too in kChunksEmpty, harmless as above.)
                         const float p = CHUNKS == kChunksEmpty ? pe[qt] : fast_exp2(x[qt][j]);
-                        const float ds = p * dp[qt][j >> 2][j & 3];
-                        dbias[i][qt][j >> 2][j & 3] += ds;
-                        dsf[qt][j] = TR::from_f(ds);
+                        dsf[qt][j] = TR::from_f(p * dp[qt][j >> 2][j & 3]);
                     }
 #pragma unroll
                 for (int dt = 0; dt < DT; ++dt) {
@@ -828,6 +894,11 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
                     for (int qt = 0; qt < QTW; ++qt)
                         dqa[qt][dt] = TR::mfma(kt, dsf[qt], dqa[qt][dt]);
                 }
+#pragma unroll
+                for (int qt = 0; qt < QTW; ++qt)
+#pragma unroll
+                    for (int t = 0; t < 2; ++t)
+                        dbias[i][qt][t] = TR::mfma(eye[t], dsf[qt], dbias[i][qt][t]);
                 __builtin_amdgcn_s_setprio(0);
             }
         };
@@ -855,7 +926,6 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
             for (int w = 1; w < 4; ++w)
                 acc += xch[(((qg * 4 + w) * QTW + qt) * DT + dt) * 64 + lane];
             pend_dq = acc * scale;
-            pend_n = n;
         }
     };
 
@@ -955,6 +1025,7 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
             __syncthreads();  // this block's prefetches read them; the combined words are read
         }
     }
+    const float absent_bias = lf.cexp > 0.f ? -INFINITY : INFINITY;
 #pragma unroll
     for (int i = 0; i < KCW; ++i)
 #pragma unroll
@@ -964,12 +1035,13 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
             for (int qt = 0; qt < QTW; ++qt) {
                 const float b = bacc[i][qt][j >> 2][j & 3];
                 bacc[i][qt][j >> 2][j & 3] =
-                    __int_as_float((~sel & __float_as_int(b)) | (sel & __float_as_int(-INFINITY)));
+                    __int_as_float((~sel & __float_as_int(b)) | (sel & __float_as_int(absent_bias)));
             }
         }
 
     if (n0 < n1) {
-        stage(n0, kv0, qd0);
+#pragma unroll
+        for (int part = 0; part < 3; ++part) stage_part(part, n0, kv0, qd0);
         prefetch(n0);
     }
     auto rows = [&](auto masked_tag) __attribute__((always_inline)) {
@@ -984,24 +1056,26 @@ __global__ __launch_bounds__(256 * QG) void attn_bwd_dq2(
         rows(std::integral_constant<int, kRowsEmpty>{});
     else
         rows(std::integral_constant<int, kRowsClean>{});
-    flush_dq();
+    flush_dq(n1 > n0 ? n1 - 1 : -1);
 
 #pragma unroll
     for (int i = 0; i < KCW; ++i) {
-        const int kk = kbeg + 32 * (i * KQ + kq) + 8 * g;
         if (kbeg + 32 * (i * KQ + kq) >= kend) continue;
 #pragma unroll
         for (int qt = 0; qt < QTW; ++qt) {
             if (qrow[qt] >= Sq) continue;
             float* drow = dbias_dst + (((size_t)chunk * H + h) * Sq + qrow[qt]) * Sk;
-            if (VEC) {
-                if (kk >= Sk) continue;  // kk % 8 == Sk % 8 == 0, so kk < Sk means kk + 8 <= Sk
-                *reinterpret_cast<f32x4*>(drow + kk) = dbias[i][qt][0];
-                *reinterpret_cast<f32x4*>(drow + kk + 4) = dbias[i][qt][1];
-            } else {
 #pragma unroll
-                for (int j = 0; j < 8; ++j)
-                    if (kk + j < Sk) drow[kk + j] = dbias[i][qt][j >> 2][j & 3];
+            for (int t = 0; t < 2; ++t) {
+                const int kk = kbeg + 32 * (i * KQ + kq) + 16 * t + 4 * g;
+                if (VEC) {
+                    // kk % 4 == Sk % 4 == 0, so kk < Sk means kk + 4 <= Sk
+                    if (kk < Sk) *reinterpret_cast<f32x4*>(drow + kk) = dbias[i][qt][t];
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        if (kk + j < Sk) drow[kk + j] = dbias[i][qt][t][j];
+                }
             }
         }
     }

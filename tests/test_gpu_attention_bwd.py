@@ -139,6 +139,29 @@ def test_attention_bwd_mixed_masks(cuda, shape):
     assert all(torch.count_nonzero(dk[i, :, k]).item() == 0 for i, k in zero_dk[:50])
 
 
+@pytest.mark.parametrize("scale", [-0.17, -1.0 / np.sqrt(32)], ids=lambda s: "%.3f" % s)
+@pytest.mark.parametrize("shape", [(3, 2, 100, 77, 32, 0.1), (2, 2, 64, 200, 32, 0.0),
+                                   (3, 2, 70, 456, 16, 0.1), (2, 2, 48, 40, 8, 0.1)],
+                         ids=lambda c: "x".join(map(str, c[:5])))
+def test_attention_bwd_negative_scale(cuda, shape, scale):
+    """A negative scale: the keys past Sk (key counts ending inside a 32-key chunk) and the
+    masked tail still get P = 0, so no infinity reaches dQ; every gradient against the oracle."""
+    n, h, sq, sk, d, tail = shape
+    inp = attention_inputs(n, h, sq, sk, d, torch.bfloat16, seed=sk + 5, masked_tail=tail,
+                           masked_rows=1)
+    inp["scale"] = scale
+    _, out, lse, (dq, dk, dv, dbias) = _run(inp, cuda)
+    ro, rl = ref.attention_fwd(np64(inp["q"]), np64(inp["k"]), np64(inp["v"]), np64(inp["bias"]),
+                               inp["kmask"].numpy(), scale)
+    assert_close("O", out, ro, TOL["bf16"]["o"])
+    rq, rk, rv, rb = _oracle(inp)
+    tol = TOL["bf16"]["grad"]
+    assert_close("dQ", dq, rq, tol)
+    assert_close("dK", dk, rk, tol)
+    assert_close("dV", dv, rv, tol)
+    assert_close("dBias", dbias, rb, tol)
+
+
 def test_attention_bwd_deterministic(cuda):
     inp = attention_inputs(6, 4, 200, 200, 32, torch.bfloat16, seed=21, masked_tail=0.1,
                            masked_rows=1)
