@@ -24,7 +24,9 @@
 // (uniform over the Sk keys), but float32 cannot subtract a running max of -1e9 exactly (its
 // rounding unit there is 128), which would scale P by up to 2^64.
 // lse = m + log(l) (natural log) is written when requested, for the backward pass; for an
-// all-masked row it is therefore ln(Sk), relative to the masked logit.
+// all-masked row it is therefore ln(Sk), relative to the masked logit. Present-key logits are
+// expected above -5e8 (half the masked logit, where the running max starts): a row whose
+// present keys all lie below it has no weight, O = 0 and lse = +inf (zero gradients).
 #include "attention_common.hpp"
 
 #include <type_traits>
@@ -686,7 +688,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
                 store4<TR>(ga.gated + ((size_t)n * Sq + row) * ga.HD + h * D + d, r);
             }
         }
-        if (lse && eg == 0) lse[nh * Sq + row] = (BM ? m_run[qt] * scale : m_run[qt]) + logf(l_tot);
+        // A row whose present-key logits all lie below the running max's start (half the masked
+        // logit) has no weight: O = 0 and lse = +inf, so the backward's P is 0 there.
+        if (lse && eg == 0)
+            lse[nh * Sq + row] =
+                l_tot > 0.f ? (BM ? m_run[qt] * scale : m_run[qt]) + logf(l_tot) : INFINITY;
     }
 }
 

@@ -1,7 +1,7 @@
 // The subset of the XLA FFI C ABI (xla/ffi/api/c_api.h, API version 0.1 as shipped with
 // jax 0.6) that the custom-call handlers in xla_ffi.cpp use, declared here because the XLA
 // headers are not part of this build's toolchain. The struct layouts must match XLA's byte for
-// byte: xla_ffi_layout_check.cpp static-asserts every offset and size below against the real
+// byte: xla_ffi_layout_check.cc static-asserts every offset and size below against the real
 // header whenever FFI_INCLUDE points at one (the same gate as the reference's
 // scripts/build_kernels.sh:44-58).
 //

@@ -146,8 +146,11 @@ clk_status clk_attention_bwd_nshd(hipStream_t stream, clk_dtype dtype, const voi
  * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc). Same operands and results as clk_attention_bwd, without the
  * workspace: it uses the library's fixed per-GPU scratch array of
- * clk_attention_bwd_noalloc_limit() bytes (64 MiB), held by each GPU from first use until the
- * process ends. Sizes whose clk_attention_bwd_workspace_size() exceeds the limit are rejected
+ * clk_attention_bwd_noalloc_limit() bytes (64 MiB). The array sits in a code object of its own,
+ * which the HIP runtime loads on a GPU at this entry's first call there: from then until the
+ * process ends that GPU holds the 64 MiB (the other entry points never load it; measured on
+ * MI355X, free device memory drops by the 64 MiB at the first call of this entry and not at
+ * the other kernels' launches). Sizes whose clk_attention_bwd_workspace_size() exceeds the limit are rejected
  * with CLK_INVALID_ARGUMENT before any device work. Calls that overlap on one GPU (several
  * streams or threads) share that array and race: serialise them.
  */

@@ -5,7 +5,7 @@ import torch
 
 from _util import TOL, assert_close, dname, np64
 from colabfold_legacy_kernels import ops
-from colabfold_legacy_kernels.workloads import attention_inputs, attention_workload
+from colabfold_legacy_kernels.workloads import attention_inputs, attention_workload, gate_inputs
 from oracle import attention as ref
 
 pytestmark = pytest.mark.gpu
@@ -179,12 +179,16 @@ def test_attention_fwd_accepts_reference_block_hints(cuda, d, block):
 @pytest.mark.parametrize("name", ["triangle_attn_256", "triangle_attn_384", "msa_row_attn",
                                   "triangle_attn_1024"])
 def test_attention_fwd_full_size_rows(cuda, name):
-    """Full workload on the GPU; sampled rows n against the oracle (rows are independent)."""
+    """Full workload on the GPU; sampled rows n against the oracle (rows are independent),
+    including two fully padded rows (no present key) where the workload has them."""
     inp = attention_workload(name, torch.bfloat16, device=cuda, with_dout=False)
     out, lse = ops.attention_fwd(inp["q"], inp["k"], inp["v"], inp["bias"], inp["kmask"],
                                  inp["scale"])
     n = inp["q"].shape[0]
-    rows = sorted({0, 1, n // 2, n - 1})
+    padded = (inp["kmask"] == 0).all(dim=1).nonzero().flatten().tolist()
+    if name == "msa_row_attn":
+        assert len(padded) == 102
+    rows = sorted({0, 1, n // 2, n - 1} | set(padded[:1] + padded[-1:]))
     cpu = {k: (v.cpu() if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
     o_ref, _ = _oracle(cpu, rows)
     assert_close("O[rows]", out[rows], o_ref, TOL["bf16"]["o"])
@@ -201,3 +205,66 @@ def test_attention_rejects_bad_operands(cuda):
         ops.attention(q24, q24, q24, g["bias"], g["kmask"])
     with pytest.raises(ops.InvalidArgument):
         ops.attention(g["q"], g["k"], g["v"], g["bias"], g["kmask"], None, 0, 64)
+
+
+@pytest.mark.parametrize("gated", [False, True], ids=["plain", "gated"])
+def test_attention_fwd_nan_propagates(cuda, gated):
+    """A NaN in one query row, and a NaN bias entry at one present key, make exactly the output
+    rows they reach NaN (every head dim), with and without the fused gate; every other row stays
+    finite. (The forward's device code assumes no NaN operand for its maxima; the exponentials
+    and the sums still carry a NaN score into its row.)"""
+    n, h, sq, sk, d = 2, 4, 70, 96, 32
+    inp = attention_inputs(n, h, sq, sk, d, torch.bfloat16, seed=5, masked_tail=0.1,
+                           with_dout=False)
+    q, bias = inp["q"].clone(), inp["bias"].clone()
+    q[1, 2, 5, 3] = float("nan")
+    bias[3, 40, 17] = float("nan")  # key 17 is present in every row
+    g = {k: (v.to(cuda) if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    g["q"], g["bias"] = q.to(cuda), bias.to(cuda)
+    nan_rows = torch.zeros((n, h, sq), dtype=torch.bool)
+    nan_rows[1, 2, 5] = True
+    nan_rows[:, 3, 40] = True
+    if gated:
+        c = 128
+        x, wg, bg = gate_inputs(n, sq, c, h * d, torch.bfloat16, seed=5, bias_std=0.5)
+        out = ops.attention_gated(g["q"], g["k"], g["v"], g["bias"], g["kmask"], x.to(cuda),
+                                  wg.to(cuda), bg.to(cuda), g["scale"]).cpu()
+        out = out.reshape(n, sq, h, d).transpose(1, 2)
+    else:
+        out = ops.attention(g["q"], g["k"], g["v"], g["bias"], g["kmask"], g["scale"]).cpu()
+    isnan = torch.isnan(out.float())
+    assert isnan[nan_rows].all()
+    assert torch.isfinite(out.float()[~nan_rows]).all()
+
+
+def test_attention_row_with_no_weight(cuda):
+    """Present-key logits below -5e8 (a bias of -1e9, the masked-logit convention, on every
+    present key of one query row): that row has no weight, O = 0 and lse = +inf, and its
+    gradients are zero; every other row is unaffected. The backward is compared with the oracle
+    on inputs whose dO of that row is zero (which removes the row from every gradient there)."""
+    n, h, sq, sk, d = 3, 2, 70, 96, 32
+    inp = attention_inputs(n, h, sq, sk, d, torch.bfloat16, seed=8, masked_tail=0.1)
+    b = inp["bias"].float()
+    b[1, 20, :] = -1e9
+    inp["bias"] = b.to(torch.bfloat16)
+    inp["dout"][:, 1, 20, :] = 0
+    g = {k: (v.to(cuda) if isinstance(v, torch.Tensor) else v) for k, v in inp.items()}
+    out, lse = ops.attention_fwd(g["q"], g["k"], g["v"], g["bias"], g["kmask"], g["scale"])
+    assert torch.count_nonzero(out[:, 1, 20]).item() == 0
+    assert torch.isinf(lse[:, 1, 20]).all() and (lse[:, 1, 20] > 0).all()
+    o_ref, _ = _oracle(inp)
+    assert_close("O[h0]", out[:, 0], o_ref[:, 0], TOL["bf16"]["o"])
+    assert_close("O[h1, :20]", out[:, 1, :20], o_ref[:, 1, :20], TOL["bf16"]["o"])
+    assert_close("O[h1, 21:]", out[:, 1, 21:], o_ref[:, 1, 21:], TOL["bf16"]["o"])
+    dq, dk, dv, dbias = ops.attention_bwd(g["q"], g["k"], g["v"], g["bias"], g["kmask"], out,
+                                          g["dout"], lse, g["scale"])
+    assert torch.count_nonzero(dq[:, 1, 20]).item() == 0
+    assert torch.count_nonzero(dbias[1, 20]).item() == 0
+    rq, rk, rv, rb = ref.attention_bwd(np64(inp["q"]), np64(inp["k"]), np64(inp["v"]),
+                                       np64(inp["bias"]), inp["kmask"].numpy(), inp["scale"],
+                                       np64(inp["dout"]))
+    tol = TOL["bf16"]["grad"]
+    assert_close("dQ", dq, rq, tol)
+    assert_close("dK", dk, rk, tol)
+    assert_close("dV", dv, rv, tol)
+    assert_close("dBias", dbias, rb, tol)

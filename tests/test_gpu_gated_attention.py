@@ -28,6 +28,11 @@ CASES = [
     (2, 1, 1, 1, 32, 160, 0.0, 0),
     (2, 4, 70, 300, 32, 128, 0.5, 1),  # the last two key tiles hold no present key
     (2, 2, 40, 256, 16, 64, 0.7, 0),   # ... the last three
+    # More than 256 gate channels: the epilogue's later rounds stage Wg rows into the freed K/V
+    # buffer, 128 channels per buffer; 544 ends on a 32-channel round.
+    (2, 4, 70, 130, 32, 384, 0.5, 1),  # and a padding tail: the last key tile is never run
+    (2, 2, 64, 64, 32, 544, 0.0, 0),
+    (1, 8, 33, 200, 16, 544, 0.6, 1),
 ]
 
 

@@ -211,3 +211,50 @@ def test_ln_gdp_bwd_composition(cuda):
         assert_close(name, a, b, tol)
     for name, a, b in zip(("dwpb", "dbpb", "dwgb", "dbgb"), gb, rb[1:]):
         assert_close(name, a, b, tol)
+
+
+def test_ln_gdp_bwd_full_pair_rep(cuda):
+    """The LN + GDP backward on the 512x512x128 pair representation (Bernoulli(0.95) row mask):
+    sampled rows of dz, and every element of the eight weight and bias gradients and of the
+    LayerNorm's dscale and doffset (sums over all 262144 rows) against the float64 oracle,
+    which runs over row chunks."""
+    from oracle import layer_norm as L
+    dt = torch.bfloat16
+    m, c, n = 512 * 512, 128, 128
+    li = layer_norm_inputs(m, c, dt, seed=3, device=cuda)
+    wa = [t.to(cuda) for t in gdp_weights(c, n, dt, seed=12, bias_std=0.3)]
+    wb = [t.to(cuda) for t in gdp_weights(c, n, dt, seed=13, bias_std=0.3)]
+    g = torch.Generator(device=cuda).manual_seed(14)
+    da, db = (torch.randn((m, n), generator=g, device=cuda).to(dt) for _ in range(2))
+    z, sc, of, mask = (li[k] for k in ("x", "scale", "offset", "mask"))
+    dz, dsc, dof, ga, gb = ops.ln_gated_dual_proj_bwd(z, sc, of, wa, wb, mask, da, db)
+    torch.cuda.synchronize()
+    wa64, wb64 = [np64(t) for t in wa], [np64(t) for t in wb]
+    sc64, of64 = np64(sc), np64(of)
+    acc_a, acc_b = [0.0] * 4, [0.0] * 4
+    rdsc, rdof = np.zeros(c), np.zeros(c)
+    rows = [0, 1, 70001, 131072, 200000, m - 1]
+    rdz = {}
+    step = 16384
+    for a in range(0, m, step):
+        zc, mc = np64(z[a:a + step]), np64(mask[a:a + step])
+        y, _, _ = L.layer_norm_fwd(zc, sc64, of64, 1e-5)
+        ra = ref.gated_dual_proj_bwd(y, *wa64, mc, np64(da[a:a + step]))
+        rb = ref.gated_dual_proj_bwd(y, *wb64, mc, np64(db[a:a + step]))
+        dyc = ra[0] + rb[0]
+        dzc, ds_c, do_c = L.layer_norm_bwd(zc, sc64, dyc, 1e-5)
+        rdsc += ds_c
+        rdof += do_c
+        acc_a = [s + t for s, t in zip(acc_a, ra[1:])]
+        acc_b = [s + t for s, t in zip(acc_b, rb[1:])]
+        for r in rows:
+            if a <= r < a + step:
+                rdz[r] = dzc[r - a]
+    tol = TOL["bf16"]["grad"]
+    assert_close("dz[rows]", dz[rows], np.stack([rdz[r] for r in rows]), tol)
+    assert_close("dscale", dsc, rdsc, tol)
+    assert_close("doffset", dof, rdof, tol)
+    for name, a, b in zip(("dwpa", "dbpa", "dwga", "dbga"), ga, acc_a):
+        assert_close(name, a, b, tol)
+    for name, a, b in zip(("dwpb", "dbpb", "dwgb", "dbgb"), gb, acc_b):
+        assert_close(name, a, b, tol)

@@ -95,9 +95,14 @@ def test_pair_block_64(cuda):
     b = ops.gated_dual_proj(yb, bf(ws[2]), bf(zeros), bf(ws[3]), bf(zeros), ones)
     assert_close("a", a, ref["a"], TOL["bf16"]["gdp"])
     assert_close("b", b, ref["b"], TOL["bf16"]["gdp"])
-    bias = (y @ wbias.to(dev)).reshape(64, 64, h).permute(2, 0, 1).contiguous()
+    # The pair bias through the library's LayerNorm-folded projection (16-bit operands: z and
+    # W_b rounded to bf16), written straight in the [H, Sq, Sk] attention-bias layout.
+    bias = ops.ln_pair_bias(z.to(dev).to(torch.bfloat16), gamma.to(dev), beta.to(dev),
+                            bf(wbias))
+    assert bias.shape == (h, 64, 64)
+    assert_close("bias", bias, ref["bias"], TOL["bf16"]["ln"])
     heads = lambda w: (y @ w.to(dev)).reshape(64, 64, h, d).permute(0, 2, 1, 3).contiguous()  # noqa
     q, k, v = (heads(w).to(torch.bfloat16) for w in (wq, wk, wv))
-    o = ops.attention(q, k, v, bias.to(torch.bfloat16), None, 1 / math.sqrt(d))
+    o = ops.attention(q, k, v, bias, None, 1 / math.sqrt(d))
     assert_close("o", o, ref["o"], TOL["bf16"]["o"])
     _ = np64

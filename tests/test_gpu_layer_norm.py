@@ -62,6 +62,16 @@ def test_layer_norm_full_pair_rep(cuda):
     assert dx.float().sum(dim=1).abs().max().item() < 0.15
     col = dy.double().sum(dim=0)
     assert (doffset.double() - col).abs().max().item() < 1e-3 * col.abs().max().item() + 1e-3
+    # The whole dscale and doffset (column sums over all 262144 rows, reduced through the
+    # kernel's per-block partials) against the float64 oracle, summed over row chunks.
+    dsr, dor = np.zeros(c), np.zeros(c)
+    for a in range(0, m, 32768):
+        _, ds_c, do_c = ref.layer_norm_bwd(np64(x[a:a + 32768]), np64(scale),
+                                           np64(dy[a:a + 32768]), 1e-5)
+        dsr += ds_c
+        dor += do_c
+    assert_close("dscale", dscale, dsr, TOL["bf16"]["ln"])
+    assert_close("doffset", doffset, dor, TOL["bf16"]["ln"])
     dx2, dscale2, doffset2 = ops.layer_norm_bwd(x, scale, dy)
     assert torch.equal(dx, dx2) and torch.equal(dscale, dscale2) and torch.equal(doffset, doffset2)
     dxr, dsr, dor = ref.layer_norm_bwd(np64(x[rows]), np64(scale), np64(dy[rows]), 1e-5)
