@@ -216,8 +216,8 @@ __global__ __launch_bounds__(kThreads) void ln_fwd_generic(const void* __restric
 
 // Backward. Per row: dx = r*(g - mean(g) - xhat*mean(g*xhat)), g = scale*dy. Column sums of
 // dy*xhat and dy accumulate per lane over the rows the lane visits, then over the block's row
-// slots in a fixed order, into the column-major partials part[which*C + c][block];
-// ln_colsum_runs adds each column's blocks in a fixed order.
+// slots in a fixed order, into the block-major partials part[block][which*C + c] (16-byte
+// stores); ln_colsum_blocks adds each column's blocks in a fixed order.
 template <typename TR, int LPR, int NV, int RB>
 __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const void* __restrict__ xv,
                                                           const float* __restrict__ scale,
@@ -321,7 +321,7 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const void* __restrict
     }
 
     // Fixed-order reduction over the ROWS row slots of this block.
-    __shared__ float red[ROWS][2][C];
+    __shared__ __attribute__((aligned(16))) float red[ROWS][2][C];
 #pragma unroll
     for (int v = 0; v < NV; ++v)
 #pragma unroll
@@ -331,13 +331,35 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const void* __restrict
             red[slot][1][c] = acc_b[v][i];
         }
     __syncthreads();
-    // Column-major partials, part[t][block] for t = which*C + c, so that each column's sums
-    // over the blocks are one contiguous run for ln_colsum_runs.
-    for (int t = threadIdx.x; t < 2 * C; t += kThreads) {
-        const int which = t / C, c = t % C;
-        float a = 0.f;
-        for (int r = 0; r < ROWS; ++r) a += red[r][which][c];
-        part[(size_t)t * gridDim.x + blockIdx.x] = a;
+    // Block-major partials part[block][t], t = which*C + c, as 16-byte vectors of four
+    // consecutive sums (one 2*C*4-byte row per block: no partial-line writes). Vector u of the
+    // row sums the ROWS slots in G groups of SPG slots each, then the groups in order.
+    constexpr int T4 = C / 2;  // 16-byte vectors in a block's row of 2*C sums
+    constexpr int G = kThreads >= 2 * T4 ? kThreads / T4 : 1;
+    constexpr int SPG = (ROWS + G - 1) / G;
+    const f32x4* red4 = reinterpret_cast<const f32x4*>(&red[0][0][0]);
+    f32x4* out4 = reinterpret_cast<f32x4*>(part + (size_t)blockIdx.x * 2 * C);
+    if constexpr (G == 1) {
+        for (int u = threadIdx.x; u < T4; u += kThreads) {
+            f32x4 a = red4[u];
+            for (int r = 1; r < ROWS; ++r) a += red4[r * T4 + u];
+            out4[u] = a;
+        }
+    } else {
+        __shared__ f32x4 grp[G][T4];
+        const int u = threadIdx.x % T4, gi = threadIdx.x / T4;
+        if (gi < G) {
+            f32x4 a = {0.f, 0.f, 0.f, 0.f};
+            for (int r = gi * SPG; r < min(ROWS, (gi + 1) * SPG); ++r) a += red4[r * T4 + u];
+            grp[gi][u] = a;
+        }
+        __syncthreads();
+        if (threadIdx.x < T4) {
+            f32x4 a = grp[0][threadIdx.x];
+#pragma unroll
+            for (int i = 1; i < G; ++i) a += grp[i][threadIdx.x];
+            out4[threadIdx.x] = a;
+        }
     }
 }
 
@@ -437,54 +459,42 @@ __global__ __launch_bounds__(1024) void ln_colsum(const float* __restrict__ part
     }
 }
 
-// out[t] (t = which*C + c) = sum of the run part[t*nblocks .. t*nblocks + nblocks-1], one wave
-// per output. With nblocks % 4 == 0 (16-byte aligned runs) lane l adds the 4-float pieces
-// l, l+64, ... into eight 4-wide accumulators (piece p into accumulator (p/64) % 8; 2048 blocks
-// are one round of eight 16-byte loads per lane), otherwise single floats the same way; then
-// the accumulators in order and the lanes in a fixed butterfly. Deterministic.
-__global__ __launch_bounds__(256) void ln_colsum_runs(const float* __restrict__ part, int nblocks,
-                                                      int C, float* __restrict__ dscale,
-                                                      float* __restrict__ doffset) {
-    const int t = blockIdx.x * 4 + (int)(threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (t >= 2 * C) return;  // whole waves
-    const float* run = part + (size_t)t * nblocks;
-    float a = 0.f;
-    if ((nblocks & 3) == 0) {
-        const f32x4* r4 = reinterpret_cast<const f32x4*>(run);
-        const int n4 = nblocks >> 2;
-        f32x4 acc[8];
+// The fast backward's column sums: out[t] = sum over the nblocks partial rows b of
+// part[b*2*C + t] (block-major, 16-byte aligned), four columns t = 4u .. 4u+3 per block of 256
+// threads: thread i adds rows i, i+256, ... in order (all its loads issued first), each wave
+// reduces its 64 lanes by a fixed butterfly (group_sum), and the four waves' sums are added in
+// order. Deterministic.
+__global__ __launch_bounds__(256) void ln_colsum_blocks(const float* __restrict__ part,
+                                                        int nblocks, int C,
+                                                        float* __restrict__ dscale,
+                                                        float* __restrict__ doffset) {
+    constexpr int kIn = 8;  // loads in flight per thread (2048 partial rows in one round)
+    const int u = blockIdx.x;
+    const f32x4* p4 = reinterpret_cast<const f32x4*>(part) + u;
+    const size_t rs = (size_t)C / 2;  // 16-byte vectors per partial row
+    f32x4 a = {0.f, 0.f, 0.f, 0.f};
+    for (int b0 = threadIdx.x; b0 < nblocks; b0 += 256 * kIn) {
+        f32x4 v[kIn];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
-        int b = lane;
-        for (; b + 7 * 64 < n4; b += 8 * 64) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) acc[i] += r4[b + 64 * i];
+        for (int i = 0; i < kIn; ++i) {
+            const int b = b0 + 256 * i;
+            v[i] = b < nblocks ? p4[(size_t)b * rs] : f32x4{0.f, 0.f, 0.f, 0.f};
         }
 #pragma unroll
-        for (int i = 0; i < 7; ++i)
-            if (b + 64 * i < n4) acc[i] += r4[b + 64 * i];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) a += (acc[i][0] + acc[i][1]) + (acc[i][2] + acc[i][3]);
-    } else {
-        float acc[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[i] = 0.f;
-        int b = lane;
-        for (; b + 7 * 64 < nblocks; b += 8 * 64) {
-#pragma unroll
-            for (int i = 0; i < 8; ++i) acc[i] += run[b + 64 * i];
-        }
-#pragma unroll
-        for (int i = 0; i < 7; ++i)
-            if (b + 64 * i < nblocks) acc[i] += run[b + 64 * i];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) a += acc[i];
+        for (int i = 0; i < kIn; ++i) a += v[i];
     }
-    a = group_sum<64>(a);
-    if (lane == 0) {
-        if (t < C) dscale[t] = a;
-        else doffset[t - C] = a;
+    __shared__ f32x4 wsum[4];
+    f32x4 w;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w[j] = group_sum<64>(a[j]);
+    if ((threadIdx.x & 63) == 0) wsum[threadIdx.x >> 6] = w;
+    __syncthreads();
+    if (threadIdx.x < 4) {
+        const float v = ((wsum[0][threadIdx.x] + wsum[1][threadIdx.x]) + wsum[2][threadIdx.x]) +
+                        wsum[3][threadIdx.x];
+        const int t = 4 * u + (int)threadIdx.x;
+        if (t < C) dscale[t] = v;
+        else doffset[t - C] = v;
     }
 }
 
@@ -492,11 +502,16 @@ __global__ __launch_bounds__(256) void ln_colsum_runs(const float* __restrict__ 
 struct RowShape {
     int lpr, nv;
 };
+// Lanes per row: a power of two from 4 to 64 dividing the row's vector count, and at most half
+// of it when there are eight vectors or more, so that a lane holds two vectors: at C = 128 bf16,
+// 8 lanes of two vectors measured 5.9 TB/s forward (the streaming copy's rate at that size)
+// against 5.0 with 16 lanes of one (shorter lane reductions, two loads in flight per lane).
 RowShape row_shape(int64_t C, int vec) {
     if (C <= 0 || C % vec != 0) return {0, 0};
     const int64_t nvec = C / vec;
+    const int64_t cap = nvec >= 8 ? nvec / 2 : nvec;
     int lpr = 1;
-    while (lpr < 64 && nvec % (lpr * 2) == 0) lpr *= 2;
+    while (lpr < 64 && lpr * 2 <= cap && nvec % (lpr * 2) == 0) lpr *= 2;
     const int64_t nv = nvec / lpr;
     if (lpr < 4 || nv > 4) return {0, 0};
     return {lpr, (int)nv};
@@ -650,13 +665,19 @@ void launch_bias(hipStream_t st, const void* x, const float* sc, const float* of
 template <typename TR, int H>
 bool dispatch_bias_h(hipStream_t st, const void* x, const float* sc, const float* of,
                      const void* w, void* bias, int M, int C, float eps) {
-    const RowShape rs = row_shape(C, Vec<TR>::N);
-#define CLK_LNB_CASE(L, V)                                              \
-    if (rs.lpr == (L) && rs.nv == (V)) {                                \
-        launch_bias<TR, L, V, H>(st, x, sc, of, w, bias, M, eps);       \
-        return true;                                                    \
+    RowShape rs = row_shape(C, Vec<TR>::N);
+    if (rs.lpr < H && rs.nv % 2 == 0) {  // one storing lane per head: twice the lanes
+        rs.lpr *= 2;
+        rs.nv /= 2;
     }
-    CLK_LNB_CASE(8, 1) CLK_LNB_CASE(16, 1) CLK_LNB_CASE(32, 1)
+#define CLK_LNB_CASE(L, V)                                              \
+    if constexpr (H <= (L))                                             \
+        if (rs.lpr == (L) && rs.nv == (V)) {                            \
+            launch_bias<TR, L, V, H>(st, x, sc, of, w, bias, M, eps);   \
+            return true;                                                \
+        }
+    CLK_LNB_CASE(4, 1) CLK_LNB_CASE(4, 2) CLK_LNB_CASE(8, 1) CLK_LNB_CASE(8, 2)
+    CLK_LNB_CASE(16, 1) CLK_LNB_CASE(16, 2) CLK_LNB_CASE(32, 1) CLK_LNB_CASE(32, 2)
 #undef CLK_LNB_CASE
     return false;
 }
@@ -810,8 +831,9 @@ extern "C" clk_status clk_layer_norm_bwd(hipStream_t stream, clk_dtype dtype, co
     if (s != CLK_OK) return s;
     if (M > 0 && (!dy || !dscale || !doffset || !workspace))
         return fail(CLK_INVALID_ARGUMENT, "layer_norm_bwd: null pointer");
-    if (M > 0 && !aligned16(dy))
-        return fail(CLK_INVALID_ARGUMENT, "layer_norm_bwd: dy must be 16-byte aligned");
+    if (M > 0 && (!aligned16(dy) || !aligned16(workspace)))
+        return fail(CLK_INVALID_ARGUMENT,
+                    "layer_norm_bwd: dy and workspace must be 16-byte aligned");
     const size_t need = clk_layer_norm_bwd_workspace_size(M, C);
     if (workspace_bytes < need)
         return fail(CLK_INVALID_ARGUMENT, "layer_norm_bwd: workspace %zu bytes, needs %zu",
@@ -841,8 +863,8 @@ extern "C" clk_status clk_layer_norm_bwd(hipStream_t stream, clk_dtype dtype, co
             break;
     }
     KernelTimer timer("ln_bwd_colsum", stream);
-    if (stride == 0)
-        ln_colsum_runs<<<ceil_div(2 * C, 4), 256, 0, stream>>>(part, nblocks, (int)C, dscale,
+    if (stride == 0)  // the fast kernel's block-major rows (C % 4 == 0: 16-byte vectors)
+        ln_colsum_blocks<<<(int)(2 * C / 4), 256, 0, stream>>>(part, nblocks, (int)C, dscale,
                                                               doffset);
     else
         ln_colsum<<<ceil_div(2 * C, kColsumCols), 1024, 0, stream>>>(part, stride, nblocks,
