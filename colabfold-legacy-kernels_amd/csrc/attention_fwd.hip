@@ -155,7 +155,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
     const typename TR::elem* __restrict__ v, const typename TR::elem* __restrict__ bias,
     const uint8_t* __restrict__ kmask, typename TR::elem* __restrict__ out,
     float* __restrict__ lse, int H, int Sq, int Sk, float scale,
-    GateArgs<typename TR::elem> ga, BiasMfma bm) {
+    GateArgs<typename TR::elem> ga, BiasMfma bm, int grp) {
     static_assert(!BM || VEC, "the bias MFMA reads the bias tile from LDS");
     static_assert(!(NSHD && GATE), "the gated entry takes the [N, H, S, D] layout");
     using E = typename TR::elem;
@@ -185,11 +185,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r16 = lane & 15, g = lane >> 4;
-    // 1-D grid of (query tile, head, row) work items, query tile fastest, placed so that the
-    // query tiles of one (row, head) -- which read the same K and V -- share an XCD's L2.
+    // 1-D grid of (query tile, head, row) work items, placed so that each XCD runs a contiguous
+    // range of them: head outermost, then groups of grp rows, then the query tile, then the row
+    // within its group. An XCD's resident blocks then read one head's bias rows (the same for
+    // every row n) and the K and V of a few rows, both of which stay in its L2; query tile
+    // fastest with the head inside the row re-streamed all H heads' bias for every row.
     const int qtiles = (Sq + BQ - 1) / BQ;
     const int item = xcd_contiguous(blockIdx.x, gridDim.x);
-    const int q0 = (item % qtiles) * BQ, h = (item / qtiles) % H, n = item / (qtiles * H);
+    const int nrows = gridDim.x / (qtiles * H), per_head = qtiles * nrows;
+    const int h = item / per_head, rem = item - h * per_head;
+    const int gi = rem / (grp * qtiles), nb = gi * grp, gsz = min(grp, nrows - nb);
+    const int q0 = (rem - gi * grp * qtiles) / gsz * BQ, n = nb + (rem - gi * grp * qtiles) % gsz;
     const size_t nh = (size_t)n * H + h;
     // Rows of one (n, h) in q, k, v and out: [N, H, S, D] (rows D apart), or with NSHD
     // [N, S, H, D] (rows H*D apart, head h at column block h).
@@ -702,6 +708,11 @@ void launch_fwd_qt(hipStream_t st, const void* q, const void* k, const void* v, 
                    float scale, GateArgs<typename TR::elem> ga) {
     using E = typename TR::elem;
     const dim3 grid(ceil_div(Sq, 64 * QT) * H * N);
+    // Rows per group of the work-item order: the query tiles of about 48 (row, head) pairs, half
+    // an XCD's resident blocks (32 CUs x 3), so that one head's bias and those rows' K and V
+    // share its L2 (at N_res = 1024 this cut the launch's time by 9%; any group of 4 to 24 rows
+    // measured within 1%).
+    const int grp = max(1, min(N, 48 / ceil_div(Sq, 64 * QT)));
     // The bias tile through LDS: whole 8-key pieces, 8-byte aligned mask rows and at most
     // kPresWords key tiles (masked bias tiles are changed in LDS from presence words kept there).
     const bool vec = Sk % 8 == 0 && (reinterpret_cast<uintptr_t>(kmask) & 7u) == 0 &&
@@ -710,15 +721,15 @@ void launch_fwd_qt(hipStream_t st, const void* q, const void* k, const void* v, 
     if (vec && bias_mfma_for<TR>(scale, &bm))
         attn_fwd_kernel<TR, D, QT, true, GATE, true, NSHD><<<grid, 256, 0, st>>>(
             (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (E*)out, lse, H, Sq, Sk,
-            scale, ga, bm);
+            scale, ga, bm, grp);
     else if (vec)
         attn_fwd_kernel<TR, D, QT, true, GATE, false, NSHD><<<grid, 256, 0, st>>>(
             (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (E*)out, lse, H, Sq, Sk,
-            scale, ga, bm);
+            scale, ga, bm, grp);
     else
         attn_fwd_kernel<TR, D, QT, false, GATE, false, NSHD><<<grid, 256, 0, st>>>(
             (const E*)q, (const E*)k, (const E*)v, (const E*)bias, kmask, (E*)out, lse, H, Sq, Sk,
-            scale, ga, bm);
+            scale, ga, bm, grp);
 }
 
 template <typename TR, int D, bool GATE>
