@@ -37,6 +37,23 @@ namespace {
 constexpr float kRescaleSlack = 8.f;  // log2 of the largest P before the running max moves
 constexpr int kGateChannels = 128;    // gate channels (wg rows) per K/V buffer in the epilogue
 constexpr int kPresWords = 256;       // most key tiles of the bias-patching forward (LDS words)
+constexpr float kLn2 = 0.69314718055994531f;
+
+// Cross-group max of two values at once (lanes l, l^16, l^32, l^48 share a query): the halves
+// of a and b meet in one register, so the three lane swaps serve both.
+__device__ __forceinline__ void xgroup_max2(float& a, float& b) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(a), __float_as_uint(b), false,
+                                                    false);
+    // lanes 0..31: a's lanes l and l+32; lanes 32..63: b's lanes l-32 and l
+    float c = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+    const auto t = __builtin_amdgcn_permlane16_swap(__float_as_uint(c), __float_as_uint(c), false,
+                                                    false);
+    c = fmaxf(__uint_as_float(t[0]), __uint_as_float(t[1]));
+    const auto u = __builtin_amdgcn_permlane32_swap(__float_as_uint(c), __float_as_uint(c), false,
+                                                    false);
+    a = __uint_as_float(u[0]);
+    b = __uint_as_float(u[1]);
+}
 
 // Per-tile "some key absent or past Sk" flags of one mask row, as bits of a 64-bit word (tiles of
 // 64 keys; tiles past the 64th always take the checked path), worked out by each wave on its
@@ -380,11 +397,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
     // set the max, and P = exp2(x*xs - m*xs) of its keys would be the exponential of the FMA's
     // rounding residue (up to 2^6 at a logit of 1e9), which float16 cannot hold. In a row with
     // no present key every logit is the masked logit 0, the start.
-    float m_run[QT];
+    // Kept as nm = -m*xs, the exponent's offset itself: a tile's move test is one FMA, its
+    // exponent FMAs take nm as it is, and lse = m*scale + ln(l) becomes -nm*ln2 + ln(l).
+    float nm[QT];
     f32x4 acc[QT][G::DT], lsum[QT];
 #pragma unroll
     for (int qt = 0; qt < QT; ++qt) {
-        m_run[qt] = 0.5f * masked_logit;
+        nm[qt] = -(0.5f * masked_logit) * xs;
         lsum[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int dt = 0; dt < G::DT; ++dt) acc[qt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -509,30 +528,39 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
             }
         }
 
+        float mt[QT];
 #pragma unroll
         for (int qt = 0; qt < QT; ++qt) {
-            float mt = x[qt][0][0];
+            mt[qt] = x[qt][0][0];
 #pragma unroll
             for (int c = 0; c < 2; ++c)
 #pragma unroll
-                for (int j = 0; j < 8; ++j) mt = fmaxf(mt, x[qt][c][j]);
-            mt = xgroup_max(mt);
+                for (int j = 0; j < 8; ++j) mt[qt] = fmaxf(mt[qt], x[qt][c][j]);
+        }
+        if constexpr (QT == 2) {
+            xgroup_max2(mt[0], mt[1]);
+        } else {
+#pragma unroll
+            for (int qt = 0; qt < QT; ++qt) mt[qt] = xgroup_max(mt[qt]);
+        }
+#pragma unroll
+        for (int qt = 0; qt < QT; ++qt) {
             // Lazy rescaling: the running max moves only when the tile's max exceeds it by more
             // than kRescaleSlack (in log2 units), so P stays below 2^kRescaleSlack and most tiles
             // skip the rescale of O and l (a wave-uniform branch).
-            const bool move = mt * xs > m_run[qt] * xs + kRescaleSlack;
+            const bool move = fmaf(mt[qt], xs, nm[qt]) > kRescaleSlack;
             if (__any(move)) {
                 // Opaque to if-conversion: without it the compiler runs the rescale on every
                 // tile (alpha = 1 when nothing moved gives the same values).
                 asm volatile("");
-                const float m_new = move ? mt : m_run[qt];
-                const float alpha = fast_exp2((m_run[qt] - m_new) * xs);
-                m_run[qt] = m_new;
+                const float nm_new = move ? -mt[qt] * xs : nm[qt];
+                const float alpha = fast_exp2(nm_new - nm[qt]);
+                nm[qt] = nm_new;
                 lsum[qt][0] *= alpha;  // only component 0 is read
 #pragma unroll
                 for (int dt = 0; dt < G::DT; ++dt) acc[qt][dt] *= alpha;
             }
-            const float neg = -m_run[qt] * xs;
+            const float neg = nm[qt];
             V8 pf[2];
 #pragma unroll
             for (int c = 0; c < 2; ++c)
@@ -590,7 +618,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
     };
     if (PATCH && row_empty) {  // block-uniform
 #pragma unroll
-        for (int qt = 0; qt < QT; ++qt) m_run[qt] = 0.f;
+        for (int qt = 0; qt < QT; ++qt) nm[qt] = 0.f;
         for (int kt = 0; kt < nrun; kt += 2) {
             tile_empty(kt, kv0, kv1, ca, cb);
             if (kt + 1 < nrun) tile_empty(kt + 1, kv1, kv0, cb, ca);
@@ -698,7 +726,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
         // logit) has no weight: O = 0 and lse = +inf, so the backward's P is 0 there.
         if (lse && eg == 0)
             lse[nh * Sq + row] =
-                l_tot > 0.f ? (BM ? m_run[qt] * scale : m_run[qt]) + logf(l_tot) : INFINITY;
+                l_tot > 0.f ? -nm[qt] * kLn2 + logf(l_tot) : INFINITY;
     }
 }
 
