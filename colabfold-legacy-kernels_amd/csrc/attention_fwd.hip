@@ -203,16 +203,28 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(D <= 32 && 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r16 = lane & 15, g = lane >> 4;
     // 1-D grid of (query tile, head, row) work items, placed so that each XCD runs a contiguous
-    // range of them: head outermost, then groups of grp rows, then the query tile, then the row
-    // within its group. An XCD's resident blocks then read one head's bias rows (the same for
-    // every row n) and the K and V of a few rows, both of which stay in its L2; query tile
-    // fastest with the head inside the row re-streamed all H heads' bias for every row.
+    // range of them. grp == 0: query tile fastest, then the head, then the row -- the blocks of
+    // one (row, query tile) read the same gate rows of x and, in the [N, S, H, D] layout, the
+    // same cache lines of q, k and v, and the query tiles of one (row, head) the same K and V.
+    // grp > 0 (a bias too large to stay in an XCD's L2 over all heads): the head outermost, then
+    // groups of grp rows, then the query tile, then the row within its group -- an XCD's resident
+    // blocks then read one head's bias rows (the same for every row n) and the K and V of a few
+    // rows, both of which stay in its L2.
     const int qtiles = (Sq + BQ - 1) / BQ;
     const int item = xcd_contiguous(blockIdx.x, gridDim.x);
-    const int nrows = gridDim.x / (qtiles * H), per_head = qtiles * nrows;
-    const int h = item / per_head, rem = item - h * per_head;
-    const int gi = rem / (grp * qtiles), nb = gi * grp, gsz = min(grp, nrows - nb);
-    const int q0 = (rem - gi * grp * qtiles) / gsz * BQ, n = nb + (rem - gi * grp * qtiles) % gsz;
+    int q0, h, n;
+    if (grp == 0) {
+        q0 = (item % qtiles) * BQ;
+        h = (item / qtiles) % H;
+        n = item / (qtiles * H);
+    } else {
+        const int nrows = gridDim.x / (qtiles * H), per_head = qtiles * nrows;
+        h = item / per_head;
+        const int rem = item - h * per_head;
+        const int gi = rem / (grp * qtiles), nb = gi * grp, gsz = min(grp, nrows - nb);
+        q0 = (rem - gi * grp * qtiles) / gsz * BQ;
+        n = nb + (rem - gi * grp * qtiles) % gsz;
+    }
     const size_t nh = (size_t)n * H + h;
     // Rows of one (n, h) in q, k, v and out: [N, H, S, D] (rows D apart), or with NSHD
     // [N, S, H, D] (rows H*D apart, head h at column block h).
@@ -736,11 +748,13 @@ void launch_fwd_qt(hipStream_t st, const void* q, const void* k, const void* v, 
                    float scale, GateArgs<typename TR::elem> ga) {
     using E = typename TR::elem;
     const dim3 grid(ceil_div(Sq, 64 * QT) * H * N);
-    // Rows per group of the work-item order: the query tiles of about 48 (row, head) pairs, half
-    // an XCD's resident blocks (32 CUs x 3), so that one head's bias and those rows' K and V
-    // share its L2 (at N_res = 1024 this cut the launch's time by 9%; any group of 4 to 24 rows
-    // measured within 1%).
-    const int grp = max(1, min(N, 48 / ceil_div(Sq, 64 * QT)));
+    // The head-outer work-item order when the bias of all heads passes half of an XCD's 4 MB L2,
+    // in groups of rows whose query tiles make about 48 work items, half an XCD's resident
+    // blocks (32 CUs x 3): at N_res = 1024 (8 MB of bias) this cut the launch's fetch from 8.2 to
+    // 0.9 GB and its time by 9% (any group of 4 to 24 rows within 1%). Otherwise the head stays
+    // inside the row: the MSA shapes' gate rows and [N, S, H, D] rows are shared by the heads.
+    const bool head_outer = (size_t)H * Sq * Sk * 2 > (2u << 20);
+    const int grp = head_outer ? max(1, min(N, 48 / ceil_div(Sq, 64 * QT))) : 0;
     // The bias tile through LDS: whole 8-key pieces, 8-byte aligned mask rows and at most
     // kPresWords key tiles (masked bias tiles are changed in LDS from presence words kept there).
     const bool vec = Sk % 8 == 0 && (reinterpret_cast<uintptr_t>(kmask) & 7u) == 0 &&
