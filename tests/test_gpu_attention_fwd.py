@@ -23,6 +23,10 @@ CASES = [
     (1, 1, 16, 4100, 32, 0.1, 0),  # more than 64 key tiles, ragged last tile
     (1, 1, 16, 16400, 32, 0.1, 0),  # more key tiles than the masked-bias patching covers
     (3, 2, 64, 320, 32, 0.6, 1),    # a padding tail of whole key tiles
+    # Biases over 2 MB run the head-outer work-item order in groups of rows: 13 rows in groups
+    # of 9 and 4 (a ragged last group), and 5 rows in one group smaller than the group size.
+    (13, 4, 640, 640, 32, 0.1, 1),
+    (5, 2, 1024, 1024, 16, 0.0, 0),
 ]
 
 
