@@ -469,7 +469,10 @@ __global__ __launch_bounds__(256) void ln_colsum_blocks(const float* __restrict_
                                                         float* __restrict__ dscale,
                                                         float* __restrict__ doffset) {
     constexpr int kIn = 8;  // loads in flight per thread (2048 partial rows in one round)
-    const int u = blockIdx.x;
+    // Column groups placed XCD-contiguously: the eight groups of one 128-byte line of every
+    // partial row then run on one XCD, whose L2 fetches the line once (the identity order put
+    // them on eight XCDs, each fetching it: 8.4 MB read for 1 MB of partials at C = 128).
+    const int u = xcd_contiguous(blockIdx.x, gridDim.x);
     const f32x4* p4 = reinterpret_cast<const f32x4*>(part) + u;
     const size_t rs = (size_t)C / 2;  // 16-byte vectors per partial row
     f32x4 a = {0.f, 0.f, 0.f, 0.f};
