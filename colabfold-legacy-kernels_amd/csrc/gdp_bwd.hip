@@ -461,7 +461,7 @@ __global__ __launch_bounds__(512) void gdp_bwd_dw_kernel(const typename TR::elem
 
 // dwp, dwg [K][N] and dbp, dbg [N] from nb partials [nb][2N*K + 2N] ([2N][K] then [2N]) and the
 // grad kernel's column sums [ng][2N]. A block owns 64 consecutive outputs: thread (c, s) adds the
-// partials s, s + 16, s + 32, ... of four consecutive outputs (16-byte loads, all in flight), and
+// partials s, s + 16, s + 32, ... of four consecutive outputs (16-byte loads, eight in flight), and
 // the 16 subtotals are then added in s order -- a fixed order, so the sums are reproducible.
 template <int K, int N>
 __global__ __launch_bounds__(256) void gdp_bwd_sum_kernel(const float* __restrict__ part, int nb,
@@ -478,8 +478,19 @@ __global__ __launch_bounds__(256) void gdp_bwd_sum_kernel(const float* __restric
     const bool weights = e0 < NW;
     const float* src = weights ? part + e0 + 4 * c : dbpart + (e0 - NW) + 4 * c;
     const int stride = weights ? PS : W2, count = weights ? nb : ng;
+    constexpr int kIn = 8;  // loads issued before their adds (in b order)
     f32x4 a = {0.f, 0.f, 0.f, 0.f};
-    for (int b = s; b < count; b += 16) a += *reinterpret_cast<const f32x4*>(src + (size_t)b * stride);
+    for (int b0 = s; b0 < count; b0 += 16 * kIn) {
+        f32x4 v[kIn];
+#pragma unroll
+        for (int i = 0; i < kIn; ++i) {
+            const int b = b0 + 16 * i;
+            v[i] = b < count ? *reinterpret_cast<const f32x4*>(src + (size_t)b * stride)
+                             : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int i = 0; i < kIn; ++i) a += v[i];
+    }
     sub[s][c] = a;
     __syncthreads();
     if (s != 0) return;
