@@ -154,6 +154,11 @@ __device__ __forceinline__ void buf_dma16(Rsrc r, int voff, int soff, char* lds_
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         r, (__attribute__((address_space(3))) void*)lds_window, 16, voff, soff, 0, 0);
 }
+// The same with the non-temporal cache policy, for rows read once.
+__device__ __forceinline__ void buf_dma16_nt(Rsrc r, int voff, int soff, char* lds_window) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(
+        r, (__attribute__((address_space(3))) void*)lds_window, 16, voff, soff, 0, 2);
+}
 __device__ __forceinline__ void buf_dma4(Rsrc r, int voff, int soff, char* lds_window) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         r, (__attribute__((address_space(3))) void*)lds_window, 4, voff, soff, 0, 0);

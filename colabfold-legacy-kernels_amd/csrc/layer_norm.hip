@@ -12,6 +12,12 @@
 
 namespace clk {
 namespace {
+// Streaming 16-byte load that does not keep its line in the caches (each row is read once):
+// measured 4-8% faster for the backward and the pair-bias projection, which only read rows;
+// 15% slower for the forward, whose stores are non-temporal already.
+__device__ __forceinline__ u32x4 ld16_nt(const void* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
 
 constexpr int kThreads = 256;
 // Row blocking, chosen by measurement on [512*512, 128] bf16 (each block owns a contiguous run
@@ -261,8 +267,8 @@ __global__ __launch_bounds__(kThreads) void ln_bwd_kernel(const void* __restrict
                 rx[r][v] = u32x4{0u, 0u, 0u, 0u};
                 rd[r][v] = u32x4{0u, 0u, 0u, 0u};
                 if (row < rend) {
-                    rx[r][v] = ld16(x + base + (v * LPR + s) * VEC);
-                    rd[r][v] = ld16(dy + base + (v * LPR + s) * VEC);
+                    rx[r][v] = ld16_nt(x + base + (v * LPR + s) * VEC);
+                    rd[r][v] = ld16_nt(dy + base + (v * LPR + s) * VEC);
                 }
             }
         }
@@ -612,7 +618,7 @@ __global__ __launch_bounds__(kThreads) void ln_bias_kernel(const void* __restric
         for (int r = 0; r < RPI; ++r)
 #pragma unroll
             for (int v = 0; v < NV; ++v)
-                raw[r][v] = r0 + r < M ? ld16(x + (r0 + r) * C + (v * LPR + s) * VEC) : u32x4{};
+                raw[r][v] = r0 + r < M ? ld16_nt(x + (r0 + r) * C + (v * LPR + s) * VEC) : u32x4{};
         E out[RPI];
 #pragma unroll
         for (int r = 0; r < RPI; ++r) {
