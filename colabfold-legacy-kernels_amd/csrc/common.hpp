@@ -188,6 +188,11 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 __device__ __forceinline__ void buf_st16(Rsrc r, int voff, int soff, u32x4 v) {
     __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, soff, 0);
 }
+// The same with the non-temporal cache policy. Pays where one wave instruction writes whole
+// 128-byte lines (a line written in pieces by several waves is evicted part-written).
+__device__ __forceinline__ void buf_st16_nt(Rsrc r, int voff, int soff, u32x4 v) {
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, soff, 2);
+}
 
 // Workgroup barrier that publishes LDS only: waits for this wave's LDS operations, not for its
 // outstanding global loads and stores (the fence of __syncthreads waits for those too, so a

@@ -286,8 +286,11 @@ __global__ __launch_bounds__(256) void gdp_stream_kernel(
 // tile j-1 as the B operand of out^T = W^T . xhat^T; one barrier per step. A-tile row r of column
 // half h stands for output column 32cb + 8*(r/4) + 4h + r%4, so a lane's accumulators hold 8
 // consecutive output columns of one row and the epilogue (bias, sigmoid gate, row mask) ends in
-// one 16-byte store per lane and 16-row sub-tile. HBM traffic is one read of z and the mask and
-// one write of a and b.
+// one 16-byte piece per lane and 16-row sub-tile. Where LDS allows (LnGdpPlan::STAGED_OUT) the
+// pieces go to an LDS staging tile and the next step stores whole rows with non-temporal
+// stores (a wave's 32 columns are only half of a 128-byte line, and non-temporal stores of half
+// lines are slower than cached ones; whole-line ones are 12-15% faster here); otherwise they
+// are stored from registers. HBM traffic is one read of z and the mask and one write of a and b.
 //
 // The row statistics follow volta_ops.cu:40-52: one pass of sum and sum of squares in fp32,
 // var = max(sum_sq/C - mean^2, 0). With bf16/f16 inputs the pair products are exact in fp32, so
@@ -303,6 +306,21 @@ struct LnGdpWeights {
 };
 
 constexpr int kLnGdpRows = 64;  // rows per tile
+
+// LDS plan of ln_gdp_kernel<C, N, NB> with row-major outputs. PER_CU blocks share a CU (one
+// 12-wave block at C = N = 128). Each projected tile goes out through an LDS staging buffer (two,
+// rows padded by 16 bytes) when both still fit PER_CU blocks: one store instruction then writes
+// whole output rows, which lets the stores stream past the caches (non-temporal).
+template <int C, int N, int NB>
+struct LnGdpPlan {
+    static constexpr int R = kLnGdpRows;
+    static constexpr int TILE = R * C * 2;             // a z or normalised tile
+    static constexpr int OSTR = 2 * N + 16;            // staged output row stride (bytes)
+    static constexpr int OBB = NB * R * OSTR;          // one staging buffer, every branch
+    static constexpr int PER_CU = NB == 2 ? 128 / N : (C == 128 ? 1 : 2);
+    static constexpr int BASE = 5 * TILE + 2 * R * 4;  // five tiles and two row-mask vectors
+    static constexpr bool STAGED_OUT = PER_CU * (BASE + 2 * OBB) <= 160 * 1024;
+};
 
 template <int PL>
 struct LnGdpGeom {
@@ -361,6 +379,9 @@ __global__ __launch_bounds__(64 * NB * N / 32 + 256) void ln_gdp_kernel(
     constexpr int ZB = R * C * 2;
     constexpr int DPW = (R * PL + NTL - 1) / NTL;  // 16-byte loads per LayerNorm lane and tile
     constexpr int ZBP = DPW * NTL * 16;
+    using PLAN = LnGdpPlan<C, N, NB>;
+    constexpr bool OST = !CM && PLAN::STAGED_OUT;
+    constexpr int OSTR = PLAN::OSTR;
 
     // Three z tiles (normalised, landing, in flight), two normalised tiles and their row masks.
     __shared__ __attribute__((aligned(16))) char z0[ZBP];
@@ -370,6 +391,9 @@ __global__ __launch_bounds__(64 * NB * N / 32 + 256) void ln_gdp_kernel(
     __shared__ __attribute__((aligned(16))) char xh1[ZB];
     __shared__ float mk0[R];
     __shared__ float mk1[R];
+    // Projected tiles on their way out (OST): written in step j to ob[j % 2], stored in step j+1.
+    __shared__ __attribute__((aligned(16))) char ob0[OST ? PLAN::OBB : 16];
+    __shared__ __attribute__((aligned(16))) char ob1[OST ? PLAN::OBB : 16];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -522,7 +546,20 @@ __global__ __launch_bounds__(64 * NB * N / 32 + 256) void ln_gdp_kernel(
                 buf_st16(pend_out, ((16 * sub + r16) * N + 32 * cb + 8 * g) * 2, 0, pend[sub]);
         }
     };
-    auto project = [&](int t, const char* xh, const float* mrow) {
+    // OST: the branch's N/32 waves store its staged tile, 64 consecutive 16-byte pieces (whole
+    // rows) per instruction, four instructions per wave.
+    auto flush_staged = [&](const char* ob) {
+        constexpr int PPR = N / 8, NWB = N / 32;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int f = (i * NWB + cb) * 64 + lane;
+            const int row = f / PPR, piece = f % PPR;
+            const u32x4 v =
+                *reinterpret_cast<const u32x4*>(ob + (br * R + row) * OSTR + piece * 16);
+            buf_st16_nt(pend_out, (row * N + piece * 8) * 2, 0, v);
+        }
+    };
+    auto project = [&](int t, const char* xh, const float* mrow, char* ob) {
 #pragma unroll
         for (int sub = 0; sub < SUB; ++sub) {
             // CM: A row r16 of sub-tile sub is tile row 16*(r16/4) + 4*sub + r16%4, so the C rows
@@ -562,7 +599,11 @@ __global__ __launch_bounds__(64 * NB * N / 32 + 256) void ln_gdp_kernel(
                     const int h = q >> 2, i = q & 3;
                     o[q] = m * acc[0][h][i] * fast_rcp(1.f + fast_exp2(acc[1][h][i]));
                 }
-                pend[sub] = pack8<TR>(o);
+                if constexpr (OST)
+                    *reinterpret_cast<u32x4*>(ob + (br * R + 16 * sub + r16) * OSTR +
+                                              (32 * cb + 8 * g) * 2) = pack8<TR>(o);
+                else
+                    pend[sub] = pack8<TR>(o);
             }
         }
         if constexpr (CM) {
@@ -576,17 +617,24 @@ __global__ __launch_bounds__(64 * NB * N / 32 + 256) void ln_gdp_kernel(
     // waves project tile j - 1; one barrier per step. The two roles run separate loops with the
     // same number of barriers, so neither holds the other's registers.
     if (mfma_wave) {
-        auto mstep = [&](int j, const char* xr, const float* mr) {
+        auto mstep = [&](int j, const char* xr, const float* mr, char* obw, const char* obr) {
             lds_barrier();
-            flush();
-            if (j >= 1) project(tile_of(j - 1), xr, mr);
+            if constexpr (OST) flush_staged(obr);
+            else flush();
+            if (j >= 1) project(tile_of(j - 1), xr, mr, obw);
         };
         for (int j = 0; j <= mine; j += 2) {
-            mstep(j, xh1, mk1);
+            mstep(j, xh1, mk1, ob0, ob1);
             if (j + 1 > mine) break;
-            mstep(j + 1, xh0, mk0);
+            mstep(j + 1, xh0, mk0, ob1, ob0);
         }
-        flush();
+        if constexpr (OST) {
+            lds_barrier();  // every wave's part of the last tile is staged (the LayerNorm waves
+                            // take this barrier too)
+            flush_staged(mine % 2 ? ob1 : ob0);
+        } else {
+            flush();
+        }
     } else {
         uint32_t ma[PASSES], mb[PASSES];
         load_mask(0, ma);
@@ -616,6 +664,7 @@ __global__ __launch_bounds__(64 * NB * N / 32 + 256) void ln_gdp_kernel(
             if (j + 5 > mine) break;
             lstep(j + 5, z2, z1, xh1, mk1, mb, ma);
         }
+        if constexpr (OST) lds_barrier();  // the MFMA waves' last one, before their last stores
     }
     async_wait();  // no direct-to-LDS load may still be in flight when the workgroup ends
 }
@@ -674,7 +723,7 @@ clk_status launch_gdp_resident(hipStream_t st, const void* x, const void* wp, co
     // Resident blocks per CU: the five 64-row LDS tiles take 80 KB at K = 128 (one block), 40 KB
     // at K = 64 (two).
     const int ntiles = (M + kLnGdpRows - 1) / kLnGdpRows;
-    const int per_cu = K == 128 ? 1 : 2;
+    const int per_cu = LnGdpPlan<K, N, 1>::PER_CU;
     const int grid = ntiles < 256 * per_cu ? ntiles : 256 * per_cu;
     KernelTimer timer("gdp", st);
     ln_gdp_kernel<TR, K, N, false, false, 1><<<grid, 2 * N + 256, 0, st>>>(
@@ -726,7 +775,7 @@ clk_status launch_ln_gdp(hipStream_t st, const void* z, const float* gamma, cons
     // One 12-wave block per CU at N = C = 128 (its five 16 KB LDS tiles take half the CU's LDS,
     // its registers three waves per SIMD); narrower N runs more, smaller blocks per CU.
     const int ntiles = (M + kLnGdpRows - 1) / kLnGdpRows;
-    const int per_cu = 128 / N;
+    const int per_cu = LnGdpPlan<C, N, 2>::PER_CU;
     const int grid = ntiles < 256 * per_cu ? ntiles : 256 * per_cu;
     KernelTimer timer("ln_gdp", st);
     ln_gdp_kernel<TR, C, N, CM><<<grid, 4 * N + 256, 0, st>>>((const E*)z, gamma, beta, wb,
