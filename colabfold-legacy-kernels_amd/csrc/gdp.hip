@@ -537,7 +537,8 @@ __global__ __launch_bounds__(64 * NB * N / 32 + 256) void ln_gdp_kernel(
 #pragma unroll
                 for (int half = 0; half < 2; ++half) {
                     const u32x2 a = pendc[2 * half][h], b = pendc[2 * half + 1][h];
-                    *reinterpret_cast<u32x4*>(at + 8 * half) = u32x4{a[0], a[1], b[0], b[1]};
+                    __builtin_nontemporal_store(u32x4{a[0], a[1], b[0], b[1]},
+                                                reinterpret_cast<u32x4*>(at + 8 * half));
                 }
             }
         } else {

@@ -289,6 +289,11 @@ __global__ __launch_bounds__(512) void tri_out_kernel(TriOutParams<typename TR::
     __shared__ __attribute__((aligned(16))) char x2[XB];
     __shared__ __attribute__((aligned(16))) char xh1[ZB];  // LN_c(x), [64][C] swizzled
     __shared__ __attribute__((aligned(16))) char xh2[ZB];  // LN_in(z), [64][C] swizzled
+    // The projected tile on its way out, rows padded by 16 bytes: written after the tile's
+    // second barrier, stored by every wave as whole rows after the next tile's first.
+    constexpr int OSTR = 2 * C + 16;
+    constexpr int NST = C / 64;  // 64-piece store instructions per wave and tile
+    __shared__ __attribute__((aligned(16))) char ob[R * OSTR];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -327,7 +332,7 @@ __global__ __launch_bounds__(512) void tri_out_kernel(TriOutParams<typename TR::
     }
 
     const int ntiles = M / R;
-    // Every tile issues DPX + DPZ direct-to-LDS loads and SUBW stores in every wave (tiles past
+    // Every tile issues DPX + DPZ direct-to-LDS loads and NST stores in every wave (tiles past
     // the end load from empty resources; the first store batch goes to an empty resource).
     // One x load of a wave covers eight channels: its resource starts at the first of them, so
     // offsets stay below 8*M*2 bytes whatever C*M is.
@@ -349,19 +354,23 @@ __global__ __launch_bounds__(512) void tri_out_kernel(TriOutParams<typename TR::
             buf_dma16(rz, (b + lane) * 16, 0, zb + b * 16);
         }
     };
-    // The pending tile's output rows (an empty resource before the first tile).
-    u32x4 pend[SUBW] = {};
+    // The staged tile's output rows (an empty resource before the first tile): 64 consecutive
+    // 16-byte pieces (whole rows) per instruction, non-temporal -- a wave's own 32 columns would
+    // be half lines, which non-temporal stores write back slowly.
     Rsrc pend_out = buffer_rsrc(pr.out, 0);
     auto flush = [&]() {
+        constexpr int PPR = C / 8;
 #pragma unroll
-        for (int s = 0; s < SUBW; ++s) {
-            const int row = 16 * (sh * SUBW + s) + r16;
-            buf_st16(pend_out, (row * C + 32 * cb + 8 * g) * 2, 0, pend[s]);
+        for (int i = 0; i < NST; ++i) {
+            const int f = (i * 8 + wave) * 64 + lane;
+            const int row = f / PPR, piece = f % PPR;
+            buf_st16_nt(pend_out, (row * C + piece * 8) * 2, 0,
+                        *reinterpret_cast<const u32x4*>(ob + row * OSTR + piece * 16));
         }
     };
 
     auto tile = [&](int t, const char* xc, const char* zc, char* xn, char* zn) {
-        vm_wait<SUBW + DPX + DPZ>();
+        vm_wait<NST + DPX + DPZ>();
         lds_barrier();  // tile t in xc, zc; every wave is done with xh1, xh2 of the last tile
         flush();
         if (wave < 4) {
@@ -456,7 +465,7 @@ __global__ __launch_bounds__(512) void tri_out_kernel(TriOutParams<typename TR::
                 const int h = j >> 2, i = j & 3;
                 o[j] = acc[0][h][i] * fast_rcp(1.f + fast_exp2(acc[1][h][i]));
             }
-            pend[s] = pack8<TR>(o);
+            *reinterpret_cast<u32x4*>(ob + xrow * OSTR + (32 * cb + 8 * g) * 2) = pack8<TR>(o);
         }
     };
 
@@ -473,6 +482,7 @@ __global__ __launch_bounds__(512) void tri_out_kernel(TriOutParams<typename TR::
         if (t + 2 * G >= ntiles) break;
         tile(t + 2 * G, x2, z2, x1, z1);
     }
+    lds_barrier();  // the last tile is staged
     flush();
     async_wait();  // no direct-to-LDS load may still be in flight when the workgroup ends
 }
