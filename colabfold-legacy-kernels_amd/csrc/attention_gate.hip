@@ -45,6 +45,10 @@ __global__ __launch_bounds__(2 * HD) void attn_gate_kernel(
     __shared__ __attribute__((aligned(16))) char x0[XB];
     __shared__ __attribute__((aligned(16))) char x1[XB];
     __shared__ __attribute__((aligned(16))) char x2[XB];
+    // The gated tile on its way out, rows padded by 16 bytes: written at the end of a tile (after
+    // a barrier: every wave has stored the last one), stored as whole rows in the next.
+    constexpr int OSTR = 2 * HD + 16;
+    __shared__ __attribute__((aligned(16))) char ob[R * OSTR];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -76,10 +80,10 @@ __global__ __launch_bounds__(2 * HD) void attn_gate_kernel(
         s0 = (t - n * qblocks) * R;
         return t < ntiles ? min(R, Sq - s0) : 0;
     };
-    // Every tile issues the same vector memory operations in every wave: DPW direct-to-LDS loads
-    // (pieces past the tile's rows read zeros; tiles past the end use an empty resource) and SUB
-    // stores (rows past the tile fall outside the store resource and are dropped). The o loads
-    // are not counted.
+    // Every tile issues the same vector memory operations in every wave: SUB = 4 stores (rows past
+    // the tile fall outside the store resource and are dropped), the o loads and DPW direct-to-
+    // LDS loads (pieces past the tile's rows read zeros; tiles past the end use an empty
+    // resource).
     auto stage = [&](int t, char* xb) {
         int n, s0;
         const int rows = rows_of(t, n, s0);
@@ -111,25 +115,37 @@ __global__ __launch_bounds__(2 * HD) void attn_gate_kernel(
         return buffer_rsrc(rows > 0 ? out + ((size_t)n * Sq + s0) * HD : out,
                            (uint32_t)rows * HD * 2);
     };
-    auto store = [&](Rsrc ro, const u32x4 (&res)[SUB]) {
+    // The staged tile as whole rows, 64 consecutive 16-byte pieces per instruction, four per
+    // wave, non-temporal (a wave's own 32 columns are half lines, which non-temporal stores
+    // write back slowly).
+    static_assert(SUB == 4, "four stores per wave and tile, as the staging writes");
+    auto store = [&](Rsrc ro) {
+        constexpr int PPR = HD / 8;
 #pragma unroll
-        for (int sub = 0; sub < SUB; ++sub)
-            buf_st16(ro, ((16 * sub + r16) * HD + col0) * 2, 0, res[sub]);
+        for (int i = 0; i < SUB; ++i) {
+            const int f = (i * NW + wave) * 64 + lane;
+            const int row = f / PPR, piece = f % PPR;
+            buf_st16_nt(ro, (row * HD + piece * 8) * 2, 0,
+                        *reinterpret_cast<const u32x4*>(ob + row * OSTR + piece * 16));
+        }
     };
 
     const int G = gridDim.x;
-    u32x4 oa[SUB], ob[SUB], res[SUB] = {};
+    u32x4 oa[SUB], ob2[SUB];
+    Rsrc pend_out = out_rsrc(ntiles);  // the staged tile's rows (none before the first)
 
     // Tile t is read from xc; tile t + 2G goes into xn, which held tile t - G. Issued after xc's
-    // loads: at least the stores of tiles t - 2G and t - G and the loads of tile t + G. The o
-    // vectors of tile t are in oc (loaded during tile t - G, before the x loads of tile t + G,
-    // so waiting for them never waits for those); tile t + G's go into on.
+    // loads: at least the stores of tile t - 2G, the o loads of tile t and the loads of tile
+    // t + G. The o vectors of tile t are in oc (loaded during tile t - G, before the x loads of
+    // tile t + G, so waiting for them never waits for those); tile t + G's go into on.
     auto tile = [&](int t, const char* xc, char* xn, const u32x4 (&oc)[SUB], u32x4 (&on)[SUB]) {
         vm_wait<2 * SUB + DPW>();
-        lds_barrier();  // x tile t in xc; every wave is done reading xn (tile t - G)
+        lds_barrier();  // x tile t in xc, tile t - G staged; every wave is done reading xn
+        store(pend_out);
         if (t + G < ntiles) load_o(t + G, on);
         stage(t + 2 * G, xn);
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
+        u32x4 res[SUB];
 #pragma unroll
         for (int sub = 0; sub < SUB; ++sub) {
             const int xrow = 16 * sub + r16;
@@ -147,8 +163,11 @@ __global__ __launch_bounds__(2 * HD) void attn_gate_kernel(
             for (int j = 0; j < 8; ++j) r[j] = ov[j] * fast_rcp(1.f + fast_exp2(acc[j >> 2][j & 3]));
             res[sub] = pack8<TR>(r);
         }
-        __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        store(out_rsrc(t), res);
+        lds_barrier();  // every wave has read the staged tile t - G
+#pragma unroll
+        for (int sub = 0; sub < SUB; ++sub)
+            *reinterpret_cast<u32x4*>(ob + (16 * sub + r16) * OSTR + col0 * 2) = res[sub];
+        pend_out = out_rsrc(t);
     };
 
     // Prologue: two tiles in flight, each followed by a batch of (empty) stores, so that the
@@ -158,24 +177,26 @@ __global__ __launch_bounds__(2 * HD) void attn_gate_kernel(
     load_o(t, oa);
     stage(t, x0);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    store(none, res);
+    store(none);
     stage(t + G, x1);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    store(none, res);
+    store(none);
     // Three x buffers and two o register sets: the pattern repeats every six tiles.
     for (; t < ntiles; t += 6 * G) {
-        tile(t, x0, x2, oa, ob);
+        tile(t, x0, x2, oa, ob2);
         if (t + G >= ntiles) break;
-        tile(t + G, x1, x0, ob, oa);
+        tile(t + G, x1, x0, ob2, oa);
         if (t + 2 * G >= ntiles) break;
-        tile(t + 2 * G, x2, x1, oa, ob);
+        tile(t + 2 * G, x2, x1, oa, ob2);
         if (t + 3 * G >= ntiles) break;
-        tile(t + 3 * G, x0, x2, ob, oa);
+        tile(t + 3 * G, x0, x2, ob2, oa);
         if (t + 4 * G >= ntiles) break;
-        tile(t + 4 * G, x1, x0, oa, ob);
+        tile(t + 4 * G, x1, x0, oa, ob2);
         if (t + 5 * G >= ntiles) break;
-        tile(t + 5 * G, x2, x1, ob, oa);
+        tile(t + 5 * G, x2, x1, ob2, oa);
     }
+    lds_barrier();  // the last tile is staged
+    store(pend_out);
     async_wait();  // no direct-to-LDS load may still be in flight when the workgroup ends
 }
 
