@@ -115,20 +115,10 @@ __global__ __launch_bounds__(2 * HD) void attn_gate_kernel(
         return buffer_rsrc(rows > 0 ? out + ((size_t)n * Sq + s0) * HD : out,
                            (uint32_t)rows * HD * 2);
     };
-    // The staged tile as whole rows, 64 consecutive 16-byte pieces per instruction, four per
-    // wave, non-temporal (a wave's own 32 columns are half lines, which non-temporal stores
-    // write back slowly).
-    static_assert(SUB == 4, "four stores per wave and tile, as the staging writes");
-    auto store = [&](Rsrc ro) {
-        constexpr int PPR = HD / 8;
-#pragma unroll
-        for (int i = 0; i < SUB; ++i) {
-            const int f = (i * NW + wave) * 64 + lane;
-            const int row = f / PPR, piece = f % PPR;
-            buf_st16_nt(ro, (row * HD + piece * 8) * 2, 0,
-                        *reinterpret_cast<const u32x4*>(ob + row * OSTR + piece * 16));
-        }
-    };
+    // The staged tile as whole rows: four store instructions per wave, as many as the SUB
+    // stores the wait counts assume.
+    static_assert(SUB == 4, "four stores per wave and tile");
+    auto store = [&](Rsrc ro) { store_staged_rows<R, HD, OSTR, NW>(ro, ob, wave, lane); };
 
     const int G = gridDim.x;
     u32x4 oa[SUB], ob2[SUB];

@@ -194,6 +194,23 @@ __device__ __forceinline__ void buf_st16_nt(Rsrc r, int voff, int soff, u32x4 v)
     __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, soff, 2);
 }
 
+// Stores a tile of R rows x W 2-byte columns staged in LDS (row stride OSTR bytes) to the rows of
+// `ro` (row stride W elements; rows past the resource are dropped) as whole rows: wave `wave` of
+// NW takes 64 consecutive 16-byte pieces per instruction, non-temporal. An MFMA wave's own
+// output is 16 rows x 64 bytes (half lines); staging it lets one instruction write whole lines.
+template <int R, int W, int OSTR, int NW>
+__device__ __forceinline__ void store_staged_rows(Rsrc ro, const char* ob, int wave, int lane) {
+    constexpr int PPR = W / 8, NI = R * PPR / (64 * NW);
+    static_assert(W % 8 == 0 && NI * 64 * NW == R * PPR, "whole store rounds");
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+        const int f = (i * NW + wave) * 64 + lane;
+        const int row = f / PPR, piece = f % PPR;
+        buf_st16_nt(ro, (row * W + piece * 8) * 2, 0,
+                    *reinterpret_cast<const u32x4*>(ob + row * OSTR + piece * 16));
+    }
+}
+
 // Workgroup barrier that publishes LDS only: waits for this wave's LDS operations, not for its
 // outstanding global loads and stores (the fence of __syncthreads waits for those too, so a
 // barrier right after a batch of stores would stall for their write-back).

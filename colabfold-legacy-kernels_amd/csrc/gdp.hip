@@ -547,18 +547,9 @@ __global__ __launch_bounds__(64 * NB * N / 32 + 256) void ln_gdp_kernel(
                 buf_st16(pend_out, ((16 * sub + r16) * N + 32 * cb + 8 * g) * 2, 0, pend[sub]);
         }
     };
-    // OST: the branch's N/32 waves store its staged tile, 64 consecutive 16-byte pieces (whole
-    // rows) per instruction, four instructions per wave.
+    // OST: the branch's N/32 waves store its staged tile as whole rows (four instructions each).
     auto flush_staged = [&](const char* ob) {
-        constexpr int PPR = N / 8, NWB = N / 32;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const int f = (i * NWB + cb) * 64 + lane;
-            const int row = f / PPR, piece = f % PPR;
-            const u32x4 v =
-                *reinterpret_cast<const u32x4*>(ob + (br * R + row) * OSTR + piece * 16);
-            buf_st16_nt(pend_out, (row * N + piece * 8) * 2, 0, v);
-        }
+        store_staged_rows<R, N, OSTR, N / 32>(pend_out, ob + br * R * OSTR, cb, lane);
     };
     auto project = [&](int t, const char* xh, const float* mrow, char* ob) {
 #pragma unroll

@@ -354,20 +354,10 @@ __global__ __launch_bounds__(512) void tri_out_kernel(TriOutParams<typename TR::
             buf_dma16(rz, (b + lane) * 16, 0, zb + b * 16);
         }
     };
-    // The staged tile's output rows (an empty resource before the first tile): 64 consecutive
-    // 16-byte pieces (whole rows) per instruction, non-temporal -- a wave's own 32 columns would
-    // be half lines, which non-temporal stores write back slowly.
+    // The staged tile's output rows (an empty resource before the first tile), stored as whole
+    // rows by all eight waves (NST instructions each).
     Rsrc pend_out = buffer_rsrc(pr.out, 0);
-    auto flush = [&]() {
-        constexpr int PPR = C / 8;
-#pragma unroll
-        for (int i = 0; i < NST; ++i) {
-            const int f = (i * 8 + wave) * 64 + lane;
-            const int row = f / PPR, piece = f % PPR;
-            buf_st16_nt(pend_out, (row * C + piece * 8) * 2, 0,
-                        *reinterpret_cast<const u32x4*>(ob + row * OSTR + piece * 16));
-        }
-    };
+    auto flush = [&]() { store_staged_rows<R, C, OSTR, 8>(pend_out, ob, wave, lane); };
 
     auto tile = [&](int t, const char* xc, const char* zc, char* xn, char* zn) {
         vm_wait<NST + DPX + DPZ>();
