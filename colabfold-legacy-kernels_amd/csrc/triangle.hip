@@ -9,44 +9,49 @@
 //
 // tri_einsum_kernel: one 256 x 256 output tile of one channel per block of 8 waves (2 x 4 wave
 // tiles of 128 i x 64 j, 32 MFMA 16x16x32 accumulators each). The operands reach LDS in
-// 32-wide k slices by direct buffer->LDS loads, three slices in flight. Contraction index last:
-// 256 rows of 64 bytes per operand, each 16-byte piece XOR-swizzled by (row / 4) % 4 so the
-// sixteen rows an operand read touches fall in distinct banks. Contraction index first: 32 rows
-// of 512 bytes, read with ds_read_b64_tr_b16 (a transposed 4 x 16 block per 16-lane group),
-// pieces swizzled by 2 * (row % 4). Per slice a block moves 32 KB from L2 for 4.2 MFLOP
-// (128 flop/B). Tiles of one channel run on one XCD, whose L2 then serves both operands.
+// 64-wide k slices by direct buffer->LDS loads, two stages (the next slice loads while the
+// current one is multiplied). Contraction index last: 256 rows of 128 bytes per operand (whole
+// cache lines: 32-wide slices read half lines, 5% slower), each 16-byte piece XOR-swizzled by
+// row % 8 so the sixteen rows an operand read touches fall in distinct banks. Contraction index
+// first: 64 rows of 512 bytes, read with ds_read_b64_tr_b16 (a transposed 4 x 16 block per
+// 16-lane group), pieces swizzled by 2 * (row % 4). Per slice a block moves 64 KB from L2 for
+// 8.4 MFLOP (128 flop/B). Tiles of one channel run on one XCD, whose L2 then serves both
+// operands.
 #include "common.hpp"
 
 namespace clk {
 namespace {
 
 constexpr int kTriTile = 256;  // output tile edge
-constexpr int kTriK = 32;      // contraction slice per stage
+constexpr int kTriK = 32;      // contraction depth of one half slice (two per stage)
 
-// The twelve 16-byte fragments of one slice (four B rows, eight A rows, 1 KB apart) read from
-// LDS and waited for in one asm statement: the loop picks its stage at run time, and a read the
-// compiler can see would have to wait for every direct-to-LDS load in flight. All outputs are
-// complete when the statement ends, so no register is read before its data has arrived; the
-// "memory" clobber keeps the statement behind the barrier that publishes the stage.
-template <typename V8>
-__device__ __forceinline__ void read_fragments(uint32_t ba, uint32_t bb, V8 (&fb)[4], V8 (&fa)[8]) {
+// The twelve 16-byte fragments of one half slice (four B rows, eight A rows, 16-row blocks STRIDE
+// bytes apart) read from LDS and waited for in one asm statement: the loop picks its stage at
+// run time, and a read the compiler can see would have to wait for every direct-to-LDS load in
+// flight. All outputs are complete when the statement ends, so no register is read before its
+// data has arrived; the "memory" clobber keeps the statement behind the barrier that publishes
+// the stage.
+template <int STRIDE, typename V8>
+__device__ __forceinline__ void read_fragments_s(uint32_t ba, uint32_t bb, V8 (&fb)[4],
+                                                 V8 (&fa)[8]) {
     asm volatile(
         "ds_read_b128 %0, %13\n\t"
-        "ds_read_b128 %1, %13 offset:1024\n\t"
-        "ds_read_b128 %2, %13 offset:2048\n\t"
-        "ds_read_b128 %3, %13 offset:3072\n\t"
+        "ds_read_b128 %1, %13 offset:%14\n\t"
+        "ds_read_b128 %2, %13 offset:%15\n\t"
+        "ds_read_b128 %3, %13 offset:%16\n\t"
         "ds_read_b128 %4, %12\n\t"
-        "ds_read_b128 %5, %12 offset:1024\n\t"
-        "ds_read_b128 %6, %12 offset:2048\n\t"
-        "ds_read_b128 %7, %12 offset:3072\n\t"
-        "ds_read_b128 %8, %12 offset:4096\n\t"
-        "ds_read_b128 %9, %12 offset:5120\n\t"
-        "ds_read_b128 %10, %12 offset:6144\n\t"
-        "ds_read_b128 %11, %12 offset:7168\n\t"
+        "ds_read_b128 %5, %12 offset:%14\n\t"
+        "ds_read_b128 %6, %12 offset:%15\n\t"
+        "ds_read_b128 %7, %12 offset:%16\n\t"
+        "ds_read_b128 %8, %12 offset:%17\n\t"
+        "ds_read_b128 %9, %12 offset:%18\n\t"
+        "ds_read_b128 %10, %12 offset:%19\n\t"
+        "ds_read_b128 %11, %12 offset:%20\n\t"
         "s_waitcnt lgkmcnt(0)"
         : "=&v"(fb[0]), "=&v"(fb[1]), "=&v"(fb[2]), "=&v"(fb[3]), "=&v"(fa[0]), "=&v"(fa[1]),
           "=&v"(fa[2]), "=&v"(fa[3]), "=&v"(fa[4]), "=&v"(fa[5]), "=&v"(fa[6]), "=&v"(fa[7])
-        : "v"(ba), "v"(bb)
+        : "v"(ba), "v"(bb), "i"(STRIDE), "i"(2 * STRIDE), "i"(3 * STRIDE), "i"(4 * STRIDE),
+          "i"(5 * STRIDE), "i"(6 * STRIDE), "i"(7 * STRIDE)
         : "memory");
 }
 
@@ -88,15 +93,15 @@ __global__ __launch_bounds__(512) void tri_einsum_kernel(const typename TR::elem
                                                          int T, int ntiles) {
     using E = typename TR::elem;
     using V8 = typename TR::vec8;
-    constexpr int BT = kTriTile, KC = kTriK;
+    constexpr int BT = kTriTile, KC = 2 * kTriK;
+    constexpr int NSTG = 2;  // two stages of 64 k
     constexpr int PR = KC / 8;             // 16-byte pieces per row slice
     constexpr int SLICE = BT * PR * 16;    // bytes of one operand slice
     constexpr int NT = 512, DPW = 2 * BT * PR / NT;  // loads per lane and slice (A and B)
     static_assert(BT * PR % NT == 0, "whole load rounds");
 
-    // Three stages of (A slice, B slice).
     constexpr int STAGE = 2 * SLICE;
-    __shared__ __attribute__((aligned(16))) char smem[3 * STAGE];
+    __shared__ __attribute__((aligned(16))) char smem[NSTG * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -120,8 +125,8 @@ __global__ __launch_bounds__(512) void tri_einsum_kernel(const typename TR::elem
     const int nk = (N + KC - 1) / KC;
 
     // Slice kk of both operands into buffer st: A rows at st, B rows at st + SLICE. Piece q of
-    // LDS row r holds the row's 16-byte piece q ^ ((r >> 2) & 3); pieces past N read zeros.
-    // TN: LDS row r (k = kk*32 + r) holds the tile's 256 columns as 32 pieces; slot q holds
+    // LDS row r holds the row's 16-byte piece q ^ (r % 8); pieces past N read zeros.
+    // TN: LDS row r (k = kk*64 + r) holds the tile's 256 columns as 32 pieces; slot q holds
     // piece q ^ 2*(r % 4), so that the four rows of a transposed read fall in distinct banks.
     auto stage = [&](int kk, char* st) {
         const bool live = kk < nk;
@@ -137,7 +142,7 @@ __global__ __launch_bounds__(512) void tri_einsum_kernel(const typename TR::elem
                 voff = col < N ? ((kk * KC + row) * N + col) * 2 : kPastEnd;
             } else {
                 const int row = slot / PR;
-                const int piece = (slot % PR) ^ ((row >> 2) & (PR - 1));
+                const int piece = (slot % PR) ^ (row & 7);
                 const int kcol = kk * KC + piece * 8;
                 voff = kcol < N ? (row * N + kcol) * 2 : kPastEnd;
             }
@@ -151,12 +156,17 @@ __global__ __launch_bounds__(512) void tri_einsum_kernel(const typename TR::elem
 #pragma unroll
         for (int b = 0; b < 8; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    // Operand reads. Lane (r16, g) reads k 8g..8g+7 of row 16t + r16 of its wave's rows; the
-    // swizzle term (row / 4) % 4 is the same for every t, so one address serves all tiles of a
-    // slice with an immediate offset of 1 KB per 16 rows.
+    // Operand reads (NT). Lane (r16, g) reads k 32h + 8g .. +7 (piece 4h + g) of row 16t + r16 of
+    // its wave's rows; the swizzle term row % 8 is the same for every t, so one address per half
+    // h serves all tiles of a slice with an immediate offset of 2 KB per 16 rows.
     const uint32_t lds0 = lds_addr(smem);
-    const uint32_t rd = (uint32_t)(r16 * PR + (g ^ ((r16 >> 2) & (PR - 1)))) * 16;
-    const uint32_t rda = rd + 128 * wi * PR * 16, rdb = rd + SLICE + 64 * wj * PR * 16;
+    uint32_t rda2[2], rdb2[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint32_t rd = (uint32_t)(r16 * PR + ((4 * h + g) ^ (r16 & 7))) * 16;
+        rda2[h] = rd + 128 * wi * PR * 16;
+        rdb2[h] = rd + SLICE + 64 * wj * PR * 16;
+    }
     // TN: fragment f (it = 0..7 of A, then jt = 0..3 of B) is column block m0 = 128wi + 16it
     // (64wj + 16jt); lane 4j + t reads row 8g + j (and + 4), columns m0 + 4t .. + 3.
     uint32_t trd[12];
@@ -170,43 +180,45 @@ __global__ __launch_bounds__(512) void tri_einsum_kernel(const typename TR::elem
         }
     }
 
-    stage(0, smem);
-    __atomic_signal_fence(__ATOMIC_SEQ_CST);
-    stage(1, smem + STAGE);
-
     // X^T tile products: the A operand is B (rows j), the B operand is A (rows i), so a lane's
-    // accumulator holds four consecutive j of one i. The loop body is not unrolled (copies of it
-    // cost the register allocator more than the 256 VGPRs a lane has), so the stage buffers are
-    // picked at run time and the fragments are read by read_fragments.
+    // accumulator holds four consecutive j of one i. Two stages of 64 k: slice kk + 1 loads
+    // while slice kk is multiplied, as two halves of 32 k. The loop body is not unrolled (copies of it cost the register allocator more than
+    // the 256 VGPRs a lane has), so the stage is picked at run time and the fragments are read
+    // by asm statements.
+    stage(0, smem);
     for (int kk = 0; kk < nk; ++kk) {
-        const int cur = kk % 3, nxt = (kk + 2) % 3;
-        vm_wait<DPW>();
-        lds_barrier();  // slice kk in stage cur; every wave is done reading stage nxt
-        stage(kk + 2, smem + nxt * STAGE);
+        const int cur = kk & 1;
+        vm_wait<0>();
+        lds_barrier();  // slice kk in stage cur; every wave is done reading the other stage
+        stage(kk + 1, smem + (cur ^ 1) * STAGE);
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
-        V8 fb[4], fa[8];
-        if constexpr (TN) {
-            uint32_t ad[12];
 #pragma unroll
-            for (int f = 0; f < 12; ++f) ad[f] = lds0 + cur * STAGE + trd[f];
-            i16x4 r[24];
-            read_tr_fragments(ad, r);
+        for (int h = 0; h < 2; ++h) {
+            V8 fb[4], fa[8];
+            if constexpr (TN) {
+                // Rows 32h .. 32h+31 of the slice.
+                uint32_t ad[12];
 #pragma unroll
-            for (int f = 0; f < 12; ++f) {
-                const i16x4 lo = r[2 * f], hi = r[2 * f + 1];
-                typedef short i16x8 __attribute__((ext_vector_type(8)));
-                const i16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-                if (f < 8) fa[f] = __builtin_bit_cast(V8, v);
-                else fb[f - 8] = __builtin_bit_cast(V8, v);
+                for (int f = 0; f < 12; ++f) ad[f] = lds0 + cur * STAGE + trd[f] + h * 32 * BT * 2;
+                i16x4 r[24];
+                read_tr_fragments(ad, r);
+#pragma unroll
+                for (int f = 0; f < 12; ++f) {
+                    const i16x4 lo = r[2 * f], hi = r[2 * f + 1];
+                    typedef short i16x8 __attribute__((ext_vector_type(8)));
+                    const i16x8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+                    if (f < 8) fa[f] = __builtin_bit_cast(V8, v);
+                    else fb[f - 8] = __builtin_bit_cast(V8, v);
+                }
+            } else {
+                read_fragments_s<16 * PR * 16>(lds0 + cur * STAGE + rda2[h],
+                                               lds0 + cur * STAGE + rdb2[h], fb, fa);
             }
-        } else {
-            const uint32_t ba = lds0 + cur * STAGE + rda, bb = lds0 + cur * STAGE + rdb;
-            read_fragments(ba, bb, fb, fa);
+#pragma unroll
+            for (int it = 0; it < 8; ++it)
+#pragma unroll
+                for (int jt = 0; jt < 4; ++jt) acc[jt][it] = TR::mfma(fb[jt], fa[it], acc[jt][it]);
         }
-#pragma unroll
-        for (int it = 0; it < 8; ++it)
-#pragma unroll
-            for (int jt = 0; jt < 4; ++jt) acc[jt][it] = TR::mfma(fb[jt], fa[it], acc[jt][it]);
     }
 
     // Lane (r16, g) of accumulator (jt, it) holds X[i][j..j+3] for i = i0 + 128wi + 16it + r16,
