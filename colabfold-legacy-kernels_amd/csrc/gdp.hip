@@ -307,16 +307,17 @@ struct LnGdpWeights {
 
 constexpr int kLnGdpRows = 64;  // rows per tile
 
-// LDS plan of ln_gdp_kernel<C, N, NB> with row-major outputs. PER_CU blocks share a CU (one
-// 12-wave block at C = N = 128). Each projected tile goes out through an LDS staging buffer (two,
-// rows padded by 16 bytes) when both still fit PER_CU blocks: one store instruction then writes
-// whole output rows, which lets the stores stream past the caches (non-temporal).
-template <int C, int N, int NB>
+// LDS plan of ln_gdp_kernel<C, N, NB, CM>. PER_CU blocks share a CU (one 12-wave block at
+// C = N = 128). Each projected tile goes out through an LDS staging buffer (two, rows padded by
+// 16 bytes) when both still fit PER_CU blocks: one store instruction then writes whole output
+// rows (row-major: a position's N channels; CM: a channel's 64 positions of the tile), which lets
+// the stores stream past the caches (non-temporal).
+template <int C, int N, int NB, bool CM = false>
 struct LnGdpPlan {
     static constexpr int R = kLnGdpRows;
-    static constexpr int TILE = R * C * 2;             // a z or normalised tile
-    static constexpr int OSTR = 2 * N + 16;            // staged output row stride (bytes)
-    static constexpr int OBB = NB * R * OSTR;          // one staging buffer, every branch
+    static constexpr int TILE = R * C * 2;                // a z or normalised tile
+    static constexpr int OSTR = (CM ? 2 * R : 2 * N) + 16;  // staged output row stride (bytes)
+    static constexpr int OBB = NB * (CM ? N : R) * OSTR;    // one staging buffer, every branch
     static constexpr int PER_CU = NB == 2 ? 128 / N : (C == 128 ? 1 : 2);
     static constexpr int BASE = 5 * TILE + 2 * R * 4;  // five tiles and two row-mask vectors
     static constexpr bool STAGED_OUT = PER_CU * (BASE + 2 * OBB) <= 160 * 1024;
@@ -357,7 +358,9 @@ __device__ __forceinline__ void lds_rows(uint32_t addr, u32x4 (&r)[N]) {
 // CM = false: a and b are [M, N] row-major (the pair layout). CM = true: a and b are channel-
 // major [N, M] (a[n][m]), the operand layout of the triangle-multiplication contraction; the MFMA
 // operands swap roles (out = xhat . W') so that a lane's accumulators hold four consecutive rows
-// of one output column, stored as one 8-byte piece of that column's plane. CM needs M % 64 == 0.
+// of one output column (16 consecutive rows per lane after the four sub-tiles), staged as a
+// [channel][64 rows] tile when LDS allows and stored as whole 128-byte lines of the channels'
+// planes, else as two 16-byte pieces per lane and column. CM needs M % 64 == 0.
 // LN = false, NB = 1: the plain gated dual projection of one branch (x = z as it is; the four
 // staging waves only move z into the swizzled tile, and gamma, beta are not read).
 // Block: NB*N/32 MFMA waves, then 4 LayerNorm (staging) waves.
@@ -379,8 +382,8 @@ __global__ __launch_bounds__(64 * NB * N / 32 + 256) void ln_gdp_kernel(
     constexpr int ZB = R * C * 2;
     constexpr int DPW = (R * PL + NTL - 1) / NTL;  // 16-byte loads per LayerNorm lane and tile
     constexpr int ZBP = DPW * NTL * 16;
-    using PLAN = LnGdpPlan<C, N, NB>;
-    constexpr bool OST = !CM && PLAN::STAGED_OUT;
+    using PLAN = LnGdpPlan<C, N, NB, CM>;
+    constexpr bool OST = PLAN::STAGED_OUT;
     constexpr int OSTR = PLAN::OSTR;
 
     // Three z tiles (normalised, landing, in flight), two normalised tiles and their row masks.
@@ -549,7 +552,20 @@ __global__ __launch_bounds__(64 * NB * N / 32 + 256) void ln_gdp_kernel(
     };
     // OST: the branch's N/32 waves store its staged tile as whole rows (four instructions each).
     auto flush_staged = [&](const char* ob) {
-        store_staged_rows<R, N, OSTR, N / 32>(pend_out, ob + br * R * OSTR, cb, lane);
+        if constexpr (CM) {
+            // 64 consecutive 16-byte pieces per instruction: eight channels' 128-byte lines.
+            if (pend_plane == nullptr) return;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int f = (i * (N / 32) + cb) * 64 + lane;
+                const int ch = f >> 3, piece = f & 7;
+                __builtin_nontemporal_store(
+                    *reinterpret_cast<const u32x4*>(ob + (br * N + ch) * OSTR + piece * 16),
+                    reinterpret_cast<u32x4*>(pend_plane + (size_t)ch * M + piece * 8));
+            }
+        } else {
+            store_staged_rows<R, N, OSTR, N / 32>(pend_out, ob + br * R * OSTR, cb, lane);
+        }
     };
     auto project = [&](int t, const char* xh, const float* mrow, char* ob) {
 #pragma unroll
@@ -599,6 +615,19 @@ __global__ __launch_bounds__(64 * NB * N / 32 + 256) void ln_gdp_kernel(
             }
         }
         if constexpr (CM) {
+            if constexpr (OST) {
+                // Rows 16g .. 16g+15 of the lane's two columns, as two 16-byte pieces each.
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    const int col = 32 * cb + 8 * (r16 >> 2) + 4 * h + (r16 & 3);
+                    char* const at = ob + (br * N + col) * OSTR + 32 * g;
+#pragma unroll
+                    for (int half = 0; half < 2; ++half) {
+                        const u32x2 a = pendc[2 * half][h], b = pendc[2 * half + 1][h];
+                        *reinterpret_cast<u32x4*>(at + 16 * half) = u32x4{a[0], a[1], b[0], b[1]};
+                    }
+                }
+            }
             pend_plane = out + (size_t)t * R;
         } else {
             pend_out = out_rsrc(t);
