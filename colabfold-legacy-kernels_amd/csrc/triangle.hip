@@ -222,26 +222,37 @@ __global__ __launch_bounds__(512) void tri_einsum_kernel(const typename TR::elem
     }
 
     // Lane (r16, g) of accumulator (jt, it) holds X[i][j..j+3] for i = i0 + 128wi + 16it + r16,
-    // j = j0 + 64wj + 16jt + 4g: one 8-byte store each. Rows past N fall outside the resource;
-    // columns past N (whole groups of four, N being a multiple of 8) are skipped.
-    const Rsrc rx = buffer_rsrc(X + c * plane + (size_t)i0 * N,
-                                (uint32_t)((size_t)min(BT, N - i0) * N * 2));
+    // j = j0 + 64wj + 16jt + 4g. The tile goes out through LDS (the two stages, 128 KB, are free
+    // once every wave's last loads have landed and its last reads are done): bf16 rows of 512
+    // bytes, 16-byte pieces XOR-swizzled by row % 32, then stored by the whole block as rows of
+    // whole cache lines (an 8-byte store per lane and accumulator writes a quarter line).
+    // Rows past N fall outside the resource; columns past N (whole pieces, N being a multiple
+    // of 8) are skipped.
+    static_assert(BT * BT * 2 <= NSTG * STAGE, "the output tile fits the stages");
+    async_wait();
+    lds_barrier();
 #pragma unroll
-    for (int jt = 0; jt < 4; ++jt) {
-        const int jl = 64 * wj + 16 * jt + 4 * g;
-        if (j0 + jl >= N) continue;
+    for (int jt = 0; jt < 4; ++jt)
 #pragma unroll
         for (int it = 0; it < 8; ++it) {
-            const int il = 128 * wi + 16 * it + r16;
+            const int il = 128 * wi + 16 * it + r16, piece = 8 * wj + 2 * jt + (g >> 1);
             E e[4];
 #pragma unroll
             for (int q = 0; q < 4; ++q) e[q] = TR::from_f(acc[jt][it][q]);
             u32x2 v;
             __builtin_memcpy(&v, e, 8);
-            __builtin_amdgcn_raw_buffer_store_b64(v, rx, (il * N + j0 + jl) * 2, 0, 0);
+            *reinterpret_cast<u32x2*>(smem + (il * 32 + (piece ^ (il & 31))) * 16 + 8 * (g & 1)) =
+                v;
         }
+    lds_barrier();
+    const Rsrc rx = buffer_rsrc(X + c * plane + (size_t)i0 * N,
+                                (uint32_t)((size_t)min(BT, N - i0) * N * 2));
+#pragma unroll
+    for (int k = 0; k < BT * BT / 8 / NT; ++k) {
+        const int f = k * NT + tid, row = f >> 5, piece = f & 31;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(smem + (row * 32 + (piece ^ (row & 31))) * 16);
+        if (j0 + 8 * piece < N) buf_st16_nt(rx, (row * N + j0 + 8 * piece) * 2, 0, v);
     }
-    async_wait();  // no direct-to-LDS load may still be in flight when the workgroup ends
 }
 
 // ---------------------------------------------------------------------------------------------
