@@ -121,7 +121,7 @@ __global__ __launch_bounds__(2 * HD) void attn_gate_kernel(
     auto store = [&](Rsrc ro) { store_staged_rows<R, HD, OSTR, NW>(ro, ob, wave, lane); };
 
     const int G = gridDim.x;
-    u32x4 oa[SUB], ob2[SUB];
+    u32x4 ov0[SUB], ov1[SUB];  // the o vectors of alternate tiles
     Rsrc pend_out = out_rsrc(ntiles);  // the staged tile's rows (none before the first)
 
     // Tile t is read from xc; tile t + 2G goes into xn, which held tile t - G. Issued after xc's
@@ -164,7 +164,7 @@ __global__ __launch_bounds__(2 * HD) void attn_gate_kernel(
     // first two waits count as every later one does.
     int t = blockIdx.x;
     const Rsrc none = out_rsrc(ntiles);
-    load_o(t, oa);
+    load_o(t, ov0);
     stage(t, x0);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
     store(none);
@@ -173,17 +173,17 @@ __global__ __launch_bounds__(2 * HD) void attn_gate_kernel(
     store(none);
     // Three x buffers and two o register sets: the pattern repeats every six tiles.
     for (; t < ntiles; t += 6 * G) {
-        tile(t, x0, x2, oa, ob2);
+        tile(t, x0, x2, ov0, ov1);
         if (t + G >= ntiles) break;
-        tile(t + G, x1, x0, ob2, oa);
+        tile(t + G, x1, x0, ov1, ov0);
         if (t + 2 * G >= ntiles) break;
-        tile(t + 2 * G, x2, x1, oa, ob2);
+        tile(t + 2 * G, x2, x1, ov0, ov1);
         if (t + 3 * G >= ntiles) break;
-        tile(t + 3 * G, x0, x2, ob2, oa);
+        tile(t + 3 * G, x0, x2, ov1, ov0);
         if (t + 4 * G >= ntiles) break;
-        tile(t + 4 * G, x1, x0, oa, ob2);
+        tile(t + 4 * G, x1, x0, ov0, ov1);
         if (t + 5 * G >= ntiles) break;
-        tile(t + 5 * G, x2, x1, ob2, oa);
+        tile(t + 5 * G, x2, x1, ov1, ov0);
     }
     lds_barrier();  // the last tile is staged
     store(pend_out);
