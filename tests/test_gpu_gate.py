@@ -34,6 +34,17 @@ def test_gate_parity(cuda, n, h, sq, d, c, dtype):
     assert_close("gated", out, r, TOL[dname(dtype)]["o"])
 
 
+# Enough 64-query tiles that the resident blocks (256 at H*D = 256, 512 at 128) run two to four
+# each: the staged tile handed from one tile step to the next, and the flush of a block's last
+# tile.
+@pytest.mark.parametrize("n,h,sq,d,c", [(773, 8, 64, 32, 256), (1100, 4, 64, 32, 128)])
+def test_gate_many_tiles(cuda, n, h, sq, d, c):
+    o, x, wg, bg = case(n, h, sq, d, c, torch.bfloat16, n + c, cuda)
+    out = ops.attention_gate(o, x, wg, bg)
+    r = ref.attention_gate(np64(o), np64(x), np64(wg), np64(bg))
+    assert_close("gated", out, r, TOL["bf16"]["o"])
+
+
 def test_gate_exact_cases(cuda):
     """A zero gate pre-activation halves O exactly; saturated biases pass O or zero it exactly;
     every result lands in the [N,Sq,H*D] layout."""

@@ -76,6 +76,41 @@ def test_ln_gdp_parity(cuda, m, c, n, dtype):
     assert_close("b", b, rb, tol)
 
 
+# Row counts around the 64-row tile and the grid of 256 resident blocks per launch: one row, a
+# tile short by one and long by one, and enough tiles that blocks run two and three of them --
+# both staging buffers of the whole-row output stores and the flush of a block's last tile.
+TILE_ROWS = [1, 63, 65, 16581, 33000]
+
+
+@pytest.mark.parametrize("m", TILE_ROWS)
+@pytest.mark.parametrize("c,n", [(128, 128), (64, 64), (128, 32)])
+def test_ln_gdp_tile_boundaries(cuda, m, c, n):
+    dtype = torch.bfloat16
+    li = layer_norm_inputs(m, c, dtype, seed=m + c * 7 + n)
+    wa = gdp_weights(c, n, dtype, seed=21, bias_std=0.2)
+    wb = gdp_weights(c, n, dtype, seed=22, bias_std=0.2)
+    dev = lambda ts: tuple(t.to(cuda) for t in ts)  # noqa: E731
+    a, b = ops.ln_gated_dual_proj(li["x"].to(cuda), li["scale"].to(cuda), li["offset"].to(cuda),
+                                  dev(wa), dev(wb), li["mask"].to(cuda), 1e-5)
+    ra, rb = ref.ln_gated_dual_proj(np64(li["x"]), np64(li["scale"]), np64(li["offset"]), 1e-5,
+                                    tuple(np64(t) for t in wa), tuple(np64(t) for t in wb),
+                                    np64(li["mask"]))
+    tol = TOL[dname(dtype)]["gdp"]
+    assert_close("a", a, ra, tol)
+    assert_close("b", b, rb, tol)
+
+
+@pytest.mark.parametrize("m", TILE_ROWS)
+@pytest.mark.parametrize("k,n", [(128, 128), (64, 128)])
+def test_gdp_tile_boundaries(cuda, m, k, n):
+    dtype = torch.bfloat16
+    li = layer_norm_inputs(m, k, dtype, seed=m + k + 3 * n)
+    w = gdp_weights(k, n, dtype, seed=n + 1, bias_std=0.3)
+    out = ops.gated_dual_proj(li["x"].to(cuda), *(t.to(cuda) for t in w), li["mask"].to(cuda))
+    r = ref.gated_dual_proj(np64(li["x"]), *(np64(t) for t in w), np64(li["mask"]))
+    assert_close("gdp", out, r, TOL[dname(dtype)]["gdp"])
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=dname)
 def test_ln_gdp_offset_and_constant_rows(cuda, dtype):
     """Rows whose mean is large against their spread (|mean|/std up to 50) and constant rows
