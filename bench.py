@@ -10,8 +10,10 @@ batch, through the C ABI with preallocated buffers; inputs rotate over 3 sets (~
 the warm-up continues past W steps until T ms (default 100) have passed, because the GPU's
 clocks ramp up over its first ~20 ms of work (the first 50 steps of a process run ~8% slower
 than every later pass); the JSON line reports the warm-up steps actually run. ms_per_step is the
-median of the per-step durations (one HIP event between consecutive steps on the launch
-stream); the bracket mean, min and max are reported beside it. Secondary figures: LayerNorm
+mean over the bracket of K steps (one HIP event before the first and one after the last, a device
+synchronize on both sides, nothing recorded in between); the median, min and max of a second
+pass with an event after every step are reported beside it (those events add 2-4 us to each
+step). Every secondary figure is a bracket mean the same way. Secondary figures: LayerNorm
 forward/backward, LayerNorm + gated dual projection, the plain projection and its backward and
 the pair-bias projection on the 512x512x128 pair representation; the attention output gate of
 MSA row attention (512 rows x 256 queries, 8 x 32 heads, 256 channels); gated attention fused
@@ -115,13 +117,22 @@ def attention_step(lib, native, stream, s):
         raise RuntimeError(native.last_error())
 
 
-def timed(torch, fn, steps, warmup, stream_obj, stats=None, min_warmup_ms=0.0):
-    """Median ms per step over `steps` timed steps after `warmup` untimed ones: one HIP event on
-    the launch stream before each step and one after the last, so every step has its own
-    duration. With min_warmup_ms > 0 the warm-up continues past `warmup` steps until that much
-    wall time has passed (the GPU's clocks ramp up over its first ~20 ms of work). `stats` (a
-    dict), when given, also receives the mean over the whole bracket and the warm-up actually
-    run."""
+# Minimum warm-up wall time of every timed section (--min-warmup-ms).
+MIN_WARMUP_MS = 100.0
+
+
+def timed(torch, fn, steps, warmup, stream_obj, stats=None, min_warmup_ms=None):
+    """Mean ms per step over `steps` timed steps after `warmup` untimed ones: one HIP event on
+    the launch stream before the first step and one after the last, with a device synchronize
+    on both sides (nothing else is recorded between the steps: an event recorded after every
+    step puts a timestamp between each pair of launches, measured at 2-4 us per step on the
+    short kernels). The warm-up continues past `warmup` steps until min_warmup_ms (default
+    MIN_WARMUP_MS) of wall time has passed: the GPU's clocks ramp up over its first ~20 ms of work
+    and again after each idle stretch, such as building the next section's inputs. `stats`
+    (a dict), when given, also receives the warm-up actually run and, from a second pass of
+    `steps` steps with an event after every step, the median, min and max step."""
+    if min_warmup_ms is None:
+        min_warmup_ms = MIN_WARMUP_MS
     t0 = time.perf_counter()
     i = 0
     while i < warmup:
@@ -138,19 +149,25 @@ def timed(torch, fn, steps, warmup, stream_obj, stats=None, min_warmup_ms=0.0):
     if stats is not None:
         stats["warmup_run"] = i
         stats["warmup_ms"] = (time.perf_counter() - t0) * 1e3
-    ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
-    ev[0].record(stream_obj)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream_obj)
     for i in range(steps):
         fn(i)
-        ev[i + 1].record(stream_obj)
+    e1.record(stream_obj)
     torch.cuda.synchronize()
-    per = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
-    mid = len(per) // 2
-    median = per[mid] if len(per) % 2 else 0.5 * (per[mid - 1] + per[mid])
+    mean = e0.elapsed_time(e1) / steps
     if stats is not None:
-        stats["mean_ms"] = ev[0].elapsed_time(ev[steps]) / steps
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
+        ev[0].record(stream_obj)
+        for i in range(steps):
+            fn(i)
+            ev[i + 1].record(stream_obj)
+        torch.cuda.synchronize()
+        per = sorted(ev[i].elapsed_time(ev[i + 1]) for i in range(steps))
+        mid = len(per) // 2
+        stats["median_ms"] = per[mid] if len(per) % 2 else 0.5 * (per[mid - 1] + per[mid])
         stats["min_ms"], stats["max_ms"] = per[0], per[-1]
-    return median
+    return mean
 
 
 def per_kernel(torch, native, fn, steps):
@@ -761,7 +778,8 @@ def main(argv=None):
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--min-warmup-ms", type=float, default=100.0,
-                    help="keep warming up past --warmup steps until this much time has passed")
+                    help="keep warming up past --warmup steps until this much time has passed "
+                         "(every timed section)")
     ap.add_argument("--cpu-rows", type=int, default=N_ROWS)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-secondary", action="store_true")
@@ -785,6 +803,8 @@ def main(argv=None):
               file=sys.stderr)
         return 2
 
+    global MIN_WARMUP_MS
+    MIN_WARMUP_MS = args.min_warmup_ms
     import torch
     from colabfold_legacy_kernels import _native as native
     from colabfold_legacy_kernels import workloads
@@ -802,8 +822,7 @@ def main(argv=None):
 
     print("bench: timing attention fwd+bwd", file=sys.stderr, flush=True)
     step_stats = {}
-    ms = timed(torch, step, args.steps, args.warmup, so, step_stats,
-               min_warmup_ms=args.min_warmup_ms)
+    ms = timed(torch, step, args.steps, args.warmup, so, step_stats)
     fl = attention_flops(N_ROWS, HEADS, NRES, NRES, HEAD_DIM)
     tflops = fl["step"] / (ms * 1e-3) / 1e12
     kernels = per_kernel(torch, native, step, args.steps)
@@ -821,7 +840,7 @@ def main(argv=None):
         "metric": METRIC, "value": tflops, "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "warmup_run": step_stats["warmup_run"],
         "warmup_ms": step_stats["warmup_ms"], "ms_per_step": ms,
-        "ms_per_step_mean": step_stats["mean_ms"], "ms_per_step_min": step_stats["min_ms"],
+        "ms_per_step_median": step_stats["median_ms"], "ms_per_step_min": step_stats["min_ms"],
         "ms_per_step_max": step_stats["max_ms"],
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic",
