@@ -72,6 +72,11 @@ PROTOTYPES = {
                                  c_void_p, c_i64, c_i64, c_i64, c_f32]),
     "clk_attention_gate": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
                                    c_void_p, c_i64, c_i64, c_i64, c_i64, c_i64]),
+    "clk_attention_gate_bwd_workspace_size": (c_size, [c_i64, c_i64, c_i64, c_i64, c_i64]),
+    "clk_attention_gate_bwd": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+                                       c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                       c_void_p, c_size, c_i64, c_i64, c_i64, c_i64, c_i64,
+                                       c_int]),
     "clk_triangle_einsum": (c_int, [c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_i64,
                                     c_i64]),
     "clk_triangle_multiply_workspace_size": (c_size, [c_i64, c_i64]),

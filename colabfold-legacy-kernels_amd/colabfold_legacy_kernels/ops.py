@@ -26,7 +26,7 @@ from . import _native
 __all__ = [
     "ClkError", "InvalidArgument", "InternalError",
     "attention", "attention_fwd", "attention_bwd",
-    "attention_gate", "attention_gated", "attention_gated_fwd",
+    "attention_gate", "attention_gate_bwd", "attention_gated", "attention_gated_fwd",
     "layer_norm", "layer_norm_bwd",
     "gated_dual_proj", "ln_gated_dual_proj",
     "AttentionFunction", "LayerNormFunction",
@@ -413,6 +413,44 @@ def attention_gate(o, x, wg, bg):
         _check(_native.lib().clk_attention_gate(_stream(dev), code, _ptr(o), _ptr(x), _ptr(wg),
                                                 _ptr(bg), _ptr(out), n, h, sq, d, c))
     return out
+
+
+def attention_gate_bwd(o, x, wg, bg, dout, dx=None):
+    """Gradients of attention_gate for dout [N,Sq,H*D]: (do, dx, dwg, dbg) with do [N,H,Sq,D]
+    (the dout of attention_bwd) and dx [N,Sq,C] in o's dtype, dwg [C,H*D] and dbg [H*D] float32.
+    If dx is given, the input gradient is added to it in place (x also feeds the q, k, v
+    projections)."""
+    what = "attention_gate_bwd"
+    dev = _require([("o", o), ("x", x), ("wg", wg), ("bg", bg), ("dout", dout), ("dx", dx)],
+                   what)
+    _shape_check(o.dim() == 4, what, "o must be [N,H,Sq,D]")
+    n, h, sq, d = o.shape
+    _shape_check(x.dim() == 3 and tuple(x.shape[:2]) == (n, sq), what, "x must be [N,Sq,C]")
+    c = x.shape[2]
+    _shape_check(tuple(wg.shape) == (c, h * d), what, "wg must be [C,H*D]")
+    _shape_check(tuple(bg.shape) == (h * d,), what, "bg must be [H*D]")
+    _shape_check(tuple(dout.shape) == (n, sq, h * d), what, "dout must be [N,Sq,H*D]")
+    _shape_check(all(t.dtype == o.dtype for t in (x, wg, bg, dout)), what,
+                 "all operands must share one dtype")
+    code = _dtype_code(o, (_native.F16, _native.BF16), what)
+    acc = dx is not None
+    if acc:
+        _shape_check(tuple(dx.shape) == (n, sq, c) and dx.dtype == o.dtype, what,
+                     "dx must be [N,Sq,C] of o's dtype")
+    else:
+        dx = torch.empty_like(x)
+    do = torch.empty_like(o)
+    f32 = dict(device=dev, dtype=torch.float32)
+    dwg, dbg = torch.empty((c, h * d), **f32), torch.empty(h * d, **f32)
+    lib = _native.lib()
+    wsb = lib.clk_attention_gate_bwd_workspace_size(n, h, sq, d, c)
+    ws = torch.empty(max(wsb, 1), device=dev, dtype=torch.uint8)
+    with torch.cuda.device(dev):
+        _check(lib.clk_attention_gate_bwd(_stream(dev), code, _ptr(o), _ptr(x), _ptr(wg),
+                                          _ptr(bg), _ptr(dout), _ptr(do), _ptr(dx), _ptr(dwg),
+                                          _ptr(dbg), _ptr(ws), wsb, n, h, sq, d, c,
+                                          1 if acc else 0))
+    return do, dx, dwg, dbg
 
 
 def _gated_call(q, k, v, bias, kmask, x, wg, bg, scale, residuals, what):

@@ -266,6 +266,28 @@ clk_status clk_attention_gate(hipStream_t stream, clk_dtype dtype, const void* o
                               int64_t Sq, int64_t D, int64_t C);
 
 /*
+ * Backward of the gated attention output (new; the reference has neither the gate nor any
+ * backward): for out = clk_attention_gate(o, x, wg, bg) and the incoming gradient dout
+ * [N,Sq,H*D], with s = sigmoid(x.wg + bg) recomputed,
+ *   d_o = dout * s           in o's layout [N,H,Sq,D] (the dout of clk_attention_bwd),
+ *   dg  = dout * o * s * (1 - s),  dx = dg.wg^T [N,Sq,C] (added to the existing dx when
+ *   accumulate_dx != 0: x also feeds the q, k, v projections),
+ *   dwg = x^T.dg [C,H*D] and dbg = sum of dg over the N*Sq rows [H*D], both float32.
+ * o, x, wg, bg, dout, d_o, dx of dtype CLK_F16 or CLK_BF16 (o, x, wg, dout, d_o, dx and the
+ * workspace 16-byte aligned); C and H*D each 64, 128 or 256; D a multiple of 8; each operand
+ * under 1 GiB. Deterministic: dwg and dbg are summed from per-block partials in a fixed order.
+ * Workspace: clk_attention_gate_bwd_workspace_size bytes (dg in the input dtype and the
+ * partials). N*Sq = 0 writes zero dwg and dbg.
+ */
+size_t clk_attention_gate_bwd_workspace_size(int64_t N, int64_t H, int64_t Sq, int64_t D,
+                                             int64_t C);
+clk_status clk_attention_gate_bwd(hipStream_t stream, clk_dtype dtype, const void* o,
+                                  const void* x, const void* wg, const void* bg, const void* dout,
+                                  void* d_o, void* dx, float* dwg, float* dbg, void* workspace,
+                                  size_t workspace_bytes, int64_t N, int64_t H, int64_t Sq,
+                                  int64_t D, int64_t C, int accumulate_dx);
+
+/*
  * Triangle-multiplication contraction, per channel (new; the reference stops at the gated
  * projection): x[c] = a[c] . b[c]^T for a, b, x [C][N][N] row-major, i.e. channel-major with the
  * contraction index last. With a[c][i][k] = a_pair[i,k,c] this is the outgoing update

@@ -210,6 +210,35 @@ def test_attention_gate_validation(n, h, sq, d, c, msg):
     assert msg in _native.last_error()
 
 
+def gate_bwd(**kw):
+    a = dict(stream=None, dtype=BF16, o=FAKE, x=FAKE, wg=FAKE, bg=FAKE, dout=FAKE, d_o=FAKE,
+             dx=FAKE, dwg=FAKE, dbg=FAKE, workspace=FAKE, workspace_bytes=1 << 40, N=2, H=8,
+             Sq=70, D=32, C=256, accumulate_dx=0)
+    a.update(kw)
+    return _native.lib().clk_attention_gate_bwd(*a.values())
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(dtype=F32), "dtype"), (dict(D=12, H=4), "multiple of 8"), (dict(H=0), "H > 0"),
+    (dict(C=96), "64, 128 or 256"), (dict(H=3), "64, 128 or 256"),
+    (dict(N=1 << 20, Sq=8), "too many"), (dict(dwg=None), "null gradient"),
+    (dict(o=None), "null operand"), (dict(workspace=None), "null operand"),
+    (dict(d_o=FAKE + 8), "aligned"), (dict(wg=FAKE + 8), "aligned"),
+    (dict(workspace_bytes=4096), "workspace"),
+])
+def test_attention_gate_bwd_validation(kw, msg):
+    assert gate_bwd(**kw) == INVALID
+    assert msg in _native.last_error()
+
+
+def test_attention_gate_bwd_workspace_size():
+    lib = _native.lib()
+    ws = lib.clk_attention_gate_bwd_workspace_size(512, 8, 256, 32, 256)
+    assert ws >= 512 * 256 * 256 * 2  # dg in the input dtype, then the partials
+    assert ws == lib.clk_attention_gate_bwd_workspace_size(512, 8, 256, 32, 256)
+    assert lib.clk_attention_gate_bwd_workspace_size(0, 8, 256, 32, 256) == 0
+
+
 def attn_gated(**kw):
     a = dict(stream=None, dtype=BF16, q=FAKE, k=FAKE, v=FAKE, bias=FAKE, kmask=FAKE, x=FAKE,
              wg=FAKE, bg=FAKE, gated=FAKE, out=None, lse=None, N=2, H=2, Sq=16, Sk=16, D=32,

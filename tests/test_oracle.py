@@ -326,6 +326,47 @@ def test_gate_matches_torch():
                                atol=1e-15)
 
 
+def test_gate_bwd_matches_torch_autograd():
+    """The gate's backward against float64 autograd of the gate written out in torch (per-head
+    einsum form, no transpose shared with the oracle)."""
+    n, h, sq, d, c = 2, 3, 5, 4, 6
+    o, x, wg, bg = gate_case(12, n=n, h=h, sq=sq, d=d, c=c)
+    dout = np.random.default_rng(13).standard_normal((n, sq, h * d))
+    to, tx, twg, tbg = (T(a).requires_grad_() for a in (o, x, wg, bg))
+    gate = torch.sigmoid(torch.einsum("nsc,chd->nshd", tx, twg.reshape(c, h, d)) +
+                         tbg.reshape(h, d))
+    out = torch.einsum("nhsd,nshd->nshd", to, gate).reshape(n, sq, h * d)
+    out.backward(T(dout))
+    got = GT.attention_gate_bwd(o, x, wg, bg, dout)
+    for name, a, b in zip(("do", "dx", "dwg", "dbg"), got,
+                          (to.grad, tx.grad, twg.grad, tbg.grad)):
+        assert a.shape == tuple(b.shape), name
+        np.testing.assert_allclose(a, b.numpy(), rtol=1e-12, atol=1e-13, err_msg=name)
+
+
+def test_gate_bwd_central_finite_differences():
+    """Every gradient of the gate's backward against central differences of attention_gate."""
+    o, x, wg, bg = gate_case(14, n=1, h=2, sq=3, d=2, c=3)
+    dout = np.random.default_rng(15).standard_normal((1, 3, 4))
+    grads = GT.attention_gate_bwd(o, x, wg, bg, dout)
+
+    def f(oo, xx, ww, bb):
+        return float((GT.attention_gate(oo, xx, ww, bb) * dout).sum())
+
+    args = [o, x, wg, bg]
+    r = np.random.default_rng(16)
+    eps = 1e-6
+    for which in range(4):
+        for _ in range(5):
+            idx = tuple(r.integers(0, s) for s in args[which].shape)
+            plus = [a.copy() for a in args]
+            minus = [a.copy() for a in args]
+            plus[which][idx] += eps
+            minus[which][idx] -= eps
+            fd = (f(*plus) - f(*minus)) / (2 * eps)
+            assert abs(fd - grads[which][idx]) < 1e-7 * max(1.0, abs(fd)), (which, idx)
+
+
 def test_pair_block_composes_the_ops():
     r = np.random.default_rng(5)
     z = r.standard_normal((6, 6, 16))
