@@ -16,9 +16,10 @@ pass with an event after every step are reported beside it (those events add 2-4
 step). Every secondary figure is a bracket mean the same way. Secondary figures: LayerNorm
 forward/backward, LayerNorm + gated dual projection, the plain projection and its backward and
 the pair-bias projection on the 512x512x128 pair representation; the attention output gate of
-MSA row attention (512 rows x 256 queries, 8 x 32 heads, 256 channels); gated attention fused
-and separate on MSA rows and at N_res = 1024; the triangle multiplication (outgoing, incoming)
-on z [512,512,128] per kernel; the library's streaming copy as the HBM ceiling.
+MSA row attention (512 rows x 256 queries, 8 x 32 heads, 256 channels) and its backward; gated
+attention fused and separate on MSA rows and at N_res = 1024; the triangle multiplication
+(outgoing, incoming) on z [512,512,128] per kernel; the library's streaming copy as the HBM
+ceiling.
 
 The roofline block names the kernel with the most time per step, its algorithmic work per launch
 divided by its average duration from per-launch HIP events on the launch stream (the library's
@@ -405,6 +406,48 @@ def bench_attn_gate(torch, native, dev, stream, steps, warmup):
     return {"attn_gate_GBps": nbytes / (t * 1e-3) / 1e9, "attn_gate_ms": t,
             "attn_gate_kernel_ms": k.get("attn_gate", {}).get("avg_ms"),
             "attn_gate_bytes": nbytes}
+
+
+def bench_attn_gate_bwd(torch, native, dev, stream, steps, warmup):
+    """Backward of the MSA row attention's output gate (the shapes of bench_attn_gate, dout
+    ~N(0,1), bg ~N(0,0.25)): do, dx, dwg, dbg; rotates 2 sets (~0.8 GB). Bytes counted: one read
+    of o, x and dout and one write of do and dx (the op's inputs and outputs; the kernels also
+    write and re-read the gate-logit gradient dg and re-read x for dwg)."""
+    n, h, sq, d, c = 512, 8, 256, 32, 256
+    lib = native.lib()
+    bf = dict(dtype=torch.bfloat16, device=dev)
+    wsb = lib.clk_attention_gate_bwd_workspace_size(n, h, sq, d, c)
+    sets = []
+    for r in range(2):
+        g = torch.Generator(device="cpu").manual_seed(70 + r)
+        o = torch.randn((n, h, sq, d), generator=g).to(**bf)
+        x = torch.randn((n, sq, c), generator=g).to(**bf)
+        wg = (torch.randn((c, h * d), generator=g) / c ** 0.5).to(**bf)
+        bg = (0.5 * torch.randn(h * d, generator=g)).to(**bf)
+        dout = torch.randn((n, sq, h * d), generator=g).to(**bf)
+        outs = (torch.empty_like(o), torch.empty_like(x),
+                torch.empty((c, h * d), device=dev), torch.empty(h * d, device=dev),
+                torch.empty(wsb, dtype=torch.uint8, device=dev))
+        sets.append((o, x, wg, bg, dout) + outs)
+
+    def run(i):
+        o, x, wg, bg, dout, do, dx, dwg, dbg, ws = sets[i % len(sets)]
+        st = lib.clk_attention_gate_bwd(stream, native.BF16, o.data_ptr(), x.data_ptr(),
+                                        wg.data_ptr(), bg.data_ptr(), dout.data_ptr(),
+                                        do.data_ptr(), dx.data_ptr(), dwg.data_ptr(),
+                                        dbg.data_ptr(), ws.data_ptr(), wsb, n, h, sq, d, c, 0)
+        if st != 0:
+            raise RuntimeError(native.last_error())
+
+    so = torch.cuda.current_stream(dev)
+    t = timed(torch, run, steps, warmup, so)
+    nbytes = 2.0 * n * sq * (2 * h * d + c) + 2.0 * n * sq * (h * d + c)
+    k = per_kernel(torch, native, run, steps)
+    res = {"attn_gate_bwd_GBps": nbytes / (t * 1e-3) / 1e9, "attn_gate_bwd_ms": t,
+           "attn_gate_bwd_bytes": nbytes}
+    for name in ("gate_bwd_grad", "gate_bwd_dx", "gate_bwd_dw", "gate_bwd_sum"):
+        res[name + "_ms"] = k.get(name, {}).get("avg_ms")
+    return res
 
 
 def bench_gated_attention(torch, workloads, native, dev, stream, steps, warmup):
@@ -879,6 +922,8 @@ def main(argv=None):
         print("bench: timing the attention output gate", file=sys.stderr, flush=True)
         sec.update(bench_attn_gate(torch, native, dev, stream, args.steps, args.warmup))
         sec["attn_gate_frac_hbm"] = sec["attn_gate_GBps"] / HBM_PEAK
+        print("bench: timing the attention output gate backward", file=sys.stderr, flush=True)
+        sec.update(bench_attn_gate_bwd(torch, native, dev, stream, args.steps, args.warmup))
         print("bench: timing gated attention, fused and separate", file=sys.stderr, flush=True)
         sec.update(bench_gated_attention(torch, workloads, native, dev, stream, args.steps,
                                          args.warmup))

@@ -43,6 +43,7 @@ _TABLE = {
     "layer_norm_bwd": ((_ARCH, _LIB, "ClkLayerNormBwd"),),
     "ln_gated_dual_proj": ((_ARCH, _LIB, "ClkLnGdp"),),
     "attention_gate": ((_ARCH, _LIB, "ClkAttentionGate"),),
+    "attention_gate_bwd": ((_ARCH, _LIB, "ClkAttentionGateBwd"),),
     "attention_gated": ((_ARCH, _LIB, "ClkAttentionGated"),),
     "attention_nshd": ((_ARCH, _LIB, "ClkAttentionNshd"),),
     "attention_bwd_nshd": ((_ARCH, _LIB, "ClkAttentionBwdNshd"),),

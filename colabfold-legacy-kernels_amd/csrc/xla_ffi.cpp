@@ -24,6 +24,9 @@
 //   ClkLnGdp          z, ln_scale, ln_offset, wpa, bpa, wga, bga, wpb, bpb, wgb, bgb, mask
 //                     -> a, b; attribute eps
 //   ClkAttentionGate  o [N,H,Sq,D], x [N,Sq,C], wg [C,H*D], bg [H*D] -> out [N,Sq,H*D]
+//   ClkAttentionGateBwd  o, x, wg, bg, dout [N,Sq,H*D] -> do [N,H,Sq,D], dx [N,Sq,C], dwg (f32
+//                     [C,H*D]), dbg (f32 [H*D]), workspace (u8,
+//                     clk_attention_gate_bwd_workspace_size bytes)
 //   ClkLnPairBias     z [..., C], scale, offset (f32 [C]), w [C,H] -> bias [H, ...]; attribute eps
 //   ClkGdpBwd         x, wp, bp, wg, bg, mask, dout -> dx, dwp, dbp, dwg, dbg (f32), workspace (u8,
 //                     clk_gated_dual_proj_bwd_workspace_size bytes)
@@ -417,6 +420,37 @@ clk_status attention_gate(const Frame& f) {
                               bg->data, out->data, N, H, Sq, D, C);
 }
 
+clk_status attention_gate_bwd(const Frame& f) {
+    const char* who = "ClkAttentionGateBwd";
+    if (f.nargs() != 5 || f.nrets() != 5)
+        return bad(who, "expects 5 operands (o, x, wg, bg, dout) and 5 results (do, dx, dwg, dbg, "
+                        "workspace)");
+    const Buffer *o = f.arg(0), *x = f.arg(1), *wg = f.arg(2), *bg = f.arg(3), *dout = f.arg(4);
+    const Buffer *dO = f.ret(0), *dx = f.ret(1), *dwg = f.ret(2), *dbg = f.ret(3), *ws = f.ret(4);
+    if (!o || !x || !wg || !bg || !dout || !dO || !dx || !dwg || !dbg || !ws)
+        return bad(who, "operands and results must be buffers");
+    if (o->rank != 4) return bad(who, "o must be [N,H,Sq,D]");
+    const int64_t N = o->dims[0], H = o->dims[1], Sq = o->dims[2], D = o->dims[3];
+    if (x->rank != 3 || x->dims[0] != N || x->dims[1] != Sq) return bad(who, "x must be [N,Sq,C]");
+    const int64_t C = x->dims[2];
+    if (!dims_are(wg, {C, H * D}) || !dims_are(bg, {H * D}) || !dims_are(dout, {N, Sq, H * D}))
+        return bad(who, "wg [C,H*D], bg [H*D], dout [N,Sq,H*D] expected");
+    if (!dims_are(dO, {N, H, Sq, D}) || !dims_are(dx, {N, Sq, C}))
+        return bad(who, "do [N,H,Sq,D] and dx [N,Sq,C] expected");
+    const DataType t = o->dtype;
+    if (!half_type(t) || x->dtype != t || wg->dtype != t || bg->dtype != t || dout->dtype != t ||
+        dO->dtype != t || dx->dtype != t)
+        return bad(who, "o, x, wg, bg, dout, do, dx must be all f16 or all bf16");
+    if (!dims_are(dwg, {C, H * D}) || !dims_are(dbg, {H * D}) || dwg->dtype != kF32 ||
+        dbg->dtype != kF32)
+        return bad(who, "dwg f32 [C,H*D] and dbg f32 [H*D] expected");
+    if (ws->dtype != kU8) return bad(who, "fifth result must be the u8 workspace");
+    return clk_attention_gate_bwd(f.stream(), static_cast<clk_dtype>(t), o->data, x->data,
+                                  wg->data, bg->data, dout->data, dO->data, dx->data,
+                                  static_cast<float*>(dwg->data), static_cast<float*>(dbg->data),
+                                  ws->data, (size_t)numel(ws), N, H, Sq, D, C, 0);
+}
+
 clk_status ln_pair_bias(const Frame& f) {
     const char* who = "ClkLnPairBias";
     if (f.nargs() != 4 || f.nrets() != 1)
@@ -558,6 +592,9 @@ CLK_FFI_EXPORT Error* ClkLnGdp(CallFrame* frame) {
 }
 CLK_FFI_EXPORT Error* ClkAttentionGate(CallFrame* frame) {
     return run(frame, [](const Frame& f) { return attention_gate(f); });
+}
+CLK_FFI_EXPORT Error* ClkAttentionGateBwd(CallFrame* frame) {
+    return run(frame, [](const Frame& f) { return attention_gate_bwd(f); });
 }
 CLK_FFI_EXPORT Error* ClkLnPairBias(CallFrame* frame) {
     return run(frame, [](const Frame& f) { return ln_pair_bias(f); });

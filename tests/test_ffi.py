@@ -14,7 +14,7 @@ pytestmark = pytest.mark.skipif(not clk.available("gfx950"), reason="library not
 TARGETS = ["VoltaMma", "VoltaWmma", "ClkAttentionFwd", "ClkAttentionBwd", "VoltaLayerNorm",
            "ClkLayerNormBwd", "VoltaGdp", "VoltaGdpWmma", "ClkLnGdp", "ClkAttentionGate",
            "ClkAttentionGated", "ClkAttentionNshd", "ClkAttentionBwdNshd", "ClkLnPairBias",
-           "ClkGdpBwd", "ClkTriangleMultiply"]
+           "ClkGdpBwd", "ClkTriangleMultiply", "ClkAttentionGateBwd"]
 FAKE = 0x100000
 
 
@@ -154,6 +154,34 @@ def test_attention_gate_decode_errors(lib):
     fr = x.frame([x.buffer(BF16, (2, 8, 16, 32), FAKE)], [x.buffer(BF16, (2, 16, 256), FAKE)], [])
     assert x.call(lib, "ClkAttentionGate", fr) is not None
     assert "4 operands" in x.errors[-1][1]
+
+
+def test_attention_gate_bwd_decode_errors(lib):
+    x = FakeXla()
+    ins = [x.buffer(BF16, (2, 8, 16, 32), FAKE), x.buffer(BF16, (2, 16, 256), FAKE),
+           x.buffer(BF16, (256, 256), FAKE), x.buffer(BF16, (256,), FAKE),
+           x.buffer(BF16, (2, 16, 256), FAKE)]
+    outs = [x.buffer(BF16, (2, 8, 16, 32), FAKE), x.buffer(BF16, (2, 16, 256), FAKE),
+            x.buffer(F32, (256, 256), FAKE), x.buffer(F32, (256,), FAKE),
+            x.buffer(U8, (1 << 20,), FAKE)]
+    fr = x.frame(ins[:4], outs, [])
+    assert x.call(lib, "ClkAttentionGateBwd", fr) is not None
+    assert "5 operands" in x.errors[-1][1]
+    fr = x.frame(ins[:4] + [x.buffer(BF16, (2, 16, 128), FAKE)], outs, [])
+    assert x.call(lib, "ClkAttentionGateBwd", fr) is not None
+    assert "dout [N,Sq,H*D]" in x.errors[-1][1]
+    fr = x.frame(ins, [x.buffer(BF16, (2, 16, 256), FAKE)] + outs[1:], [])
+    assert x.call(lib, "ClkAttentionGateBwd", fr) is not None
+    assert "do [N,H,Sq,D]" in x.errors[-1][1]
+    fr = x.frame(ins, outs[:2] + [x.buffer(BF16, (256, 256), FAKE)] + outs[3:], [])
+    assert x.call(lib, "ClkAttentionGateBwd", fr) is not None
+    assert "dwg f32" in x.errors[-1][1]
+    fr = x.frame(ins, outs[:4] + [x.buffer(F32, (1 << 18,), FAKE)], [])
+    assert x.call(lib, "ClkAttentionGateBwd", fr) is not None
+    assert "u8 workspace" in x.errors[-1][1]
+    fr = x.frame(ins, outs[:4] + [x.buffer(U8, (64,), FAKE)], [])
+    assert x.call(lib, "ClkAttentionGateBwd", fr) is not None
+    assert "workspace" in x.errors[-1][1]
 
 
 def test_attention_gated_decode_errors(lib):

@@ -147,8 +147,8 @@ def test_layer_norm_and_gdp_targets(cuda):
 
 
 def test_new_targets_match_the_c_abi(cuda):
-    """ClkAttentionGate, ClkAttentionGated, ClkAttentionNshd, ClkLnPairBias, ClkGdpBwd and
-    ClkTriangleMultiply on device buffers."""
+    """ClkAttentionGate, ClkAttentionGateBwd, ClkAttentionGated, ClkAttentionNshd, ClkLnPairBias,
+    ClkGdpBwd and ClkTriangleMultiply on device buffers."""
     lib, x = lib_and_runtime(cuda)
     g = torch.Generator().manual_seed(21)
     bf = lambda *s, std=1.0: (torch.randn(s, generator=g) * std).to(torch.bfloat16).to(cuda)  # noqa
@@ -160,6 +160,21 @@ def test_new_targets_match_the_c_abi(cuda):
     assert x.call(lib, "ClkAttentionGate", fr) is None, x.errors
     torch.cuda.synchronize()
     assert torch.equal(out, ops.attention_gate(o, xin, wgt, bgt))
+
+    dgate = bf(2, 40, 256)
+    gws = lib.clk_attention_gate_bwd_workspace_size
+    gws.restype = ctypes.c_size_t
+    gws.argtypes = [ctypes.c_int64] * 5
+    ws = torch.empty(gws(2, 8, 40, 32, 256), dtype=torch.uint8, device=cuda)
+    grets = [torch.empty_like(o), torch.empty_like(xin), torch.empty((256, 256), device=cuda),
+             torch.empty((256,), device=cuda)]
+    fr = x.frame([buf(x, t) for t in (o, xin, wgt, bgt, dgate)],
+                 [buf(x, t) for t in grets] + [buf(x, ws)])
+    assert x.call(lib, "ClkAttentionGateBwd", fr) is None, x.errors
+    ref = ops.attention_gate_bwd(o, xin, wgt, bgt, dgate)
+    torch.cuda.synchronize()
+    for a, b in zip(grets, ref):
+        assert torch.equal(a, b)
 
     q, k, v = bf(2, 8, 40, 32), bf(2, 8, 40, 32), bf(2, 8, 40, 32)
     ab, km = bf(8, 40, 40), (torch.rand((2, 40), generator=g) > 0.2).to(torch.uint8).to(cuda)
