@@ -29,7 +29,7 @@ __all__ = [
     "attention_gate", "attention_gate_bwd", "attention_gated", "attention_gated_fwd",
     "layer_norm", "layer_norm_bwd",
     "gated_dual_proj", "ln_gated_dual_proj",
-    "AttentionFunction", "LayerNormFunction",
+    "AttentionFunction", "GatedAttentionFunction", "LayerNormFunction",
 ]
 
 
@@ -560,6 +560,33 @@ class AttentionFunction(torch.autograd.Function):
         dq, dk, dv, dbias = attention_bwd(q, k, v, bias, kmask, out, dout.contiguous(), lse,
                                           ctx.scale)
         return dq, dk, dv, dbias.to(bias.dtype), None, None
+
+
+class GatedAttentionFunction(torch.autograd.Function):
+    """Differentiable gated attention, o(q, k, v, bias, kmask) * sigmoid(x.wg + bg) in the output
+    projection's [N,Sq,H*D] layout. forward: attention_gated_fwd (one launch) when fused, else
+    attention_fwd then attention_gate (the faster pair on MSA row shapes); both keep the ungated
+    output and the logsumexp. backward: attention_gate_bwd (do, dx, dwg, dbg), then
+    attention_bwd with that do. Gradients for q, k, v, bias, x, wg, bg."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, bias, kmask, x, wg, bg, scale, fused=False):
+        if fused:
+            gated, out, lse = attention_gated_fwd(q, k, v, bias, kmask, x, wg, bg, scale)
+        else:
+            out, lse = attention_fwd(q, k, v, bias, kmask, scale)
+            gated = attention_gate(out, x, wg, bg)
+        ctx.save_for_backward(q, k, v, bias, kmask, x, wg, bg, out, lse)
+        ctx.scale = scale
+        return gated
+
+    @staticmethod
+    def backward(ctx, dgated):
+        q, k, v, bias, kmask, x, wg, bg, out, lse = ctx.saved_tensors
+        do, dx, dwg, dbg = attention_gate_bwd(out, x, wg, bg, dgated.contiguous())
+        dq, dk, dv, dbias = attention_bwd(q, k, v, bias, kmask, out, do, lse, ctx.scale)
+        return (dq, dk, dv, dbias.to(bias.dtype), None, dx, dwg.to(wg.dtype), dbg.to(bg.dtype),
+                None, None)
 
 
 class LayerNormFunction(torch.autograd.Function):

@@ -1,11 +1,15 @@
 """Backward of the gated attention output on the GPU against the float64 oracle: parity over every
 supported (C, H*D) pair, ragged row counts and many tiles per block, exact special cases that pin
-the layouts, dx accumulation, repeatability and the MSA-size workload."""
+the layouts, dx accumulation, repeatability and the MSA-size workload; and gated attention's
+whole forward + backward through ops.GatedAttentionFunction against the oracle's composition
+(attention, gate, gate backward, attention backward)."""
 import pytest
 import torch
 
 from _util import TOL, assert_close, dname, np64
 from colabfold_legacy_kernels import ops
+from colabfold_legacy_kernels.workloads import attention_inputs, gate_inputs
+from oracle import attention as ref_attn
 from oracle import gate as ref
 
 pytestmark = pytest.mark.gpu
@@ -107,3 +111,32 @@ def test_gate_bwd_msa_workload(cuda):
     for u, v in zip(a, b):
         assert torch.equal(u, v)
     check(a, *t, TOL["bf16"]["grad"])
+
+
+@pytest.mark.parametrize("fused", [False, True], ids=["separate", "fused"])
+@pytest.mark.parametrize("n,h,sq,sk,d,c,tail", [(2, 8, 70, 70, 32, 256, 0.1),
+                                                (3, 4, 64, 64, 32, 128, 0.0),
+                                                (2, 4, 33, 40, 16, 64, 0.2)])
+def test_gated_attention_autograd(cuda, n, h, sq, sk, d, c, tail, fused):
+    """Gradients of q, k, v, bias, x, wg and bg through the library's gated attention (forward
+    fused or as two launches; backward = gate backward, then attention backward) against the
+    float64 oracle's chain."""
+    dt = torch.bfloat16
+    inp = attention_inputs(n, h, sq, sk, d, dt, seed=sq + c, masked_tail=tail, with_dout=False)
+    x, wg, bg = gate_inputs(n, sq, c, h * d, dt, seed=sq + c, bias_std=0.5)
+    dgated = torch.randn((n, sq, h * d), generator=torch.Generator().manual_seed(7)).to(dt)
+    kmask, scale = inp["kmask"], inp["scale"]
+    host = [inp["q"], inp["k"], inp["v"], inp["bias"], x, wg, bg]
+    q, k, v, b, xx, w, bb = (t.to(cuda).requires_grad_(True) for t in host)
+    gated = ops.GatedAttentionFunction.apply(q, k, v, b, kmask.to(cuda), xx, w, bb, scale, fused)
+    gated.backward(dgated.to(cuda))
+    qh, kh, vh, bh = (np64(t) for t in host[:4])
+    o, _ = ref_attn.attention_fwd(qh, kh, vh, bh, kmask.numpy(), scale)
+    r_do, r_dx, r_dwg, r_dbg = ref.attention_gate_bwd(o, np64(x), np64(wg), np64(bg),
+                                                      np64(dgated))
+    rq, rk, rv, rb = ref_attn.attention_bwd(qh, kh, vh, bh, kmask.numpy(), scale, r_do)
+    tol = TOL["bf16"]["grad"]
+    for name, t, r in (("dq", q, rq), ("dk", k, rk), ("dv", v, rv), ("dbias", b, rb),
+                       ("dx", xx, r_dx), ("dwg", w, r_dwg), ("dbg", bb, r_dbg)):
+        assert t.grad is not None and t.grad.dtype == dt, name
+        assert_close(name, t.grad, r, tol)
