@@ -54,7 +54,7 @@ def test_attention_fwd_bwd_graph(cuda):
 
 def test_attention_layouts_gates_and_pair_bias_graph(cuda):
     """The [N,S,H,D] forward and backward, the forward with the gate fused, the separate gate and
-    the pair-bias projection."""
+    its backward, and the pair-bias projection."""
     inp = attention_inputs(2, 4, 70, 96, 32, torch.bfloat16, seed=23, device=cuda,
                            masked_tail=0.1, masked_rows=1)
     q, k, v, bias, km, s = (inp[n] for n in ("q", "k", "v", "bias", "kmask", "scale"))
@@ -65,13 +65,15 @@ def test_attention_layouts_gates_and_pair_bias_graph(cuda):
     sc = (1.0 + 0.1 * torch.randn(128, generator=g)).to(cuda)
     of = (0.1 * torch.randn(128, generator=g)).to(cuda)
     w = (torch.randn((128, 4), generator=g) / 11.3).to(torch.bfloat16).to(cuda)
+    dgate = torch.randn((2, 70, 128), generator=g).to(torch.bfloat16).to(cuda)
 
     def step():
         o = ops.attention(q, k, v, bias, km, s)
         os_, lse = ops.attention_nshd(qs, ks, vs, bias, km, s, want_lse=True)
         return (os_, lse, ops.attention_bwd_nshd(qs, ks, vs, bias, km, os_, dos, lse, s),
                 ops.attention_gated(q, k, v, bias, km, x, wg, bg, s),
-                ops.attention_gate(o, x, wg, bg), ops.ln_pair_bias(z, sc, of, w))
+                ops.attention_gate(o, x, wg, bg), ops.attention_gate_bwd(o, x, wg, bg, dgate),
+                ops.ln_pair_bias(z, sc, of, w))
 
     _check_replays(step)
 
