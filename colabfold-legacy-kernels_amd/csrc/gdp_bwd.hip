@@ -17,6 +17,9 @@ namespace clk {
 namespace {
 
 constexpr int kBwdRows = 64;  // rows per tile
+// Most rows of one backward call: row and tile indices are 32-bit, and so is the tiles' row
+// count rounded up to whole tiles.
+constexpr int64_t kMaxBwdM = ((int64_t)1 << 31) - kBwdRows;
 
 // Rows of a [rows, W] 2-byte tile in LDS, 16-byte pieces XOR-swizzled by row % 8 (W >= 128): the
 // operand reads of 16 rows and the transposed reads of 4 rows x 32 bytes hit distinct banks.
@@ -287,7 +290,7 @@ __global__ __launch_bounds__(2 * N) void gate_bwd_grad_kernel(
     // Element offset of (row m, column col0) in o's [N, H, Sq, D] layout.
     auto o_at = [&](int m) {
         const int n = m / Sq, sq = m - n * Sq;
-        return ((size_t)(n * H + hd) * Sq + sq) * D + d0;
+        return (((size_t)n * H + hd) * Sq + sq) * D + d0;
     };
     auto stage = [&](int t, char* xb) {
         const int rows = rows_of(t);
@@ -320,14 +323,35 @@ __global__ __launch_bounds__(2 * N) void gate_bwd_grad_kernel(
     float cs[8];  // column sums of dgl over this block's rows
 #pragma unroll
     for (int j = 0; j < 8; ++j) cs[j] = 0.f;
-    // do through one resource over the whole tensor (M * N * 2 < 2^30 bytes): rows past M get an
-    // offset past its end and are dropped, so every tile issues the same 2 * SUB stores (two per
-    // sub-tile, as soon as it is computed), the count the waits below assume.
-    const Rsrc rdo = buffer_rsrc(dov, (uint32_t)M * N * 2);
-    auto store_sub = [&](Rsrc rd, int t, int rows, int sub, u32x4 vg, u32x4 vo) {
+    // do of tile t through a resource based at its first row's sample n0 (element n0*H*Sq*D of
+    // do), covering at most 2^30 - 16 bytes from there: the tile's rows lie in samples n0 and
+    // n0 + 1 (Sq >= 64) or within 3 * 64 rows of n0's first (Sq < 64), so with Sq*H*D*4 < 2^30
+    // bytes every offset fits. Rows past M get an offset past its end and are dropped, so every
+    // tile issues the same 2 * SUB stores (two per sub-tile, as soon as it is computed), the
+    // count the waits below assume.
+    struct DoTile {
+        Rsrc r;
+        int n0;  // the sample the resource starts at
+    };
+    auto do_tile = [&](int t) {
+        const int rows = rows_of(t);
+        if (rows == 0) return DoTile{buffer_rsrc(dov, 0), 0};
+        const int n0 = (t * R) / Sq;
+        const size_t base = (size_t)n0 * H * Sq * D;
+        const size_t left = ((size_t)M * N - base) * 2;
+        const size_t cap = (size_t)kPastEnd - 16;
+        return DoTile{buffer_rsrc(dov + base, (uint32_t)(left < cap ? left : cap)), n0};
+    };
+    // Byte offset of (row m, column col0) from sample n0's first element (32-bit: bounded above).
+    auto do_at = [&](int m, int n0) {
+        const int n = m / Sq, sq = m - n * Sq;
+        return ((((n - n0) * H + hd) * Sq + sq) * D + d0) * 2;
+    };
+    auto store_sub = [&](Rsrc rd, const DoTile& dt, int t, int rows, int sub, u32x4 vg,
+                         u32x4 vo) {
         const int xrow = 16 * sub + r16;
         buf_st16(rd, (xrow * N + col0) * 2, 0, vg);
-        buf_st16(rdo, xrow < rows ? (int)o_at(t * R + xrow) * 2 : kPastEnd, 0, vo);
+        buf_st16(dt.r, xrow < rows ? do_at(t * R + xrow, dt.n0) : kPastEnd, 0, vo);
     };
 
     const int G = gridDim.x;
@@ -345,6 +369,7 @@ __global__ __launch_bounds__(2 * N) void gate_bwd_grad_kernel(
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         const int rows = rows_of(t);
         const Rsrc rd = out_rsrc(t);
+        const DoTile dt = do_tile(t);
 #pragma unroll
         for (int sub = 0; sub < SUB; ++sub) {
             const int xrow = 16 * sub + r16;
@@ -367,7 +392,7 @@ __global__ __launch_bounds__(2 * N) void gate_bwd_grad_kernel(
                 dg[j] = dov8[j] * ov[j] * (1.f - sg);
                 cs[j] += live * dg[j];
             }
-            store_sub(rd, t, rows, sub, pack8<TR>(dg), pack8<TR>(dov8));
+            store_sub(rd, dt, t, rows, sub, pack8<TR>(dg), pack8<TR>(dov8));
         }
     };
 
@@ -378,12 +403,13 @@ __global__ __launch_bounds__(2 * N) void gate_bwd_grad_kernel(
     // Stores of no rows (all dropped): the per-tile count of memory operations the waits assume.
     const u32x4 zero = {0u, 0u, 0u, 0u};
     const Rsrc none = out_rsrc(ntiles);
+    const DoTile no_do = do_tile(ntiles);
 #pragma unroll
-    for (int sub = 0; sub < SUB; ++sub) store_sub(none, ntiles, 0, sub, zero, zero);
+    for (int sub = 0; sub < SUB; ++sub) store_sub(none, no_do, ntiles, 0, sub, zero, zero);
     stage(t + G, x1);
     __atomic_signal_fence(__ATOMIC_SEQ_CST);
 #pragma unroll
-    for (int sub = 0; sub < SUB; ++sub) store_sub(none, ntiles, 0, sub, zero, zero);
+    for (int sub = 0; sub < SUB; ++sub) store_sub(none, no_do, ntiles, 0, sub, zero, zero);
     // Without PREF every tile uses the one register set (da, oa).
     u32x4 (&dB)[SUB] = PREF ? db : da;
     u32x4 (&oB)[SUB] = PREF ? ob : oa;
@@ -915,8 +941,9 @@ extern "C" clk_status clk_gated_dual_proj_bwd(hipStream_t stream, clk_dtype dtyp
     if (M < 0 || (K != 64 && K != 128) || (N != 64 && N != 128))
         return fail(CLK_INVALID_ARGUMENT, "%s: K and N must be 64 or 128 (K=%lld, N=%lld)", who,
                     (long long)K, (long long)N);
-    if (M * 2 * N * 2 >= ((int64_t)1 << 31) || M * K * 2 >= ((int64_t)1 << 31))
-        return fail(CLK_INVALID_ARGUMENT, "%s: M=%lld too large", who, (long long)M);
+    if (M > kMaxBwdM)
+        return fail(CLK_INVALID_ARGUMENT, "%s: M=%lld too large (at most 2^31 - 64 rows)", who,
+                    (long long)M);
     if (M == 0) {
         if (!dwp || !dbp || !dwg || !dbg)
             return fail(CLK_INVALID_ARGUMENT, "%s: null gradient pointer", who);
@@ -967,9 +994,12 @@ extern "C" clk_status clk_attention_gate_bwd(hipStream_t stream, clk_dtype dtype
         return fail(CLK_INVALID_ARGUMENT, "%s: C and H*D must each be 64, 128 or 256 (C=%lld, "
                     "H*D=%lld)", who, (long long)C, (long long)HD);
     const int64_t M = N * Sq;
-    if (M * (C > HD ? C : HD) * 2 >= ((int64_t)1 << 30))
-        return fail(CLK_INVALID_ARGUMENT, "%s: N*Sq=%lld rows too many (each operand must stay "
-                    "under 1 GiB)", who, (long long)M);
+    if (M > kMaxBwdM)
+        return fail(CLK_INVALID_ARGUMENT, "%s: N*Sq=%lld rows too many (at most 2^31 - 64)", who,
+                    (long long)M);
+    if (Sq * HD * 4 >= ((int64_t)1 << 30))
+        return fail(CLK_INVALID_ARGUMENT, "%s: Sq=%lld too long (Sq*H*D*4 must stay under 2^30)",
+                    who, (long long)Sq);
     if (!dwg || !dbg) return fail(CLK_INVALID_ARGUMENT, "%s: null gradient pointer", who);
     if (M == 0) return zero_gate_bwd(stream, dwg, dbg, (int)C, (int)HD);
     if (!o || !x || !wg || !bg || !dout || !d_o || !dx || !workspace)

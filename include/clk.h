@@ -217,9 +217,10 @@ clk_status clk_gated_dual_proj(hipStream_t stream, clk_dtype dtype, const void* 
  * (x.wp + bp) * sigmoid(x.wg + bg) and the incoming gradient dout [M,N], writes dx [M,K] (added
  * to the existing dx when accumulate_dx != 0, for two branches reading the same x), dwp, dwg
  * [K,N] and dbp, dbg [N] in float32. x, weights, biases, mask, dout, dx of dtype CLK_F16 or
- * CLK_BF16. K and N in {64, 128}. Deterministic: the weight and bias gradients are summed from
- * per-block partials in a fixed order. Workspace: clk_gated_dual_proj_bwd_workspace_size bytes.
- * M = 0 writes zero weight and bias gradients (sums over no rows).
+ * CLK_BF16. K and N in {64, 128}; M at most 2^31 - 64. Deterministic: the weight and bias
+ * gradients are summed from per-block partials in a fixed order. Workspace:
+ * clk_gated_dual_proj_bwd_workspace_size bytes. M = 0 writes zero weight and bias gradients
+ * (sums over no rows).
  */
 size_t clk_gated_dual_proj_bwd_workspace_size(int64_t M, int64_t K, int64_t N);
 clk_status clk_gated_dual_proj_bwd(hipStream_t stream, clk_dtype dtype, const void* x,
@@ -274,8 +275,9 @@ clk_status clk_attention_gate(hipStream_t stream, clk_dtype dtype, const void* o
  *   accumulate_dx != 0: x also feeds the q, k, v projections),
  *   dwg = x^T.dg [C,H*D] and dbg = sum of dg over the N*Sq rows [H*D], both float32.
  * o, x, wg, bg, dout, d_o, dx of dtype CLK_F16 or CLK_BF16 (o, x, wg, dout, d_o, dx and the
- * workspace 16-byte aligned); C and H*D each 64, 128 or 256; D a multiple of 8; each operand
- * under 1 GiB. Deterministic: dwg and dbg are summed from per-block partials in a fixed order.
+ * workspace 16-byte aligned); C and H*D each 64, 128 or 256; D a multiple of 8; N*Sq at most
+ * 2^31 - 64 rows and Sq*H*D*4 under 2^30 bytes. Deterministic: dwg and dbg are summed from
+ * per-block partials in a fixed order.
  * Workspace: clk_attention_gate_bwd_workspace_size bytes (dg in the input dtype and the
  * partials). N*Sq = 0 writes zero dwg and dbg.
  */

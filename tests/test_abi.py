@@ -221,7 +221,8 @@ def gate_bwd(**kw):
 @pytest.mark.parametrize("kw,msg", [
     (dict(dtype=F32), "dtype"), (dict(D=12, H=4), "multiple of 8"), (dict(H=0), "H > 0"),
     (dict(C=96), "64, 128 or 256"), (dict(H=3), "64, 128 or 256"),
-    (dict(N=1 << 20, Sq=8), "too many"), (dict(dwg=None), "null gradient"),
+    (dict(N=1 << 28, Sq=16), "too many"), (dict(Sq=1 << 21), "too long"),
+    (dict(dwg=None), "null gradient"),
     (dict(o=None), "null operand"), (dict(workspace=None), "null operand"),
     (dict(d_o=FAKE + 8), "aligned"), (dict(wg=FAKE + 8), "aligned"),
     (dict(workspace_bytes=4096), "workspace"),
@@ -264,7 +265,8 @@ def test_attention_gated_empty_is_ok():
 
 
 @pytest.mark.parametrize("m,k,n,msg", [(4, 96, 128, "64 or 128"), (4, 128, 32, "64 or 128"),
-                                       (-1, 128, 128, "64 or 128")])
+                                       (-1, 128, 128, "64 or 128"),
+                                       (1 << 31, 128, 128, "too large")])
 def test_gdp_bwd_validation(m, k, n, msg):
     lib = _native.lib()
     assert lib.clk_gated_dual_proj_bwd(None, BF16, *([FAKE] * 13), 1 << 30, m, k, n, 0) == INVALID

@@ -113,6 +113,37 @@ def test_gate_bwd_msa_workload(cuda):
     check(a, *t, TOL["bf16"]["grad"])
 
 
+def test_gate_bwd_beyond_one_gib(cuda):
+    """N = 8200 MSA rows of 256 queries, 8 x 32 heads on 256 channels: each operand 1.07 GB, past
+    2^30 bytes. Sampled samples' do and dx at the start, around the 2^30-byte point and at the
+    end against the oracle, and dwg, dbg against the oracle summed over sample chunks."""
+    n, h, sq, d, c = 8200, 8, 256, 32, 256
+    dt = torch.bfloat16
+    g = torch.Generator(device=cuda).manual_seed(51)
+    o = torch.randn((n, h, sq, d), generator=g, device=cuda).to(dt)
+    x = torch.randn((n, sq, c), generator=g, device=cuda).to(dt)
+    wg = (torch.randn((c, h * d), generator=g, device=cuda) / c ** 0.5).to(dt)
+    bg = (0.5 * torch.randn((h * d,), generator=g, device=cuda)).to(dt)
+    dout = torch.randn((n, sq, h * d), generator=g, device=cuda).to(dt)
+    do, dx, dwg, dbg = ops.attention_gate_bwd(o, x, wg, bg, dout)
+    wn, bn = np64(wg), np64(bg)
+    tol = TOL["bf16"]["grad"]
+    mid = (1 << 30) // (sq * h * d * 2)  # the first sample past 2^30 bytes
+    for a in (0, mid - 2, n - 3):
+        r = ref.attention_gate_bwd(np64(o[a:a + 3]), np64(x[a:a + 3]), wn, bn,
+                                   np64(dout[a:a + 3]))
+        assert_close("do[%d:]" % a, do[a:a + 3], r[0], tol)
+        assert_close("dx[%d:]" % a, dx[a:a + 3], r[1], tol)
+    sums = None
+    step = 512
+    for a in range(0, n, step):
+        r = ref.attention_gate_bwd(np64(o[a:a + step]), np64(x[a:a + step]), wn, bn,
+                                   np64(dout[a:a + step]))[2:]
+        sums = list(r) if sums is None else [u + v for u, v in zip(sums, r)]
+    assert_close("dwg", dwg, sums[0], tol)
+    assert_close("dbg", dbg, sums[1], tol)
+
+
 @pytest.mark.parametrize("fused", [False, True], ids=["separate", "fused"])
 @pytest.mark.parametrize("n,h,sq,sk,d,c,tail", [(2, 8, 70, 70, 32, 256, 0.1),
                                                 (3, 4, 64, 64, 32, 128, 0.0),

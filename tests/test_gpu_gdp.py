@@ -293,3 +293,33 @@ def test_ln_gdp_bwd_full_pair_rep(cuda):
         assert_close(name, a, b, tol)
     for name, a, b in zip(("dwpb", "dbpb", "dwgb", "dbgb"), gb, acc_b):
         assert_close(name, a, b, tol)
+
+
+def test_gdp_bwd_beyond_two_gib(cuda):
+    """M = 2048*2048 + 37 rows at K = N = 128: the projection gradient dpg (2.1 GB) and x, dout,
+    dx (1.07 GB each) exceed 2^31 bytes. Sampled rows of dx at the start, across the 2^31-byte
+    point of dpg and at the end against the oracle, and every weight and bias gradient against
+    the oracle summed over row chunks."""
+    m, k, n = 2048 * 2048 + 37, 128, 128
+    dt = torch.bfloat16
+    g = torch.Generator(device=cuda).manual_seed(41)
+    x = torch.randn((m, k), generator=g, device=cuda).to(dt)
+    dout = torch.randn((m, n), generator=g, device=cuda).to(dt)
+    mask = (torch.rand((m,), generator=g, device=cuda) > 0.05).to(dt)
+    w = [t.to(cuda) for t in gdp_weights(k, n, dt, seed=42, bias_std=0.3)]
+    dx, dwp, dbp, dwg, dbg = ops.gated_dual_proj_bwd(x, *w, mask, dout)
+    wn = [np64(t) for t in w]
+    tol = TOL["bf16"]["grad"]
+    half = (1 << 31) // (2 * n * 2)  # first row of dpg past 2^31 bytes
+    for a in (0, half - 300, m - 300):
+        r = ref.gated_dual_proj_bwd(np64(x[a:a + 300]), *wn, np64(mask[a:a + 300]),
+                                    np64(dout[a:a + 300]))
+        assert_close("dx[%d:]" % a, dx[a:a + 300], r[0], tol)
+    sums = None
+    step = 1 << 18
+    for a in range(0, m, step):
+        r = ref.gated_dual_proj_bwd(np64(x[a:a + step]), *wn, np64(mask[a:a + step]),
+                                    np64(dout[a:a + step]))[1:]
+        sums = list(r) if sums is None else [u + v for u, v in zip(sums, r)]
+    for name, got, want in zip(("dwp", "dbp", "dwg", "dbg"), (dwp, dbp, dwg, dbg), sums):
+        assert_close(name, got, want, tol)
