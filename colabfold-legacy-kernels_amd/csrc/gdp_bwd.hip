@@ -54,14 +54,20 @@ __device__ __forceinline__ void stage_swz(Rsrc rsrc, char* lds, int wave, int la
 // x arrives by buffer->LDS loads two tiles ahead and dout, mask of the next tile are loaded into
 // registers. A lane's accumulators hold 8 consecutive columns of one row, the layout of its
 // 16-byte dout vector and of its two 16-byte stores into dpg.
+// FDX (K == N): dx of the tile as well, so that dpg is not read back for it. The tile's
+// [dp | dg] rows go into LDS in the dx kernel's swizzled layout, and after a second barrier wave
+// w computes dx columns 32w..32w+31 = [dp | dg] . wcat^T's rows, held as A operands in registers
+// as in the dx kernel (with one wave per SIMD the registers allow it); dx is stored (or added to,
+// with accumulate) through a resource per tile.
 // ---------------------------------------------------------------------------------------------
-template <typename TR, int K, int N>
+template <typename TR, int K, int N, bool FDX = false>
 __global__ __launch_bounds__(2 * N) void gdp_bwd_grad_kernel(
     const typename TR::elem* __restrict__ x, const typename TR::elem* __restrict__ wp,
     const typename TR::elem* __restrict__ bp, const typename TR::elem* __restrict__ wg,
     const typename TR::elem* __restrict__ bg, const typename TR::elem* __restrict__ mask,
     const typename TR::elem* __restrict__ dout, typename TR::elem* __restrict__ dpg,
-    float* __restrict__ dbpart, int M) {
+    float* __restrict__ dbpart, int M, typename TR::elem* __restrict__ dx = nullptr,
+    int accumulate = 0) {
     using E = typename TR::elem;
     using V8 = typename TR::vec8;
     using S = SwzRows<K < 128 ? 128 : K>;  // K = 64 rows use a 128-wide tile (upper half zero)
@@ -70,13 +76,32 @@ __global__ __launch_bounds__(2 * N) void gdp_bwd_grad_kernel(
     constexpr int XB = R * KT * 2;
     constexpr int DPW = R * S::PL / NT;
 
+    static_assert(!FDX || K == N, "the fused dx takes one wave per 32 dx columns: K == N");
+    constexpr int W2 = 2 * N, KS2 = W2 / 32;
+    using S2 = SwzRows<W2>;
+
     __shared__ __attribute__((aligned(16))) char x0[XB];
     __shared__ __attribute__((aligned(16))) char x1[XB];
     __shared__ __attribute__((aligned(16))) char x2[XB];
+    __shared__ __attribute__((aligned(16))) char tg[FDX ? R * W2 * 2 : 16];  // [dp | dg] tile
 
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int r16 = lane & 15, g = lane >> 4;
+
+    // FDX: wcat^T's rows k = 32w + 8(r16/4) + 4h + r16%4 (8 consecutive n' per 16-byte load).
+    V8 wd[FDX ? 2 : 1][FDX ? KS2 : 1];
+    if constexpr (FDX) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const int k = 32 * wave + 8 * (r16 >> 2) + 4 * h + (r16 & 3);
+#pragma unroll
+            for (int ks = 0; ks < KS2; ++ks) {
+                const int n = 32 * ks + 8 * g;
+                wd[h][ks] = bits_as<V8>(ld16(n < N ? wp + k * N + n : wg + k * N + (n - N)));
+            }
+        }
+    }
 
     V8 wa[2][2][KS];
     f32x4 binit[2][2];
@@ -194,6 +219,40 @@ __global__ __launch_bounds__(2 * N) void gdp_bwd_grad_kernel(
         }
         __atomic_signal_fence(__ATOMIC_SEQ_CST);
         store(out_rsrc(t));
+        if constexpr (FDX) {
+            // tg is free: every wave finished reading the previous tile's before this tile's
+            // first barrier.
+#pragma unroll
+            for (int sub = 0; sub < SUB; ++sub)
+#pragma unroll
+                for (int q = 0; q < 2; ++q)
+                    *reinterpret_cast<u32x4*>(
+                        tg + S2::piece_at(16 * sub + r16, (q * N + col0) / 8) * 16) = res[q][sub];
+            lds_barrier();
+            const Rsrc rdx = buffer_rsrc(rows > 0 ? dx + (size_t)t * R * K : dx,
+                                         (uint32_t)rows * K * 2);
+#pragma unroll
+            for (int sub = 0; sub < SUB; ++sub) {
+                const int xrow = 16 * sub + r16;
+                f32x4 acc[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+                for (int ks = 0; ks < KS2; ++ks) {
+                    const V8 v = *reinterpret_cast<const V8*>(tg + S2::piece_at(xrow, 4 * ks + g) * 16);
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) acc[h] = TR::mfma(wd[h][ks], v, acc[h]);
+                }
+                float o[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) o[j] = acc[j >> 2][j & 3];
+                if (accumulate && xrow < rows) {
+                    float prev[8];
+                    unpack8<TR>(ld16(dx + ((size_t)t * R + xrow) * K + col0), prev);
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) o[j] += prev[j];
+                }
+                buf_st16(rdx, (xrow * K + col0) * 2, 0, pack8<TR>(o));
+            }
+        }
     };
 
     int t = blockIdx.x;
@@ -756,13 +815,19 @@ clk_status run_gdp_bwd(hipStream_t st, const void* x, const void* wp, const void
     E* dpg = reinterpret_cast<E*>(ws + gm.dpg_off);
     float* part = reinterpret_cast<float*>(ws + gm.part_off);
     float* dbpart = reinterpret_cast<float*>(ws + gm.dbpart_off);
-    {
+    if constexpr (K == N) {
+        // dx computed by the grad kernel from the tile it already holds.
         KernelTimer timer("gdp_bwd_grad", st);
-        gdp_bwd_grad_kernel<TR, K, N><<<gm.grad_blocks, 2 * N, 0, st>>>(
+        gdp_bwd_grad_kernel<TR, K, N, true><<<gm.grad_blocks, 2 * N, 0, st>>>(
             (const E*)x, (const E*)wp, (const E*)bp, (const E*)wg, (const E*)bg, (const E*)mask,
-            (const E*)dout, dpg, dbpart, M);
-    }
-    {
+            (const E*)dout, dpg, dbpart, M, (E*)dx, accumulate);
+    } else {
+        {
+            KernelTimer timer("gdp_bwd_grad", st);
+            gdp_bwd_grad_kernel<TR, K, N><<<gm.grad_blocks, 2 * N, 0, st>>>(
+                (const E*)x, (const E*)wp, (const E*)bp, (const E*)wg, (const E*)bg,
+                (const E*)mask, (const E*)dout, dpg, dbpart, M);
+        }
         const int ntiles = (M + kBwdRows - 1) / kBwdRows;
         const int per_cu = 128 / K;
         const int grid = ntiles < 256 * per_cu ? ntiles : 256 * per_cu;
