@@ -3,14 +3,18 @@
 //   out = mask * p * s,  p = x.wp + bp,  s = sigmoid(x.wg + bg)
 //   dp = dout * mask * s,  dg = dout * mask * p * s * (1 - s)
 //   dx = dp.wp^T + dg.wg^T,  dwp = x^T.dp,  dwg = x^T.dg,  dbp = sum_m dp,  dbg = sum_m dg
-// Four kernels, deterministic (no float atomics):
+// Four kernels (three at K = N), deterministic (no float atomics):
 //   gdp_bwd_grad  recomputes p and the gate on MFMA (weights resident as in the forward) and
 //                 writes dpg = [dp | dg] (M x 2N, input dtype) and per-block column sums of dp, dg;
+//                 at K = N it also computes dx from the tile it holds;
 //   gdp_bwd_dx    dx = dpg . [wp | wg]^T, the transposed weights resident as MFMA A operands;
 //   gdp_bwd_dw    per-block partials of x^T . dpg over a contiguous range of rows, both operands
 //                 read transposed from LDS (ds_read_b64_tr_b16);
 //   gdp_bwd_sum   adds the partials in block order into dwp, dwg, dbp, dbg (float32).
 // Layout: x [M,K], wp, wg [K,N], bp, bg [N], mask [M], dout, [M,N], dx [M,K]; K, N in {64, 128}.
+// The attention output gate's backward (further below) is the same computation with o in the
+// role of p and one weight matrix: its own grad kernel, then gdp_bwd_dx, _dw and _sum with
+// NMAT = 1.
 #include "common.hpp"
 
 namespace clk {
